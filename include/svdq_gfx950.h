@@ -1,0 +1,108 @@
+/* C-ABI of the MI355X (gfx950) SVDQuantLinear backend.
+ *
+ * Plain pointers, sizes and a hipStream_t; no torch types.  Every buffer is device memory on
+ * the current HIP device, 16-byte aligned, row-major.  Every entry point enqueues work on
+ * `stream` and returns immediately (no host synchronisation); it returns SVDQ_OK (0) or a
+ * negative svdq_status, and svdq_last_error() then describes the failure (per host thread).
+ *
+ * Storage dtypes follow the reference checkpoint layout (reference runtime/load.py:90-126,
+ * scripts/convert_simulated.py:201-208):
+ *   bf16  : smooth_scale [K], l1 [N, r], l2 [r, K], bias [N], activations
+ *   fp16  : weight_scales [N, K/G]
+ *   uint8 : qweight_packed [N, K/2], byte j = (q[2j] + 8) | (q[2j+1] + 8) << 4
+ *
+ * A layer forward (reference runtime/linear.py:156-161 -> SVDQuantLinear.forward) is
+ *   svdq_act_quant  (smoothing, A4 quantization + packing, low-rank and LoRA down)
+ *   svdq_w4a4_gemm  (W4A4 GEMM + low-rank up + LoRA up + bias)
+ * or, for the W4A16 variant,
+ *   svdq_act_quant with SVDQ_ACT_XHAT only, then svdq_w4a16_gemm.
+ */
+#ifndef SVDQ_GFX950_H
+#define SVDQ_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum svdq_status {
+  SVDQ_OK = 0,
+  SVDQ_ERR_ARG = -1,         /* null pointer, non-positive size, bad flag            */
+  SVDQ_ERR_SHAPE = -2,       /* K % group, rank limits, leading dimensions            */
+  SVDQ_ERR_ALIGN = -3,       /* pointer or leading dimension not 16-byte aligned      */
+  SVDQ_ERR_UNSUPPORTED = -4, /* group size or rank combination without a kernel       */
+  SVDQ_ERR_LAUNCH = -5       /* the HIP runtime rejected the launch                   */
+} svdq_status;
+
+/* flags of svdq_act_quant */
+#define SVDQ_ACT_QUANT 1u      /* write packed A4 codes qx and bf16 scales sx          */
+#define SVDQ_ACT_XHAT 2u       /* write the smoothed bf16 activation x_hat              */
+#define SVDQ_ACT_EXACT_DIV 4u  /* IEEE division for x / s everywhere (slow reference)   */
+
+/* Library version string. */
+const char* svdq_version(void);
+
+/* Message for the most recent failing call on this host thread ("" if none). */
+const char* svdq_last_error(void);
+
+/* Group sizes with kernels in this build; returns 1 if `group` is supported. */
+int svdq_group_supported(int group);
+
+/* Per-layer constant of the activation pass: srs[0:K] = float(smooth), srs[K:2K] =
+ * RN(1 / float(smooth)).  Replaces the per-call `x / smooth` set-up of reference
+ * quant/svd.py:121-122 and kernels/triton/generic_int4.py:167-171.
+ *   smooth : bf16 [K]      srs : f32 [2K] (output) */
+int svdq_prepare_smooth(const void* smooth, float* srs, int K, hipStream_t stream);
+
+/* Workspace of svdq_act_quant for (M, K, group, RTp): number of K splits, floats of the
+ * split-partial buffer `midp` and ints of the `counters` buffer.  `counters` must be zero
+ * before the first call; every completed call leaves it zero again.  Calls sharing one
+ * `counters`/`midp` pair must not run concurrently. */
+int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int64_t* midp_floats,
+                             int64_t* counter_ints);
+
+/* Fused activation pass.  Replaces reference quant/svd.py:121-122 (x_hat = x / smooth),
+ * quant/pack.py:6-23 + 47-56 applied per group to x_hat (the A4 step of README.md:188-195),
+ * quant/svd.py:159 / kernels/triton/generic_int4.py:238-241 (mid = x_hat @ l2^T) and
+ * runtime/linear.py:42-45 (LoRA down x @ A^T on the raw x, times the multiplier).
+ *   x        : bf16 [M, ldx]          srs : f32 [2K] from svdq_prepare_smooth
+ *   l2       : bf16 [r, K]            lora_down : bf16 [rl, K] or NULL (rl = 0)
+ *   lora_mult: f32 [rl]: per-column multiplier scale * alpha / rank of the owning adapter
+ *   qx       : u8 [M, K/2]   (SVDQ_ACT_QUANT)      sx : bf16 [M, K/group]
+ *   xhat     : bf16 [M, ldxh] (SVDQ_ACT_XHAT)
+ *   mid      : f32 [M, RTp]: columns [0, r) = x_hat @ l2^T, [r, r+rl) = mult * (x @ A^T),
+ *              [r+rl, RTp) = 0.   RTp % 32 == 0, RTp >= r + rl, ceil(r/32)+ceil(rl/32) <= 4.
+ *   midp, counters : workspace sized by svdq_act_quant_workspace. */
+int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
+                   const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
+                   int RTp, unsigned flags, void* qx, void* sx, void* xhat, int64_t ldxh, float* mid,
+                   float* midp, int* counters, int splits, hipStream_t stream);
+
+/* W4A4 GEMM with fused epilogue.  Replaces the residual product of reference
+ * quant/svd.py:158 / kernels/triton/generic_int4.py:18-82 (with INT4 activations), the
+ * low-rank add + bias of generic_int4.py:84-133 / svd.py:159-163 and the LoRA add of
+ * runtime/linear.py:158-160:
+ *   y = sum_g sx sw (qx . qw)_g + mid @ l1cat^T + bias
+ *   qx : u8 [M, K/2]   sx : bf16 [M, K/group]   qw : u8 [N, K/2]   sw : fp16 [N, K/group]
+ *   mid: f32 [M, RTp]  l1cat : bf16 [N, RTp] = [l1 | up_1 | up_2 ... | 0]
+ *   bias: bf16 [N] or NULL     y : [M, ldy], bf16 (out_f32 = 0) or f32 (out_f32 = 1) */
+int svdq_w4a4_gemm(const void* qx, const void* sx, const void* qw, const void* sw, const float* mid,
+                   const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                   void* y, int64_t ldy, int out_f32, hipStream_t stream);
+
+/* W4A16 GEMM with fused epilogue: the reference pytorch_sim math (quant/svd.py:119-163;
+ * dequantization pack.py:26-44 in bf16) and kernels/triton/generic_int4.py:18-133.
+ *   xhat : bf16 [M, ldxh] (from svdq_act_quant with SVDQ_ACT_XHAT); other arguments as in
+ *   svdq_w4a4_gemm. */
+int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const float* mid,
+                    const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                    void* y, int64_t ldy, int out_f32, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SVDQ_GFX950_H */

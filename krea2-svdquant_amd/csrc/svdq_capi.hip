@@ -1,0 +1,181 @@
+// extern "C" entry points of libsvdq_gfx950.so: argument validation and kernel launch.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string>
+
+#include "../../include/svdq_gfx950.h"
+#include "svdq_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return SVDQ_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(SVDQ_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+int check_group(int group, int K) {
+  if (!svdq_group_supported(group)) return fail(SVDQ_ERR_UNSUPPORTED, "group size %d has no kernel (64 or 128)", group);
+  if (K <= 0 || K % group != 0) return fail(SVDQ_ERR_SHAPE, "K=%d must be a positive multiple of group=%d", K, group);
+  return SVDQ_OK;
+}
+
+int mid_tiles(int r, int rl) { return (r + 31) / 32 + (rl + 31) / 32; }
+
+}  // namespace
+
+extern "C" {
+
+const char* svdq_version(void) { return "svdq_gfx950 0.1.0"; }
+
+const char* svdq_last_error(void) { return g_last_error.c_str(); }
+
+int svdq_group_supported(int group) { return group == 64 || group == 128; }
+
+int svdq_prepare_smooth(const void* smooth, float* srs, int K, hipStream_t stream) {
+  if (!smooth || !srs) return fail(SVDQ_ERR_ARG, "prepare_smooth: null pointer");
+  if (K <= 0) return fail(SVDQ_ERR_ARG, "prepare_smooth: K=%d", K);
+  return launched(svdq::launch_prepare_smooth(static_cast<const uint16_t*>(smooth), srs, K, stream),
+                  "prepare_smooth");
+}
+
+int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int64_t* midp_floats,
+                             int64_t* counter_ints) {
+  if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant_workspace: M=%d", M);
+  if (int e = check_group(group, K)) return e;
+  if (RTp <= 0 || RTp % 32) return fail(SVDQ_ERR_SHAPE, "RTp=%d must be a positive multiple of 32", RTp);
+  const int s = svdq::act_splits(M, K, group);
+  if (splits) *splits = s;
+  if (midp_floats) *midp_floats = s > 1 ? (int64_t)s * M * RTp : 0;
+  if (counter_ints) *counter_ints = (M + 63) / 64;
+  return ok();
+}
+
+int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
+                   const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
+                   int RTp, unsigned flags, void* qx, void* sx, void* xhat, int64_t ldxh, float* mid,
+                   float* midp, int* counters, int splits, hipStream_t stream) {
+  const bool quant = flags & SVDQ_ACT_QUANT, want_xhat = flags & SVDQ_ACT_XHAT;
+  if (flags & ~(unsigned)(SVDQ_ACT_QUANT | SVDQ_ACT_XHAT | SVDQ_ACT_EXACT_DIV))
+    return fail(SVDQ_ERR_ARG, "act_quant: unknown flags 0x%x", flags);
+  if (!quant && !want_xhat) return fail(SVDQ_ERR_ARG, "act_quant: neither QUANT nor XHAT requested");
+  if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant: M=%d", M);
+  if (int e = check_group(group, K)) return e;
+  if (r < 1 || rl < 0) return fail(SVDQ_ERR_SHAPE, "act_quant: rank r=%d rl=%d", r, rl);
+  if (RTp % 32 || RTp < r + rl) return fail(SVDQ_ERR_SHAPE, "act_quant: RTp=%d (r=%d rl=%d)", RTp, r, rl);
+  const int nt = mid_tiles(r, rl);
+  if (nt > 4) return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: ceil(r/32)+ceil(rl/32)=%d > 4", nt);
+  if (!x || !srs || !l2 || !mid || (rl > 0 && (!lora_down || !lora_mult)) || (quant && (!qx || !sx)) ||
+      (want_xhat && !xhat))
+    return fail(SVDQ_ERR_ARG, "act_quant: null pointer");
+  if (ldx < K || ldx % 8 || (want_xhat && (ldxh < K || ldxh % 8)))
+    return fail(SVDQ_ERR_ALIGN, "act_quant: ldx=%lld ldxh=%lld must be >= K and multiples of 8",
+                (long long)ldx, (long long)ldxh);
+  if (!aligned16(x) || !aligned16(srs) || !aligned16(l2) || !aligned16(mid) ||
+      (rl > 0 && !aligned16(lora_down)) || (quant && !aligned16(qx)) || (want_xhat && !aligned16(xhat)))
+    return fail(SVDQ_ERR_ALIGN, "act_quant: device pointers must be 16-byte aligned");
+  const int expect = svdq::act_splits(M, K, group);
+  if (splits != expect) return fail(SVDQ_ERR_ARG, "act_quant: splits=%d, workspace says %d", splits, expect);
+  if (splits > 1 && (!midp || !counters)) return fail(SVDQ_ERR_ARG, "act_quant: split workspace missing");
+
+  svdq::ActParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.ldx = ldx;
+  p.srs = srs;
+  p.l2 = static_cast<const uint16_t*>(l2);
+  p.lora = static_cast<const uint16_t*>(lora_down);
+  p.lora_mult = lora_mult;
+  p.r = r;
+  p.rl = rl;
+  p.M = M;
+  p.K = K;
+  p.RTp = RTp;
+  p.qx = static_cast<uint8_t*>(qx);
+  p.sx = static_cast<uint16_t*>(sx);
+  p.xhat = static_cast<uint16_t*>(xhat);
+  p.ldxh = ldxh;
+  p.mid = mid;
+  p.midp = midp;
+  p.counters = counters;
+  const int ngroups = K / group;
+  p.gps = (ngroups + splits - 1) / splits;
+  p.exact = (flags & SVDQ_ACT_EXACT_DIV) ? 1 : 0;
+  return launched(svdq::launch_act(p, group, nt, quant, want_xhat, splits, stream), "act_quant");
+}
+
+static int gemm_common_checks(const char* who, const void* qw, const void* sw, const float* mid,
+                              const void* l1cat, int RTp, int M, int N, int K, int group, void* y,
+                              int64_t ldy, int out_f32) {
+  if (M <= 0 || N <= 0) return fail(SVDQ_ERR_ARG, "%s: M=%d N=%d", who, M, N);
+  if (int e = check_group(group, K)) return e;
+  if (!qw || !sw || !mid || !l1cat || !y) return fail(SVDQ_ERR_ARG, "%s: null pointer", who);
+  if (RTp <= 0 || RTp % 32) return fail(SVDQ_ERR_SHAPE, "%s: RTp=%d must be a positive multiple of 32", who, RTp);
+  if (out_f32 != 0 && out_f32 != 1) return fail(SVDQ_ERR_ARG, "%s: out_f32=%d", who, out_f32);
+  if (ldy < N) return fail(SVDQ_ERR_SHAPE, "%s: ldy=%lld < N=%d", who, (long long)ldy, N);
+  if (!aligned16(qw) || !aligned16(mid) || !aligned16(l1cat))
+    return fail(SVDQ_ERR_ALIGN, "%s: device pointers must be 16-byte aligned", who);
+  return SVDQ_OK;
+}
+
+static svdq::GemmParams gemm_params(const void* qw, const void* sw, const float* mid, const void* l1cat,
+                                    int RTp, const void* bias, int M, int N, int K, void* y, int64_t ldy) {
+  svdq::GemmParams p{};
+  p.qw = static_cast<const uint8_t*>(qw);
+  p.sw = static_cast<const uint16_t*>(sw);
+  p.mid = mid;
+  p.l1cat = static_cast<const uint16_t*>(l1cat);
+  p.RTp = RTp;
+  p.bias = static_cast<const uint16_t*>(bias);
+  p.y = y;
+  p.ldy = ldy;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  return p;
+}
+
+int svdq_w4a4_gemm(const void* qx, const void* sx, const void* qw, const void* sw, const float* mid,
+                   const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                   void* y, int64_t ldy, int out_f32, hipStream_t stream) {
+  if (int e = gemm_common_checks("w4a4_gemm", qw, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32)) return e;
+  if (!qx || !sx) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
+  if (!aligned16(qx)) return fail(SVDQ_ERR_ALIGN, "w4a4_gemm: qx must be 16-byte aligned");
+  svdq::GemmParams p = gemm_params(qw, sw, mid, l1cat, RTp, bias, M, N, K, y, ldy);
+  p.qx = static_cast<const uint8_t*>(qx);
+  p.sx = static_cast<const uint16_t*>(sx);
+  return launched(svdq::launch_w4a4(p, group, out_f32 == 1, stream), "w4a4_gemm");
+}
+
+int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const float* mid,
+                    const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                    void* y, int64_t ldy, int out_f32, hipStream_t stream) {
+  if (int e = gemm_common_checks("w4a16_gemm", qw, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32)) return e;
+  if (!xhat) return fail(SVDQ_ERR_ARG, "w4a16_gemm: null pointer");
+  if (ldxh < K || ldxh % 8 || !aligned16(xhat))
+    return fail(SVDQ_ERR_ALIGN, "w4a16_gemm: xhat must be 16-byte aligned with ldxh >= K, ldxh %% 8 == 0");
+  svdq::GemmParams p = gemm_params(qw, sw, mid, l1cat, RTp, bias, M, N, K, y, ldy);
+  p.xhat = static_cast<const uint16_t*>(xhat);
+  p.ldxh = ldxh;
+  return launched(svdq::launch_w4a16(p, group, out_f32 == 1, stream), "w4a16_gemm");
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+// Shared device helpers for the gfx950 SVDQuant kernels.
+//
+// Storage conventions (the reference checkpoint layout, runtime/load.py:90-126):
+//   activations / smooth / l1 / l2 / bias : bf16, carried as uint16_t bits
+//   weight scales                         : fp16 bits
+//   packed INT4                           : uint8, byte j = (q[2j]+8) | (q[2j+1]+8) << 4
+//
+// MFMA register layouts used throughout (CDNA 32x32 family, wave64):
+//   A operand of a 32x32xK MFMA: lane l supplies row (l % 32); lanes 0-31 and
+//   32-63 supply two disjoint halves of the K slice.  B likewise with columns.
+//   The kernels only rely on A and B using the SAME (lane-half, element) -> k
+//   assignment, which makes the product independent of the hardware's
+//   internal k order.
+//   D (32x32 accumulator, 16 regs/lane): reg r of lane l holds
+//   row = 8*(r/4) + 4*(l/32) + (r%4), col = l % 32.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace svdq {
+
+typedef int      i32x4  __attribute__((ext_vector_type(4)));
+typedef int      i32x16 __attribute__((ext_vector_type(16)));
+typedef float    f32x2  __attribute__((ext_vector_type(2)));
+typedef float    f32x4  __attribute__((ext_vector_type(4)));
+typedef float    f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16   bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16   bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2  __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4  __attribute__((ext_vector_type(4)));
+
+// ---- bf16 / fp16 bit helpers ------------------------------------------------
+__device__ __forceinline__ float bf16lo(uint32_t d) { return __uint_as_float(d << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t d) { return __uint_as_float(d & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+// Two floats -> two bf16 (round to nearest even: v_cvt_pk_bf16_f32), low half = lo.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  bf16x2 b = __builtin_convertvector(v, bf16x2);
+  return __builtin_bit_cast(uint32_t, b);
+}
+// Round one float to the nearest bf16 value, returned as float.
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16lo(pack_bf16x2(f, 0.0f));
+}
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// ---- division ---------------------------------------------------------------
+// Correctly rounded float32 quotient x / s given rs = RN(1/s) (one multiply and two
+// FMAs).  Exhaustively verified for every pair of bf16-representable operands whose
+// quotient is a normal float32 (tests/test_division_exact.py); callers guarantee that
+// range and use the IEEE division otherwise.
+__device__ __forceinline__ float div_rcp(float x, float s, float rs) {
+  float q0 = x * rs;
+  float r = __builtin_fmaf(-q0, s, x);
+  return __builtin_fmaf(r, rs, q0);
+}
+
+// ---- MFMA wrappers ----------------------------------------------------------
+__device__ __forceinline__ i32x16 mfma_i8_32x32x32(i32x4 a, i32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_bf16_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Split 8 floats into bf16 hi + bf16 lo parts (x ~= hi + lo to ~2^-17 relative).
+__device__ __forceinline__ void split_hi_lo(const float* v, u32x4& hi, u32x4& lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t h = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    hi[i] = h;
+    lo[i] = pack_bf16x2(v[2 * i] - bf16lo(h), v[2 * i + 1] - bf16hi(h));
+  }
+}
+
+// XCD-aware block order: hardware hands consecutive workgroup ids to the 8 XCDs round-robin;
+// remap so that each XCD receives a contiguous range of output tiles (shared A rows / B columns
+// stay within one L2), then walk tiles in column-major groups of `group_m` block-rows.
+__device__ __forceinline__ void tile_coords(int bid, int nbm, int nbn, int group_m, int& bm, int& bn) {
+  const int nblk = nbm * nbn;
+  int lin = bid;
+  if (nblk % 8 == 0) lin = (bid % 8) * (nblk / 8) + bid / 8;
+  const int per_group = group_m * nbn;
+  const int gid = lin / per_group;
+  const int first_m = gid * group_m;
+  const int gm = min(nbm - first_m, group_m);
+  const int in = lin % per_group;
+  bm = first_m + in % gm;
+  bn = in / gm;
+}
+
+}  // namespace svdq

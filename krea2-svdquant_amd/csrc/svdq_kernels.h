@@ -1,0 +1,50 @@
+// Internal kernel parameter blocks and launchers (host side).  Not part of the C-ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace svdq {
+
+struct ActParams {
+  const uint16_t* x;        // [M, ldx] bf16
+  long ldx;
+  const float* srs;         // [2K] f32: s, then RN(1/s)
+  const uint16_t* l2;       // [r, K] bf16
+  const uint16_t* lora;     // [rl, K] bf16 (null when rl == 0)
+  const float* lora_mult;   // [rl]
+  int r, rl;
+  int M, K, RTp;            // RTp: row stride of mid (>= r + rl, multiple of 32)
+  uint8_t* qx;              // [M, K/2]
+  uint16_t* sx;             // [M, K/G] bf16
+  uint16_t* xhat;           // [M, ldxh] bf16 (null unless requested)
+  long ldxh;
+  float* mid;               // [M, RTp]
+  float* midp;              // [S, M, RTp] split partials (S > 1)
+  int* counters;            // [ceil(M/64)] arrival counters, zero between launches
+  int gps;                  // K-groups per split
+  int exact;                // 1: IEEE division for x / s everywhere
+};
+
+struct GemmParams {
+  const uint8_t* qx;        // W4A4: [M, K/2] packed activation codes
+  const uint16_t* sx;       // W4A4: [M, K/G] bf16 activation scales
+  const uint16_t* xhat;     // W4A16: [M, ldxh] bf16 smoothed activations
+  long ldxh;
+  const uint8_t* qw;        // [N, K/2] packed weight codes
+  const uint16_t* sw;       // [N, K/G] fp16 weight scales
+  const float* mid;         // [M, RTp] f32 low-rank/LoRA down projections
+  const uint16_t* l1cat;    // [N, RTp] bf16 up projections (zero padded)
+  int RTp;
+  const uint16_t* bias;     // [N] bf16 or null
+  void* y;                  // [M, ldy] bf16 or f32
+  long ldy;
+  int M, N, K;
+};
+
+int act_splits(int M, int K, int G);
+hipError_t launch_act(const ActParams& p, int G, int nt, bool quant, bool xhat, int splits, hipStream_t st);
+hipError_t launch_prepare_smooth(const uint16_t* s, float* srs, int K, hipStream_t st);
+hipError_t launch_w4a4(const GemmParams& p, int G, bool out_f32, hipStream_t st);
+hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st);
+
+}  // namespace svdq

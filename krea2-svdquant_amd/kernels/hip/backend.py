@@ -1,0 +1,165 @@
+"""The gfx950 backend function: ``fn(x, state) -> y`` like reference
+``kernels/triton/generic_int4.py:227-244`` (``svdquant_linear_triton_generic``).
+
+Two launches per layer forward:
+
+* W4A4  (``mode="w4a4"``):  ``svdq::act_quant`` (codes, scales, mid) -> ``svdq::w4a4_gemm``;
+* W4A16 (``mode="w4a16"``): ``svdq::act_quant`` (x_hat, mid)         -> ``svdq::w4a16_gemm``.
+
+LoRA adapters (reference ``runtime/linear.py:11-45``) are fused: their down projections run
+in the activation pass on the raw x (times each adapter's multiplier) and their up
+projections are concatenated behind ``l1`` in the GEMM epilogue.  Per-layer constants
+(``1/s``, the concatenated ``l1 | up`` matrix, the padded ``l2``) are built once by
+``prepare_layer`` and cached by ``SVDQuantLinear``.
+
+Errors follow the reference: ``ValueError`` for shapes, ``TypeError`` for dtypes,
+``RuntimeError`` for an unusable backend (no GPU, unpacked checkpoint, missing library).
+Nothing falls back to another implementation.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+from torch import Tensor
+
+from ...quant.state import SVDQuantLinearState
+from . import ops
+
+
+@dataclass
+class PreparedLayer:
+    """Device-resident per-layer operands of the two kernels."""
+    srs: Tensor                  # f32 [2Kp]: s, RN(1/s)
+    l2: Tensor                   # bf16 [r, Kp]
+    l1cat: Tensor                # bf16 [N, RTp] = [l1 | up_1 | ... | 0]
+    lora_down: Optional[Tensor]  # bf16 [rl, Kp]
+    lora_mult: Optional[Tensor]  # f32 [rl]
+    qweight: Tensor              # uint8 [N, Kp/2]
+    weight_scales: Tensor        # fp16 [N, Kp/G]
+    bias: Optional[Tensor]       # bf16 [N]
+    group_size: int
+    n: int
+    k: int                       # logical in_features
+    kp: int                      # padded in_features
+    rtp: int
+
+    @property
+    def device(self) -> torch.device:
+        return self.qweight.device
+
+
+def _pad_cols(t: Tensor, kp: int, value: float = 0.0) -> Tensor:
+    if t.shape[-1] == kp:
+        return t.contiguous()
+    out = t.new_full((*t.shape[:-1], kp), value)
+    out[..., : t.shape[-1]] = t
+    return out
+
+
+def prepare_layer(state: SVDQuantLinearState, adapters: Sequence = (),
+                  device: torch.device | str | None = None) -> PreparedLayer:
+    """Validate a packed state and build the kernels' per-layer operands on ``device``.
+
+    ``adapters`` are objects with ``down_weight`` [rl, K], ``up_weight`` [N, rl] and
+    ``multiplier`` (``SVDQuantLoRAAdapter``).
+    """
+    if not state.qweight_packed:
+        raise RuntimeError("HIP gfx950 backend expects packed uint8 qweight (qweight_packed=True)")
+    dev = torch.device(device) if device is not None else state.qweight.device
+    if dev.type != "cuda":
+        raise RuntimeError("HIP gfx950 backend needs its state on a GPU device")
+    n, k = (int(v) for v in state.original_shape)
+    qweight = state.qweight.to(dev).contiguous()
+    if qweight.dtype != torch.uint8 or qweight.dim() != 2 or qweight.shape[0] != n:
+        raise TypeError(f"qweight must be uint8 [{n}, Kp/2], got {qweight.dtype} {tuple(qweight.shape)}")
+    kp = int(state.padded_in_features or qweight.shape[1] * 2)
+    if kp != qweight.shape[1] * 2 or kp < k:
+        raise ValueError(f"padded_in_features={kp} inconsistent with qweight {tuple(qweight.shape)} and K={k}")
+    g = int(state.group_size)
+    if kp % g:
+        raise ValueError(f"padded K={kp} is not a multiple of group_size={g}")
+    scales = state.weight_scales.to(dev)
+    if scales.dtype != torch.float16:
+        raise TypeError(f"weight_scales must be float16 (checkpoint layout), got {scales.dtype}")
+    smooth = _pad_cols(state.smooth_scale.to(dev, torch.bfloat16), kp, 1.0)
+    l1 = state.l1.to(dev, torch.bfloat16)
+    l2 = _pad_cols(state.l2.to(dev, torch.bfloat16), kp)
+    r = int(l2.shape[0])
+    if tuple(l1.shape) != (n, r):
+        raise ValueError(f"l1 must be [{n}, {r}], got {tuple(l1.shape)}")
+    downs, ups, mults = [], [], []
+    for ad in adapters:
+        down = ad.down_weight.to(dev, torch.bfloat16)
+        up = ad.up_weight.to(dev, torch.bfloat16)
+        downs.append(_pad_cols(down, kp))
+        ups.append(up)
+        mults.append(torch.full((down.shape[0],), float(ad.multiplier), dtype=torch.float32, device=dev))
+    rl = sum(d.shape[0] for d in downs)
+    rtp = ops.rank_padded(r + rl)
+    l1cat = torch.zeros((n, rtp), dtype=torch.bfloat16, device=dev)
+    l1cat[:, :r] = l1
+    col = r
+    for up in ups:
+        l1cat[:, col: col + up.shape[1]] = up
+        col += up.shape[1]
+    bias = None if state.bias is None else state.bias.to(dev, torch.bfloat16).contiguous()
+    return PreparedLayer(
+        srs=ops.prepare_smooth(smooth.contiguous()),
+        l2=l2.contiguous(),
+        l1cat=l1cat,
+        lora_down=torch.cat(downs, 0).contiguous() if downs else None,
+        lora_mult=torch.cat(mults, 0).contiguous() if mults else None,
+        qweight=qweight,
+        weight_scales=scales.contiguous(),
+        bias=bias,
+        group_size=g, n=n, k=k, kp=kp, rtp=rtp,
+    )
+
+
+def _flatten(x: Tensor) -> tuple[Tensor, tuple[int, ...]]:
+    if x.ndim < 2:
+        raise ValueError(f"expected [..., K] activation, got shape {tuple(x.shape)}")
+    return x.reshape(-1, x.shape[-1]).contiguous(), tuple(x.shape[:-1])
+
+
+def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_f32: bool = False,
+                     exact_div: bool = False) -> Tensor:
+    """One SVDQuantLinear forward on prepared operands; returns [..., N]."""
+    if not x.is_cuda:
+        raise RuntimeError("HIP gfx950 backend needs a GPU tensor")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"HIP gfx950 backend takes bfloat16 activations, got {x.dtype}")
+    if x.device != prep.device:
+        raise ValueError(f"activation on {x.device}, layer on {prep.device}")
+    x2, lead = _flatten(x)
+    k = x2.shape[1]
+    if k > prep.kp:
+        raise ValueError(f"activation K={k} exceeds packed weight K={prep.kp}")
+    if k != prep.kp:
+        x2 = _pad_cols(x2, prep.kp)
+    if mode == "w4a4":
+        qx, sx, _, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
+                                       prep.group_size, prep.rtp, True, False, exact_div)
+        y = ops.w4a4_gemm(qx, sx, prep.qweight, prep.weight_scales, mid, prep.l1cat, prep.bias,
+                          prep.group_size, out_f32)
+    elif mode == "w4a16":
+        _, _, xhat, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
+                                        prep.group_size, prep.rtp, False, True, exact_div)
+        y = ops.w4a16_gemm(xhat, prep.qweight, prep.weight_scales, mid, prep.l1cat, prep.bias,
+                           prep.group_size, out_f32)
+    else:
+        raise ValueError(f"mode must be 'w4a4' or 'w4a16', got {mode!r}")
+    return y.reshape(*lead, prep.n)
+
+
+def svdquant_linear_hip_gfx950(x: Tensor, state: SVDQuantLinearState, *, adapters: Sequence = (),
+                               mode: str = "w4a4", out_f32: bool = False) -> Tensor:
+    """Stateless backend entry (prepares the layer on every call; modules cache it)."""
+    return forward_prepared(x, prepare_layer(state, adapters, x.device), mode=mode, out_f32=out_f32)
+
+
+def svdquant_linear_hip_gfx950_w4a16(x: Tensor, state: SVDQuantLinearState, *, adapters: Sequence = (),
+                                     out_f32: bool = False) -> Tensor:
+    return svdquant_linear_hip_gfx950(x, state, adapters=adapters, mode="w4a16", out_f32=out_f32)

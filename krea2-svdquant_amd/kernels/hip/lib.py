@@ -1,0 +1,86 @@
+"""ctypes binding of ``libsvdq_gfx950.so`` (the C-ABI declared in ``include/svdq_gfx950.h``).
+
+The library is loaded after ``import torch`` so that its ``libamdhip64.so.7`` dependency
+resolves to the HIP runtime torch already loaded.  There is no fallback: if the library is
+missing or fails to load, every entry raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the library load: HIP runtime binding)
+
+PKG_DIR = Path(__file__).resolve().parents[2]
+LIB_PATH = Path(os.environ.get("SVDQ_GFX950_LIB", PKG_DIR / "_lib" / "libsvdq_gfx950.so"))
+
+SVDQ_ACT_QUANT = 1
+SVDQ_ACT_XHAT = 2
+SVDQ_ACT_EXACT_DIV = 4
+
+STATUS = {0: "SVDQ_OK", -1: "SVDQ_ERR_ARG", -2: "SVDQ_ERR_SHAPE", -3: "SVDQ_ERR_ALIGN",
+          -4: "SVDQ_ERR_UNSUPPORTED", -5: "SVDQ_ERR_LAUNCH"}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_U = ctypes.c_uint
+
+# name -> (restype, argtypes); the exact set of symbols include/svdq_gfx950.h declares.
+SIGNATURES = {
+    "svdq_version": (ctypes.c_char_p, []),
+    "svdq_last_error": (ctypes.c_char_p, []),
+    "svdq_group_supported": (_I, [_I]),
+    "svdq_prepare_smooth": (_I, [_P, _P, _I, _P]),
+    "svdq_act_quant_workspace": (_I, [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_L),
+                                      ctypes.POINTER(_L)]),
+    "svdq_act_quant": (_I, [_P, _L, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _U, _P, _P, _P, _L,
+                            _P, _P, _P, _I, _P]),
+    "svdq_w4a4_gemm": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
+    "svdq_w4a16_gemm": (_I, [_P, _L, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class SVDQError(RuntimeError):
+    """A C-ABI call returned a non-zero svdq_status."""
+
+    def __init__(self, fn: str, status: int, message: str):
+        super().__init__(f"{fn} failed with {STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library, with argument types set."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"gfx950 kernel library not found at {LIB_PATH}; build it with "
+                    "__graft_entry__.build() (hipcc --offload-arch=gfx950)")
+            lib = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call a status-returning entry point; raise ``SVDQError`` on a non-zero status."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        raise SVDQError(name, status, lib.svdq_last_error().decode())
+
+
+def version() -> str:
+    return load().svdq_version().decode()

@@ -1,0 +1,69 @@
+"""The C-ABI library: built, loadable, exports exactly what include/svdq_gfx950.h declares, and
+validates arguments on the host (calls that fail validation make no GPU call)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from krea2_svdquant_amd.kernels.hip import lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "svdq_gfx950.h"
+
+
+def declared_symbols() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(svdq_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    handle = lib.load()
+    decl = declared_symbols()
+    assert decl == set(lib.SIGNATURES), "ctypes signatures out of sync with the header"
+    for name in decl:
+        assert getattr(handle, name) is not None
+    assert lib.version().startswith("svdq_gfx950")
+
+
+def test_group_support_and_workspace_sizing():
+    h = lib.load()
+    assert h.svdq_group_supported(64) == 1 and h.svdq_group_supported(128) == 1
+    assert h.svdq_group_supported(32) == 0
+    s, mp, ct = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64()
+    lib.call("svdq_act_quant_workspace", 4096, 6144, 64, 32, ctypes.byref(s), ctypes.byref(mp), ctypes.byref(ct))
+    assert s.value >= 1 and ct.value == 64
+    assert mp.value == (s.value * 4096 * 32 if s.value > 1 else 0)
+    lib.call("svdq_act_quant_workspace", 256, 6144, 64, 32, ctypes.byref(s), ctypes.byref(mp), ctypes.byref(ct))
+    assert 1 < s.value <= 6144 // 64 // 4
+
+
+@pytest.mark.parametrize("args,status,needle", [
+    ((4096, 6144, 32, 32), -4, "group size 32"),
+    ((4096, 6100, 64, 32), -2, "multiple of group"),
+    ((4096, 6144, 64, 48), -2, "RTp=48"),
+    ((0, 6144, 64, 32), -1, "M=0"),
+])
+def test_workspace_rejects_bad_arguments(args, status, needle):
+    s, mp, ct = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64()
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_act_quant_workspace", *args, ctypes.byref(s), ctypes.byref(mp), ctypes.byref(ct))
+    assert ei.value.status == status and needle in str(ei.value)
+
+
+def test_gemm_rejects_null_and_misaligned_pointers_before_any_launch():
+    nul = None
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a4_gemm", nul, nul, nul, nul, nul, nul, 32, nul, 128, 128, 128, 64, nul, 128, 0, nul)
+    assert ei.value.status == -1
+    fake = ctypes.c_void_p(0x1000)
+    odd = ctypes.c_void_p(0x1008)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a4_gemm", fake, fake, odd, fake, fake, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0, nul)
+    assert ei.value.status == -3
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a16_gemm", fake, 100, fake, fake, fake, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0, nul)
+    assert ei.value.status == -3
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_act_quant", fake, 128, fake, fake, 200, nul, 0, nul, 64, 128, 64, 224, 1, fake, fake, nul, 0,
+                 fake, nul, nul, 1, nul)
+    assert ei.value.status == -4  # ceil(200/32) = 7 MFMA column tiles > 4

@@ -1,0 +1,92 @@
+"""GPU tests of the module boundary (SVDQuantLinear) and BASELINE-sized layers."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as nm
+from oracle import sim, synth
+from tests.gpu_util import bf16_bits_of, bf16_tensor, from_device_state, rel_l2, to_device_state
+
+pytestmark = pytest.mark.gpu
+
+
+def test_module_forward_with_lora_matches_oracle(dev):
+    from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
+    x = synth.make_activation(96, 1024, seed=31)
+    st = synth.make_layer(384, 1024, x, rank=32, group_size=64, seed=32, bias=True)
+    mod = SVDQuantLinear(to_device_state(st, dev), backend="auto")
+    y0 = mod(bf16_tensor(x, dev).reshape(2, 48, 1024))
+    assert tuple(y0.shape) == (2, 48, 384) and y0.dtype == torch.bfloat16
+    ref0 = sim.w4a4_eval(x, st)["y"]
+    assert rel_l2(y0.float().cpu().numpy().reshape(96, 384), nm.bf16(ref0.astype(np.float32))) < 1e-3
+    ad = synth.make_adapter(384, 1024, rank=64, seed=33, scale=0.8)
+    mod.add_lora_adapter(bf16_tensor(ad.down, dev), bf16_tensor(ad.up, dev), scale=0.8)
+    st.adapters.append(ad)
+    y1 = mod(bf16_tensor(x, dev))
+    ref1 = sim.w4a4_eval(x, st)["y"]
+    assert rel_l2(y1.float().cpu().numpy(), nm.bf16(ref1.astype(np.float32))) < 1e-3
+    # _forward_base excludes adapters, as in the reference
+    yb = mod._forward_base(bf16_tensor(x, dev))
+    assert torch.equal(yb, y0.reshape(96, 384))
+
+
+def test_w4a16_module_matches_sim_math(dev):
+    from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
+    x = synth.make_activation(64, 512, seed=41)
+    st = synth.make_layer(256, 512, x, rank=32, group_size=64, seed=42, bias=True)
+    mod = SVDQuantLinear(to_device_state(st, dev), backend="hip_gfx950_w4a16")
+    y = mod(bf16_tensor(x, dev)).float().cpu().numpy()
+    ref = sim.w4a16_eval(x, st)["y"]
+    assert rel_l2(y, nm.bf16(ref.astype(np.float32))) < 1e-3
+    y_sim = sim.sim_forward_torch(torch.from_numpy(x).to(torch.bfloat16), st).float().numpy()
+    assert rel_l2(y, y_sim) < 1e-2   # the reference sim rounds mid and every sum to bf16
+
+
+def test_config0_layer(dev):
+    """BASELINE config 0 shape: M=256, K=N=6144, rank 32, group 64, outlier channels."""
+    from krea2_svdquant_amd.kernels.hip import backend
+    x = synth.make_activation(256, 6144, seed=0)
+    st = synth.make_layer(6144, 6144, x, rank=32, group_size=64, seed=1)
+    prep = backend.prepare_layer(to_device_state(st, dev), (), dev)
+    xd = bf16_tensor(x, dev)
+    r = sim.w4a4_eval(x, st)
+    y32 = backend.forward_prepared(xd, prep, mode="w4a4", out_f32=True).cpu().numpy()
+    e = rel_l2(y32, r["y"])
+    print(f"  config0 w4a4 rel_l2={e:.3e}")
+    assert e < 1e-4
+    y16 = backend.forward_prepared(xd, prep, mode="w4a16", out_f32=True).cpu().numpy()
+    e16 = rel_l2(y16, sim.w4a16_eval(x, st)["y"])
+    print(f"  config0 w4a16 rel_l2={e16:.3e}")
+    assert e16 < 1e-4
+
+
+def test_full_size_ffup_codes_exact_and_rows_sampled(dev):
+    """Config 1 ff.up at full size (M=4096, K=6144, N=16384): every activation code and scale
+    bit-exact, a row sample of the layer output against float64, and the exact power-of-two
+    homogeneity y(2x) - b = 2 (y(x) - b) over the whole output."""
+    from krea2_svdquant_amd.kernels.hip import backend, ops
+    from krea2_svdquant_amd.quant.convert import convert_linear
+    torch.manual_seed(0)
+    m, k, n = 4096, 6144, 16384
+    x = synth.make_activation(m, k, seed=0)
+    xd = bf16_tensor(x, dev)
+    w = torch.randn(n, k, device=dev) * 0.02
+    ds = convert_linear(w, torch.randn(n, device=dev) * 0.1, xd.float().abs().amax(0), rank=32,
+                        group_size=64, smooth_clamp=(None, None), seed=3)
+    del w
+    prep = backend.prepare_layer(ds, (), dev)
+    qx, sx, _, mid = ops.act_quant(xd, prep.srs, prep.l2, None, None, 64, prep.rtp, True, False, False)
+    st = from_device_state(ds)
+    xh, packed, sxo, _ = sim.quantize_activations(x, st)
+    assert np.array_equal(qx.cpu().numpy(), packed)
+    assert np.array_equal(bf16_bits_of(sx), nm.bf16_bits(sxo))
+    y = backend.forward_prepared(xd, prep, mode="w4a4", out_f32=True)
+    rows = np.random.default_rng(1).choice(m, 48, replace=False)
+    r = sim.w4a4_eval(x[rows], st)
+    e = rel_l2(y[torch.from_numpy(rows).to(dev)].cpu().numpy(), r["y"])
+    print(f"  ff.up sampled rel_l2={e:.3e}")
+    assert e < 1e-4
+    y2 = backend.forward_prepared(xd * 2, prep, mode="w4a4", out_f32=True)
+    b = ds.bias.float()
+    hom = ((y2 - b) - 2 * (y - b)).norm() / (y - b).norm()
+    assert hom.item() < 1e-6
