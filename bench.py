@@ -125,11 +125,12 @@ def main() -> int:
     log(f"{ms:.4f} ms/step")
 
     # per-kernel averages, each kernel timed alone on the same (current) stream
-    qx, sx, _, mid = ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, True, False, False)
-    ms_act = time_loop(lambda: ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, True, False, False),
-                       args.steps)
-    ms_gemm = time_loop(lambda: ops.w4a4_gemm(qx, sx, prep.qweight, prep.weight_scales, mid, prep.l1cat, None, g,
-                                              False), args.steps)
+    opc = ops.OPERAND_E4M3
+    qa, sx, _, _, mid = ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False)
+    ms_act = time_loop(lambda: ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False,
+                                             False), args.steps)
+    ms_gemm = time_loop(lambda: ops.w4a4_gemm(qa, sx, prep.qweight, prep.weight_scale_pairs(opc), mid, prep.l1cat,
+                                              None, g, opc, False), args.steps)
     log(f"act {ms_act:.4f} ms, gemm {ms_gemm:.4f} ms")
     flops = 2.0 * m * n * k
     act_bytes = 2 * m * k + 8 * k + 2 * r * k + m * k // 2 + 2 * m * (k // g) + 4 * m * prep.rtp

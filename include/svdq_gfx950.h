@@ -38,9 +38,15 @@ typedef enum svdq_status {
 } svdq_status;
 
 /* flags of svdq_act_quant */
-#define SVDQ_ACT_QUANT 1u      /* write packed A4 codes qx and bf16 scales sx          */
-#define SVDQ_ACT_XHAT 2u       /* write the smoothed bf16 activation x_hat              */
-#define SVDQ_ACT_EXACT_DIV 4u  /* IEEE division for x / s everywhere (slow reference)   */
+#define SVDQ_ACT_PACKED 1u        /* also write the canonical packed A4 codes qx (pack.py layout) */
+#define SVDQ_ACT_XHAT 2u          /* write the smoothed bf16 activation x_hat                   */
+#define SVDQ_ACT_EXACT_DIV 4u     /* IEEE division for x / s everywhere (slow reference mode)   */
+#define SVDQ_ACT_OPERAND_E4M3 8u  /* quantize: write scales sx and e4m3 operand codes qa        */
+#define SVDQ_ACT_OPERAND_I8 16u   /* quantize: write scales sx and int8 (16*q) operand codes qa */
+
+/* Operand formats of svdq_w4a4_gemm (must match the SVDQ_ACT_OPERAND_* flag used). */
+#define SVDQ_OPERAND_E4M3 0    /* FP8 MFMA (v_mfma_f32_32x32x64_f8f6f4): every INT4 code is exact */
+#define SVDQ_OPERAND_I8 1      /* INT8 MFMA (v_mfma_i32_32x32x32_i8) on 16*q                     */
 
 /* Library version string. */
 const char* svdq_version(void);
@@ -57,12 +63,10 @@ int svdq_group_supported(int group);
  *   smooth : bf16 [K]      srs : f32 [2K] (output) */
 int svdq_prepare_smooth(const void* smooth, float* srs, int K, hipStream_t stream);
 
-/* Workspace of svdq_act_quant for (M, K, group, RTp): number of K splits, floats of the
- * split-partial buffer `midp` and ints of the `counters` buffer.  `counters` must be zero
- * before the first call; every completed call leaves it zero again.  Calls sharing one
- * `counters`/`midp` pair must not run concurrently. */
-int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int64_t* midp_floats,
-                             int64_t* counter_ints);
+/* Output sizing of svdq_act_quant for (M, K, group, RTp): the number S of K splits the
+ * activation pass uses and the floats of its `mid` output (S * M * RTp: one partial per
+ * split, added by the GEMM epilogue in split order). */
+int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int64_t* mid_floats);
 
 /* Fused activation pass.  Replaces reference quant/svd.py:121-122 (x_hat = x / smooth),
  * quant/pack.py:6-23 + 47-56 applied per group to x_hat (the A4 step of README.md:188-195),
@@ -71,34 +75,48 @@ int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int6
  *   x        : bf16 [M, ldx]          srs : f32 [2K] from svdq_prepare_smooth
  *   l2       : bf16 [r, K]            lora_down : bf16 [rl, K] or NULL (rl = 0)
  *   lora_mult: f32 [rl]: per-column multiplier scale * alpha / rank of the owning adapter
- *   qx       : u8 [M, K/2]   (SVDQ_ACT_QUANT)      sx : bf16 [M, K/group]
- *   xhat     : bf16 [M, ldxh] (SVDQ_ACT_XHAT)
- *   mid      : f32 [M, RTp]: columns [0, r) = x_hat @ l2^T, [r, r+rl) = mult * (x @ A^T),
- *              [r+rl, RTp) = 0.   RTp % 32 == 0, RTp >= r + rl, ceil(r/32)+ceil(rl/32) <= 4.
- *   midp, counters : workspace sized by svdq_act_quant_workspace. */
+ *   Quantizing (one SVDQ_ACT_OPERAND_* flag):
+ *     sx : bf16 [M, K/group] scales, bit-exact bf16(max(amax, bf16(1e-8)) / 7)
+ *     qa : u8 [M, K] operand codes of the W4A4 GEMM: the code of k sits at byte
+ *          8*(k/8) + perm(k%8), perm = {0,4,1,5,2,6,3,7} (even k of a chunk of 8, then odd k);
+ *          e4m3(q) or int8 16*q
+ *     qx : u8 [M, K/2] canonical packed codes (pack.py:47-56), if SVDQ_ACT_PACKED
+ *   xhat     : bf16 [M, ldxh] (SVDQ_ACT_XHAT; with a quantizing flag only for e4m3)
+ *   mid      : f32 [S, M, RTp] split partials, summed over S: columns [0, r) = x_hat @ l2^T,
+ *              [r, r+rl) = mult * (x @ A^T), [r+rl, RTp) = 0.   RTp % 32 == 0, RTp >= r + rl,
+ *              ceil(r/32) + ceil(rl/32) <= 4;  S (`splits`) from svdq_act_quant_workspace. */
 int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
                    const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
-                   int RTp, unsigned flags, void* qx, void* sx, void* xhat, int64_t ldxh, float* mid,
-                   float* midp, int* counters, int splits, hipStream_t stream);
+                   int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
+                   float* mid, int splits, hipStream_t stream);
+
+/* Per-layer weight-scale operand of svdq_w4a4_gemm: swp[i] = bf16 hi | bf16 lo << 16 with
+ * hi + lo == float(sw[i]) exactly (times 1/256 for SVDQ_OPERAND_I8).  No reference
+ * counterpart: it splits the checkpoint's fp16 weight_scales (runtime/load.py:116) for the
+ * bf16 MFMA that forms the per-group scale products.
+ *   sw : fp16 [count]      swp : u32 [count] (output) */
+int svdq_prepare_weight_scales(const void* sw, void* swp, int64_t count, int operand, hipStream_t stream);
 
 /* W4A4 GEMM with fused epilogue.  Replaces the residual product of reference
  * quant/svd.py:158 / kernels/triton/generic_int4.py:18-82 (with INT4 activations), the
  * low-rank add + bias of generic_int4.py:84-133 / svd.py:159-163 and the LoRA add of
  * runtime/linear.py:158-160:
- *   y = sum_g sx sw (qx . qw)_g + mid @ l1cat^T + bias
- *   qx : u8 [M, K/2]   sx : bf16 [M, K/group]   qw : u8 [N, K/2]   sw : fp16 [N, K/group]
- *   mid: f32 [M, RTp]  l1cat : bf16 [N, RTp] = [l1 | up_1 | up_2 ... | 0]
+ *   y = sum_g sx sw (qa . qw)_g + mid @ l1cat^T + bias
+ *   qa : u8 [M, K] operand codes (svdq_act_quant) in `operand` format (SVDQ_OPERAND_*)
+ *   sx : bf16 [M, K/group]   qw : u8 [N, K/2] (checkpoint layout)
+ *   swp: u32 [N, K/group] from svdq_prepare_weight_scales (same operand format)
+ *   mid: f32 [splits, M, RTp] from svdq_act_quant    l1cat : bf16 [N, RTp] = [l1 | up_1 | ... | 0]
  *   bias: bf16 [N] or NULL     y : [M, ldy], bf16 (out_f32 = 0) or f32 (out_f32 = 1) */
-int svdq_w4a4_gemm(const void* qx, const void* sx, const void* qw, const void* sw, const float* mid,
-                   const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
-                   void* y, int64_t ldy, int out_f32, hipStream_t stream);
+int svdq_w4a4_gemm(const void* qa, int operand, const void* sx, const void* qw, const void* swp,
+                   const float* mid, int splits, const void* l1cat, int RTp, const void* bias, int M, int N,
+                   int K, int group, void* y, int64_t ldy, int out_f32, hipStream_t stream);
 
 /* W4A16 GEMM with fused epilogue: the reference pytorch_sim math (quant/svd.py:119-163;
  * dequantization pack.py:26-44 in bf16) and kernels/triton/generic_int4.py:18-133.
  *   xhat : bf16 [M, ldxh] (from svdq_act_quant with SVDQ_ACT_XHAT); other arguments as in
  *   svdq_w4a4_gemm. */
 int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const float* mid,
-                    const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                    int splits, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
                     void* y, int64_t ldy, int out_f32, hipStream_t stream);
 
 #ifdef __cplusplus

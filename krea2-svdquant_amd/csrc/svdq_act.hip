@@ -2,18 +2,23 @@
 //
 //   x_hat = bf16(x / s)                                  quant/svd.py:121-122
 //   sx    = bf16(max(amax_g |x_hat|, bf16(1e-8)) / 7)    quant/pack.py:20
-//   qx    = clamp(rne(x_hat / sx), -8, 7), packed         quant/pack.py:21, :53-56
+//   q     = rne(x_hat / sx)  (clamp(-8, 7) never binds)   quant/pack.py:21
+//   qa    = 8-bit GEMM operand codes of q;  qx = canonical packed codes, pack.py:53-56
 //   mid   = x_hat @ L2^T            (low-rank down)      quant/svd.py:159
 //   lmid  = mult * (x @ A^T)        (LoRA down, raw x)    runtime/linear.py:42-45
 //
-// Work split: a workgroup (4 waves) owns 64 rows and a contiguous range of K-groups (one
-// "split"); wave w takes every 4th group of the range.  Within a wave, lane l handles rows
-// l%32 and 32 + l%32 and, of each group, the G/2 contiguous columns of lane-half l/32, which
-// is exactly the A-operand layout of the 32x32x16 bf16 MFMA, so mid/lmid accumulate in
-// registers without an LDS round trip.  Per-wave partials are summed in a fixed wave order
-// in LDS; partials of the splits of a row tile are summed in a fixed split order by the
-// last workgroup to finish (atomic arrival counter, reset by that workgroup), so results are
-// deterministic.
+// Layout: a workgroup (4 waves) owns 64 rows and a contiguous range of K-groups (one
+// "split"); wave w takes every 4th group of the range.  Lane l of a wave holds row l, so a
+// group's smoothing scales are the same for the whole wave (scalar loads, SGPR operands) and
+// the group absmax is lane-local.  The 32x32x16 bf16 A operand of the low-rank MFMAs wants
+// the two 8-column halves of a 16-column slice of one row in lanes l and l+32; one
+// v_permlane32_swap per register turns the lane-per-row data into exactly that for both
+// 32-row tiles.  Per-wave partials are summed in a fixed wave order in LDS and each split
+// writes its own partial mid[split]; the GEMM epilogue adds the splits in a fixed order
+// (deterministic, and no device-scope fences, which cost an L2 write-back each).
+//
+// Codes never need the reference's clamp: |x_hat| <= amax and sx >= (amax/7)(1 - 2^-9), so
+// |x_hat / sx| < 7.02 rounds into [-7, 7].
 #include "svdq_common.h"
 #include "svdq_kernels.h"
 
@@ -23,53 +28,75 @@ namespace {
 
 constexpr float kBf16OneEMinus8 = 1.00117176e-08f;  // bf16(1e-8)
 constexpr float kRcp7 = 0.142857149f;               // RN(1/7)
-constexpr float kMagic8 = 12582920.0f;              // 1.5 * 2^23 + 8
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ f32x4 ld16f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
-// Smooth 8 bf16 values (one dword quad) by s with the reciprocal-corrected division;
-// exact IEEE division where the caller asks for it (element out of the fast path's range).
-template <bool PER_ELEMENT_GUARD>
-__device__ __forceinline__ uint32_t smooth_pair(uint32_t d, float s0, float r0, float s1, float r1,
-                                                bool exact) {
-  const float a = bf16lo(d), b = bf16hi(d);
-  float qa, qb;
-  if (exact) {
-    qa = a / s0;
-    qb = b / s1;
-  } else {
-    qa = div_rcp(a, s0, r0);
-    qb = div_rcp(b, s1, r1);
-    if (PER_ELEMENT_GUARD) {
-      if (!(fabsf(qa) >= 0x1p-90f && fabsf(qa) <= 0x1p100f) && a != 0.0f) qa = a / s0;
-      if (!(fabsf(qb) >= 0x1p-90f && fabsf(qb) <= 0x1p100f) && b != 0.0f) qb = b / s1;
-      qa = __builtin_copysignf(qa, a * s0);
-      qb = __builtin_copysignf(qb, b * s1);
+// x_hat = bf16(x / s) for the lane's row over 64 columns (8 chunks of 8), plus its absmax.
+// EXACT selects IEEE division; otherwise the reciprocal-corrected division (div_rcp), exact
+// while quotients are normal floats.  `range_bad` flags a nonzero x whose quotient left
+// [2^-90, 2^100].  SIGNED_ZERO restores the sign of a zero quotient (-0 / s), which the
+// correction step loses; only x_hat itself needs it.
+// The scale vectors are read through the constant address space: they are read-only while
+// the kernel runs, the addresses are wave-uniform, so they become scalar loads and SGPR
+// operands instead of per-lane vector loads.
+typedef const __attribute__((address_space(4))) float* cfloat_ptr;
+
+template <bool EXACT, bool SIGNED_ZERO>
+__device__ __forceinline__ void smooth64(const u32x4 (&xr)[8], cfloat_ptr sv, cfloat_ptr rv, u32x4 (&xh)[8],
+                                         float& am, bool& range_bad) {
+  bool bad = false;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t d = xr[c][e];
+      const float s0 = sv[8 * c + 2 * e], s1 = sv[8 * c + 2 * e + 1];
+      const float xa = bf16lo(d), xb = bf16hi(d);
+      float qa, qb;
+      if (EXACT) {
+        qa = xa / s0;
+        qb = xb / s1;
+      } else {
+        qa = div_rcp(xa, s0, rv[8 * c + 2 * e]);
+        qb = div_rcp(xb, s1, rv[8 * c + 2 * e + 1]);
+        const bool ba = !(fabsf(qa) >= 0x1p-90f && fabsf(qa) <= 0x1p100f) && xa != 0.0f;
+        const bool bb = !(fabsf(qb) >= 0x1p-90f && fabsf(qb) <= 0x1p100f) && xb != 0.0f;
+        bad = bad || ba || bb;
+        if (SIGNED_ZERO) {
+          qa = __builtin_copysignf(qa, __uint_as_float(__float_as_uint(xa) ^ (__float_as_uint(s0) & 0x80000000u)));
+          qb = __builtin_copysignf(qb, __uint_as_float(__float_as_uint(xb) ^ (__float_as_uint(s1) & 0x80000000u)));
+        }
+      }
+      const uint32_t pk = pack_bf16x2(qa, qb);
+      xh[c][e] = pk;
+      am = fmaxf(am, fmaxf(fabsf(bf16lo(pk)), fabsf(bf16hi(pk))));
     }
   }
-  return pack_bf16x2(qa, qb);
+  range_bad = bad;
 }
 
-template <int G, int NT, bool QUANT, bool XHAT>
+// OPER: GEMM operand codes written (0 none, 1 e4m3, 2 int8 16*q).
+template <int G, int NT, int OPER, bool XHAT>
 __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
-  constexpr int HALF = G / 2;   // columns of a group held by one lane
-  constexpr int CH = G / 16;    // 8-column chunks per lane per group == MFMA K=16 slices
-  __shared__ float red[4][64 * 32];
-  __shared__ int s_last;
+  constexpr int HB = G / 64;             // 64-column blocks per group
+  constexpr bool QUANT = OPER != 0;
+  constexpr int TR_MIN = 1;                // at least one low-rank tile; more tiles may be LoRA
+  __shared__ __attribute__((aligned(16))) float red[4 * 64 * 32];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6, h = lane >> 5, lr = lane & 31;
+  const int lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m0 = blockIdx.x * 64;
-  const int row[2] = {m0 + lr, m0 + 32 + lr};
-  const bool rok[2] = {row[0] < p.M, row[1] < p.M};
+  const int row = m0 + lane;
+  const bool rok = row < p.M;
+  const long rowc = min(row, p.M - 1);   // rows past M read row M-1; never stored
   const int K = p.K;
   const int ngroups = K / G;
   const int gb = blockIdx.y * p.gps;
   const int ge = min(ngroups, gb + p.gps);
   const int TR = (p.r + 31) >> 5;
-  const float* __restrict__ sv = p.srs;
-  const float* __restrict__ rv = p.srs + K;
+  const cfloat_ptr sv = (cfloat_ptr)p.srs;
+  const cfloat_ptr rv = (cfloat_ptr)(p.srs + K);
 
   f32x16 acc[2][NT];
 #pragma unroll
@@ -78,118 +105,134 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
     for (int t = 0; t < NT; ++t) acc[a][t] = f32x16{};
 
   for (int g = gb + wave; g < ge; g += 4) {
-    const int kb = g * G + h * HALF;
-    u32x4 xr[2][CH], xh[2][CH];
+    u32x4 xr[HB][8], xh[HB][8];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int b = 0; b < HB; ++b)
 #pragma unroll
-      for (int c = 0; c < CH; ++c)
-        xr[a][c] = rok[a] ? ld16(p.x + (long)row[a] * p.ldx + kb + 8 * c) : u32x4{};
+      for (int c = 0; c < 8; ++c) xr[b][c] = ld16(p.x + rowc * p.ldx + g * G + 64 * b + 8 * c);
 
-    // ---- smoothing: x_hat = bf16(x / s) ----
-    auto smooth_all = [&](bool exact) {
+    float am = 0.0f;
+    bool bad = false;
 #pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const f32x4 s0 = ld16f(sv + kb + 8 * c), s1 = ld16f(sv + kb + 8 * c + 4);
-        const f32x4 r0 = ld16f(rv + kb + 8 * c), r1 = ld16f(rv + kb + 8 * c + 4);
-        const float s8[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-        const float r8[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+    for (int b = 0; b < HB; ++b) {
+      bool bb;
+      smooth64<false, XHAT>(xr[b], sv + g * G + 64 * b, rv + g * G + 64 * b, xh[b], am, bb);
+      bad = bad || bb;
+    }
+    // Codes and scales only depend on elements within 2^-4 of the group absmax, so an absmax
+    // inside [2^-90, 2^100] keeps them exact; x_hat itself needs every element.
+    if (!XHAT) bad = am != 0.0f && !(am >= 0x1p-90f && am <= 0x1p100f);
+    if (p.exact || __any(bad)) {
+      am = 0.0f;
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            xh[a][c][e] = smooth_pair<XHAT>(xr[a][c][e], s8[2 * e], r8[2 * e], s8[2 * e + 1],
-                                            r8[2 * e + 1], exact);
+      for (int b = 0; b < HB; ++b) {
+        bool unused;
+        smooth64<true, XHAT>(xr[b], sv + g * G + 64 * b, rv + g * G + 64 * b, xh[b], am, unused);
       }
-    };
-    smooth_all(p.exact != 0);
+    }
 
     if (QUANT) {
-      float am[2];
+      const float sc = round_bf16(div_rcp(fmaxf(am, kBf16OneEMinus8), 7.0f, kRcp7));
+      const float rsc = 1.0f / sc;
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        float m = 0.0f;
+      for (int b = 0; b < HB; ++b) {
+        u32x4 op[4];
+        uint32_t nib[8];
 #pragma unroll
-        for (int c = 0; c < CH; ++c)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            m = fmaxf(m, fmaxf(fabsf(bf16lo(xh[a][c][e])), fabsf(bf16hi(xh[a][c][e]))));
-        am[a] = fmaxf(m, __shfl_xor(m, 32));
-      }
-      // The reciprocal division is exact while quotients stay normal; a group whose
-      // absmax leaves [2^-90, 2^100] is recomputed with IEEE division.
-      const bool bad0 = am[0] != 0.0f && !(am[0] >= 0x1p-90f && am[0] <= 0x1p100f);
-      const bool bad1 = am[1] != 0.0f && !(am[1] >= 0x1p-90f && am[1] <= 0x1p100f);
-      if (!p.exact && (bad0 || bad1)) {
-        smooth_all(true);
-#pragma unroll
-        for (int a = 0; a < 2; ++a) {
-          float m = 0.0f;
-#pragma unroll
-          for (int c = 0; c < CH; ++c)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              m = fmaxf(m, fmaxf(fabsf(bf16lo(xh[a][c][e])), fabsf(bf16hi(xh[a][c][e]))));
-          am[a] = fmaxf(m, __shfl_xor(m, 32));
-        }
-      }
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        const float sc = round_bf16(div_rcp(fmaxf(am[a], kBf16OneEMinus8), 7.0f, kRcp7));
-        const float rsc = 1.0f / sc;
-        uint32_t codes[CH];
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-          uint32_t w = 0;
+        for (int c = 0; c < 8; ++c) {
+          float t[8];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            float ta = div_rcp(bf16lo(xh[a][c][e]), sc, rsc);
-            float tb = div_rcp(bf16hi(xh[a][c][e]), sc, rsc);
-            ta = fminf(fmaxf(ta, -8.0f), 7.0f) + kMagic8;
-            tb = fminf(fmaxf(tb, -8.0f), 7.0f) + kMagic8;
-            w |= (__float_as_uint(ta) & 0xFu) << (8 * e);
-            w |= (__float_as_uint(tb) & 0xFu) << (8 * e + 4);
+            // rint, then +0 turns -0 into +0 (canonical code bytes)
+            t[2 * e] = __builtin_rintf(div_rcp(bf16lo(xh[b][c][e]), sc, rsc)) + 0.0f;
+            t[2 * e + 1] = __builtin_rintf(div_rcp(bf16hi(xh[b][c][e]), sc, rsc)) + 0.0f;
           }
-          codes[c] = w;
-        }
-        if (rok[a]) {
-          uint8_t* dst = p.qx + (long)row[a] * (K / 2) + kb / 2;
+          if (OPER == 1) {
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+                t[4], t[6], __builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[2], 0, false), true);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+                t[5], t[7], __builtin_amdgcn_cvt_pk_fp8_f32(t[1], t[3], 0, false), true);
+            op[c >> 1][2 * (c & 1)] = lo;
+            op[c >> 1][2 * (c & 1) + 1] = hi;
+          }
+          if (OPER == 2 || p.qx) {
+            uint32_t w = 0;
 #pragma unroll
-          for (int c = 0; c < CH; c += 4)
-            *reinterpret_cast<u32x4*>(dst + 4 * c) = u32x4{codes[c], codes[c + 1], codes[c + 2], codes[c + 3]};
-          if (h == 0) p.sx[(long)row[a] * ngroups + g] = (uint16_t)(__float_as_uint(sc) >> 16);
+            for (int e = 0; e < 8; ++e) w |= (uint32_t)((int)t[e] + 8) << (4 * e);
+            nib[c] = w;
+            if (OPER == 2) {
+              uint32_t lo, hi;
+              nib8_to_i8x16(w, lo, hi);
+              op[c >> 1][2 * (c & 1)] = lo;
+              op[c >> 1][2 * (c & 1) + 1] = hi;
+            }
+          }
+        }
+        if (rok) {
+          uint8_t* od = p.qa + rowc * K + g * G + 64 * b;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(od + 16 * q) = op[q];
+          if (p.qx) {
+            uint8_t* dst = p.qx + rowc * (K / 2) + (g * G + 64 * b) / 2;
+            *reinterpret_cast<u32x4*>(dst) = u32x4{nib[0], nib[1], nib[2], nib[3]};
+            *reinterpret_cast<u32x4*>(dst + 16) = u32x4{nib[4], nib[5], nib[6], nib[7]};
+          }
         }
       }
+      if (rok) p.sx[rowc * ngroups + g] = (uint16_t)(__float_as_uint(sc) >> 16);
     }
-    if (XHAT) {
+    if (XHAT && rok) {
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
-        if (rok[a])
+      for (int b = 0; b < HB; ++b)
 #pragma unroll
-          for (int c = 0; c < CH; ++c)
-            *reinterpret_cast<u32x4*>(p.xhat + (long)row[a] * p.ldxh + kb + 8 * c) = xh[a][c];
+        for (int c = 0; c < 8; ++c)
+          *reinterpret_cast<u32x4*>(p.xhat + rowc * p.ldxh + g * G + 64 * b + 8 * c) = xh[b][c];
     }
 
-    // ---- low-rank down (x_hat @ L2^T) and LoRA down (x @ A^T) on MFMA ----
+    // ---- low-rank down (x_hat @ L2^T) and LoRA down (x @ A^T) on MFMA, per 64 columns ----
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const bool is_l2 = t < TR;
-      const int n = is_l2 ? 32 * t + lr : 32 * (t - TR) + lr;
-      const bool nok = is_l2 ? n < p.r : n < p.rl;
-      const uint16_t* bsrc = is_l2 ? p.l2 : p.lora;
+    for (int b = 0; b < HB; ++b) {
+      // fa[i][c]: A operand of row tile i (rows 32i..32i+31) for the 16-column slice c
+      u32x4 fa[2][4], fx[2][4];
 #pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const u32x4 b = nok ? ld16(bsrc + (long)n * K + kb + 8 * c) : u32x4{};
+      for (int c = 0; c < 4; ++c) {
 #pragma unroll
-        for (int a = 0; a < 2; ++a) acc[a][t] = mfma_bf16_32x32x16(is_l2 ? xh[a][c] : xr[a][c], b, acc[a][t]);
+        for (int d = 0; d < 4; ++d) {
+          uint32_t v0 = xh[b][2 * c][d], v1 = xh[b][2 * c + 1][d];
+          permlane32_swap(v0, v1);
+          fa[0][c][d] = v0;
+          fa[1][c][d] = v1;
+          if (NT > TR_MIN) {
+            uint32_t w0 = xr[b][2 * c][d], w1 = xr[b][2 * c + 1][d];
+            permlane32_swap(w0, w1);
+            fx[0][c][d] = w0;
+            fx[1][c][d] = w1;
+          }
+        }
+      }
+      const int kb = g * G + 64 * b;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const bool is_l2 = t < TR;
+        const int n = is_l2 ? 32 * t + lr : 32 * (t - TR) + lr;
+        const int nmax = is_l2 ? p.r : p.rl;
+        const uint16_t* bsrc = (is_l2 ? p.l2 : p.lora) + (long)min(n, nmax - 1) * K + kb + 8 * h;
+        const bool nok = n < nmax;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          u32x4 bf = ld16(bsrc + 16 * c);
+          if (!nok) bf = u32x4{};
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            acc[i][t] = mfma_bf16_32x32x16(is_l2 ? fa[i][c] : fx[i][c], bf, acc[i][t]);
+        }
       }
     }
   }
 
   // ---- reduce the 4 waves (fixed order) and write this split's partial ----
-  const int S = gridDim.y;
   const int RTp = p.RTp;
-  float* dst = (S == 1) ? p.mid : p.midp + (long)blockIdx.y * p.M * RTp;
+  float* dst = p.mid + (long)blockIdx.y * p.M * RTp;
   const int nval = p.r + p.rl;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -197,7 +240,7 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        red[wave][(32 * a + 8 * (i >> 2) + 4 * h + (i & 3)) * 32 + lr] = acc[a][t][i];
+        red[wave * 2048 + (32 * a + 8 * (i >> 2) + 4 * h + (i & 3)) * 32 + lr] = acc[a][t][i];
     __syncthreads();
     const bool is_l2 = t < TR;
 #pragma unroll
@@ -208,7 +251,7 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
       const int j = is_l2 ? 32 * t + cc : 32 * (t - TR) + cc;
       const bool ok = is_l2 ? j < p.r : j < p.rl;
       if (grow < p.M && ok) {
-        float v = ((red[0][idx] + red[1][idx]) + red[2][idx]) + red[3][idx];
+        float v = ((red[idx] + red[2048 + idx]) + red[4096 + idx]) + red[6144 + idx];
         if (!is_l2) v *= p.lora_mult[j];
         dst[(long)grow * RTp + (is_l2 ? j : p.r + j)] = v;
       }
@@ -221,23 +264,6 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
     if (grow < p.M) dst[(long)grow * RTp + nval + idx % npad] = 0.0f;
   }
 
-  if (S > 1) {
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(p.counters + blockIdx.x, 1) == S - 1);
-    __syncthreads();
-    if (s_last) {
-      __threadfence();
-      for (int idx = tid; idx < 64 * RTp; idx += 256) {
-        const int grow = m0 + idx / RTp, cc = idx % RTp;
-        if (grow >= p.M) continue;
-        float v = 0.0f;
-        for (int s = 0; s < S; ++s) v += p.midp[((long)s * p.M + grow) * RTp + cc];
-        p.mid[(long)grow * RTp + cc] = v;
-      }
-      if (tid == 0) atomicExch(p.counters + blockIdx.x, 0);
-    }
-  }
 }
 
 // (s, RN(1/s)) in float32 for a bf16 smoothing vector: computed once per layer.
@@ -250,23 +276,24 @@ __global__ void prepare_smooth_kernel(const uint16_t* __restrict__ s, float* __r
   }
 }
 
-template <int G, bool QUANT, bool XHAT>
+template <int G, int OPER, bool XHAT>
 hipError_t launch_act_nt(const ActParams& p, int nt, dim3 grid, hipStream_t st) {
   switch (nt) {
-    case 1: act_kernel<G, 1, QUANT, XHAT><<<grid, 256, 0, st>>>(p); break;
-    case 2: act_kernel<G, 2, QUANT, XHAT><<<grid, 256, 0, st>>>(p); break;
-    case 3: act_kernel<G, 3, QUANT, XHAT><<<grid, 256, 0, st>>>(p); break;
-    case 4: act_kernel<G, 4, QUANT, XHAT><<<grid, 256, 0, st>>>(p); break;
+    case 1: act_kernel<G, 1, OPER, XHAT><<<grid, 256, 0, st>>>(p); break;
+    case 2: act_kernel<G, 2, OPER, XHAT><<<grid, 256, 0, st>>>(p); break;
+    case 3: act_kernel<G, 3, OPER, XHAT><<<grid, 256, 0, st>>>(p); break;
+    case 4: act_kernel<G, 4, OPER, XHAT><<<grid, 256, 0, st>>>(p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 template <int G>
-hipError_t launch_act_g(const ActParams& p, int nt, bool quant, bool xhat, dim3 grid, hipStream_t st) {
-  if (quant && xhat) return launch_act_nt<G, true, true>(p, nt, grid, st);
-  if (quant) return launch_act_nt<G, true, false>(p, nt, grid, st);
-  if (xhat) return launch_act_nt<G, false, true>(p, nt, grid, st);
+hipError_t launch_act_g(const ActParams& p, int nt, int oper, bool xhat, dim3 grid, hipStream_t st) {
+  if (oper == 1 && !xhat) return launch_act_nt<G, 1, false>(p, nt, grid, st);
+  if (oper == 1 && xhat) return launch_act_nt<G, 1, true>(p, nt, grid, st);
+  if (oper == 2 && !xhat) return launch_act_nt<G, 2, false>(p, nt, grid, st);
+  if (oper == 0 && xhat) return launch_act_nt<G, 0, true>(p, nt, grid, st);
   return hipErrorInvalidValue;
 }
 
@@ -282,10 +309,10 @@ int act_splits(int M, int K, int G) {
   return s;
 }
 
-hipError_t launch_act(const ActParams& p, int G, int nt, bool quant, bool xhat, int splits, hipStream_t st) {
+hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, int splits, hipStream_t st) {
   dim3 grid((p.M + 63) / 64, splits);
-  if (G == 64) return launch_act_g<64>(p, nt, quant, xhat, grid, st);
-  if (G == 128) return launch_act_g<128>(p, nt, quant, xhat, grid, st);
+  if (G == 64) return launch_act_g<64>(p, nt, oper, xhat, grid, st);
+  if (G == 128) return launch_act_g<128>(p, nt, oper, xhat, grid, st);
   return hipErrorInvalidValue;
 }
 

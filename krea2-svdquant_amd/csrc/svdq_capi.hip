@@ -58,44 +58,47 @@ int svdq_prepare_smooth(const void* smooth, float* srs, int K, hipStream_t strea
                   "prepare_smooth");
 }
 
-int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int64_t* midp_floats,
-                             int64_t* counter_ints) {
+int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int64_t* mid_floats) {
   if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant_workspace: M=%d", M);
   if (int e = check_group(group, K)) return e;
   if (RTp <= 0 || RTp % 32) return fail(SVDQ_ERR_SHAPE, "RTp=%d must be a positive multiple of 32", RTp);
   const int s = svdq::act_splits(M, K, group);
   if (splits) *splits = s;
-  if (midp_floats) *midp_floats = s > 1 ? (int64_t)s * M * RTp : 0;
-  if (counter_ints) *counter_ints = (M + 63) / 64;
+  if (mid_floats) *mid_floats = (int64_t)s * M * RTp;
   return ok();
 }
 
 int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
                    const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
-                   int RTp, unsigned flags, void* qx, void* sx, void* xhat, int64_t ldxh, float* mid,
-                   float* midp, int* counters, int splits, hipStream_t stream) {
-  const bool quant = flags & SVDQ_ACT_QUANT, want_xhat = flags & SVDQ_ACT_XHAT;
-  if (flags & ~(unsigned)(SVDQ_ACT_QUANT | SVDQ_ACT_XHAT | SVDQ_ACT_EXACT_DIV))
-    return fail(SVDQ_ERR_ARG, "act_quant: unknown flags 0x%x", flags);
-  if (!quant && !want_xhat) return fail(SVDQ_ERR_ARG, "act_quant: neither QUANT nor XHAT requested");
+                   int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
+                   float* mid, int splits, hipStream_t stream) {
+  const unsigned known = SVDQ_ACT_PACKED | SVDQ_ACT_XHAT | SVDQ_ACT_EXACT_DIV | SVDQ_ACT_OPERAND_E4M3 |
+                         SVDQ_ACT_OPERAND_I8;
+  if (flags & ~known) return fail(SVDQ_ERR_ARG, "act_quant: unknown flags 0x%x", flags);
+  const bool e4m3 = flags & SVDQ_ACT_OPERAND_E4M3, i8 = flags & SVDQ_ACT_OPERAND_I8;
+  const bool quant = e4m3 || i8, want_xhat = flags & SVDQ_ACT_XHAT, packed = flags & SVDQ_ACT_PACKED;
+  if (e4m3 && i8) return fail(SVDQ_ERR_ARG, "act_quant: two operand formats requested");
+  if (!quant && !want_xhat) return fail(SVDQ_ERR_ARG, "act_quant: neither an operand format nor XHAT requested");
+  if (packed && !quant) return fail(SVDQ_ERR_ARG, "act_quant: PACKED needs an operand format");
+  if (i8 && want_xhat) return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: XHAT with int8 operands has no kernel");
   if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant: M=%d", M);
   if (int e = check_group(group, K)) return e;
   if (r < 1 || rl < 0) return fail(SVDQ_ERR_SHAPE, "act_quant: rank r=%d rl=%d", r, rl);
   if (RTp % 32 || RTp < r + rl) return fail(SVDQ_ERR_SHAPE, "act_quant: RTp=%d (r=%d rl=%d)", RTp, r, rl);
   const int nt = mid_tiles(r, rl);
   if (nt > 4) return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: ceil(r/32)+ceil(rl/32)=%d > 4", nt);
-  if (!x || !srs || !l2 || !mid || (rl > 0 && (!lora_down || !lora_mult)) || (quant && (!qx || !sx)) ||
-      (want_xhat && !xhat))
+  if (!x || !srs || !l2 || !mid || (rl > 0 && (!lora_down || !lora_mult)) || (quant && (!qa || !sx)) ||
+      (packed && !qx) || (want_xhat && !xhat))
     return fail(SVDQ_ERR_ARG, "act_quant: null pointer");
   if (ldx < K || ldx % 8 || (want_xhat && (ldxh < K || ldxh % 8)))
     return fail(SVDQ_ERR_ALIGN, "act_quant: ldx=%lld ldxh=%lld must be >= K and multiples of 8",
                 (long long)ldx, (long long)ldxh);
   if (!aligned16(x) || !aligned16(srs) || !aligned16(l2) || !aligned16(mid) ||
-      (rl > 0 && !aligned16(lora_down)) || (quant && !aligned16(qx)) || (want_xhat && !aligned16(xhat)))
+      (rl > 0 && !aligned16(lora_down)) || (quant && !aligned16(qa)) || (packed && !aligned16(qx)) ||
+      (want_xhat && !aligned16(xhat)))
     return fail(SVDQ_ERR_ALIGN, "act_quant: device pointers must be 16-byte aligned");
   const int expect = svdq::act_splits(M, K, group);
   if (splits != expect) return fail(SVDQ_ERR_ARG, "act_quant: splits=%d, workspace says %d", splits, expect);
-  if (splits > 1 && (!midp || !counters)) return fail(SVDQ_ERR_ARG, "act_quant: split workspace missing");
 
   svdq::ActParams p{};
   p.x = static_cast<const uint16_t*>(x);
@@ -109,39 +112,42 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
   p.M = M;
   p.K = K;
   p.RTp = RTp;
-  p.qx = static_cast<uint8_t*>(qx);
+  p.qx = packed ? static_cast<uint8_t*>(qx) : nullptr;
+  p.qa = static_cast<uint8_t*>(qa);
   p.sx = static_cast<uint16_t*>(sx);
   p.xhat = static_cast<uint16_t*>(xhat);
   p.ldxh = ldxh;
   p.mid = mid;
-  p.midp = midp;
-  p.counters = counters;
   const int ngroups = K / group;
   p.gps = (ngroups + splits - 1) / splits;
   p.exact = (flags & SVDQ_ACT_EXACT_DIV) ? 1 : 0;
-  return launched(svdq::launch_act(p, group, nt, quant, want_xhat, splits, stream), "act_quant");
+  return launched(svdq::launch_act(p, group, nt, e4m3 ? 1 : (i8 ? 2 : 0), want_xhat, splits, stream),
+                  "act_quant");
 }
 
 static int gemm_common_checks(const char* who, const void* qw, const void* sw, const float* mid,
-                              const void* l1cat, int RTp, int M, int N, int K, int group, void* y,
-                              int64_t ldy, int out_f32) {
+                              int splits, const void* l1cat, int RTp, int M, int N, int K, int group,
+                              void* y, int64_t ldy, int out_f32) {
   if (M <= 0 || N <= 0) return fail(SVDQ_ERR_ARG, "%s: M=%d N=%d", who, M, N);
   if (int e = check_group(group, K)) return e;
   if (!qw || !sw || !mid || !l1cat || !y) return fail(SVDQ_ERR_ARG, "%s: null pointer", who);
   if (RTp <= 0 || RTp % 32) return fail(SVDQ_ERR_SHAPE, "%s: RTp=%d must be a positive multiple of 32", who, RTp);
+  if (splits < 1) return fail(SVDQ_ERR_ARG, "%s: splits=%d", who, splits);
   if (out_f32 != 0 && out_f32 != 1) return fail(SVDQ_ERR_ARG, "%s: out_f32=%d", who, out_f32);
   if (ldy < N) return fail(SVDQ_ERR_SHAPE, "%s: ldy=%lld < N=%d", who, (long long)ldy, N);
-  if (!aligned16(qw) || !aligned16(mid) || !aligned16(l1cat))
+  if (!aligned16(qw) || !aligned16(mid) || !aligned16(l1cat) || (K / 2) % 8)
     return fail(SVDQ_ERR_ALIGN, "%s: device pointers must be 16-byte aligned", who);
   return SVDQ_OK;
 }
 
-static svdq::GemmParams gemm_params(const void* qw, const void* sw, const float* mid, const void* l1cat,
-                                    int RTp, const void* bias, int M, int N, int K, void* y, int64_t ldy) {
+static svdq::GemmParams gemm_params(const void* qw, const void* sw, const float* mid, int splits,
+                                    const void* l1cat, int RTp, const void* bias, int M, int N, int K, void* y,
+                                    int64_t ldy) {
   svdq::GemmParams p{};
   p.qw = static_cast<const uint8_t*>(qw);
   p.sw = static_cast<const uint16_t*>(sw);
   p.mid = mid;
+  p.splits = splits;
   p.l1cat = static_cast<const uint16_t*>(l1cat);
   p.RTp = RTp;
   p.bias = static_cast<const uint16_t*>(bias);
@@ -153,26 +159,46 @@ static svdq::GemmParams gemm_params(const void* qw, const void* sw, const float*
   return p;
 }
 
-int svdq_w4a4_gemm(const void* qx, const void* sx, const void* qw, const void* sw, const float* mid,
-                   const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
-                   void* y, int64_t ldy, int out_f32, hipStream_t stream) {
-  if (int e = gemm_common_checks("w4a4_gemm", qw, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32)) return e;
-  if (!qx || !sx) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
-  if (!aligned16(qx)) return fail(SVDQ_ERR_ALIGN, "w4a4_gemm: qx must be 16-byte aligned");
-  svdq::GemmParams p = gemm_params(qw, sw, mid, l1cat, RTp, bias, M, N, K, y, ldy);
-  p.qx = static_cast<const uint8_t*>(qx);
+int svdq_prepare_weight_scales(const void* sw, void* swp, int64_t count, int operand, hipStream_t stream) {
+  if (!sw || !swp) return fail(SVDQ_ERR_ARG, "prepare_weight_scales: null pointer");
+  if (count <= 0) return fail(SVDQ_ERR_ARG, "prepare_weight_scales: count=%lld", (long long)count);
+  if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
+    return fail(SVDQ_ERR_ARG, "prepare_weight_scales: operand format %d", operand);
+  return launched(svdq::launch_weight_scale_pairs(static_cast<const uint16_t*>(sw), static_cast<uint32_t*>(swp),
+                                                  (long)count, operand, stream),
+                  "prepare_weight_scales");
+}
+
+int svdq_w4a4_gemm(const void* qa, int operand, const void* sx, const void* qw, const void* swp,
+                   const float* mid, int splits, const void* l1cat, int RTp, const void* bias, int M, int N,
+                   int K, int group, void* y, int64_t ldy, int out_f32, hipStream_t stream) {
+  const void* sw = swp;
+  if (int e = gemm_common_checks("w4a4_gemm", qw, sw, mid, splits, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
+    return e;
+  if (!qa || !sx) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
+  if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
+    return fail(SVDQ_ERR_ARG, "w4a4_gemm: operand format %d", operand);
+  if (!aligned16(qa)) return fail(SVDQ_ERR_ALIGN, "w4a4_gemm: qa must be 16-byte aligned");
+  // The kernel addresses qa and qw with 32-bit byte offsets.
+  if ((int64_t)M * K > INT32_MAX || (int64_t)N * (K / 2) > INT32_MAX)
+    return fail(SVDQ_ERR_SHAPE, "w4a4_gemm: M*K=%lld or N*K/2=%lld exceeds 2^31-1 bytes; split the call",
+                (long long)M * K, (long long)N * (K / 2));
+  svdq::GemmParams p = gemm_params(qw, sw, mid, splits, l1cat, RTp, bias, M, N, K, y, ldy);
+  p.qa = static_cast<const uint8_t*>(qa);
   p.sx = static_cast<const uint16_t*>(sx);
-  return launched(svdq::launch_w4a4(p, group, out_f32 == 1, stream), "w4a4_gemm");
+  p.swp = static_cast<const uint32_t*>(swp);
+  return launched(svdq::launch_w4a4(p, group, operand, out_f32 == 1, stream), "w4a4_gemm");
 }
 
 int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const float* mid,
-                    const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                    int splits, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
                     void* y, int64_t ldy, int out_f32, hipStream_t stream) {
-  if (int e = gemm_common_checks("w4a16_gemm", qw, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32)) return e;
+  if (int e = gemm_common_checks("w4a16_gemm", qw, sw, mid, splits, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
+    return e;
   if (!xhat) return fail(SVDQ_ERR_ARG, "w4a16_gemm: null pointer");
   if (ldxh < K || ldxh % 8 || !aligned16(xhat))
     return fail(SVDQ_ERR_ALIGN, "w4a16_gemm: xhat must be 16-byte aligned with ldxh >= K, ldxh %% 8 == 0");
-  svdq::GemmParams p = gemm_params(qw, sw, mid, l1cat, RTp, bias, M, N, K, y, ldy);
+  svdq::GemmParams p = gemm_params(qw, sw, mid, splits, l1cat, RTp, bias, M, N, K, y, ldy);
   p.xhat = static_cast<const uint16_t*>(xhat);
   p.ldxh = ldxh;
   return launched(svdq::launch_w4a16(p, group, out_f32 == 1, stream), "w4a16_gemm");

@@ -68,6 +68,50 @@ __device__ __forceinline__ f32x16 mfma_bf16_32x32x16(u32x4 a, u32x4 b, f32x16 c)
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+__device__ __forceinline__ f32x16 mfma_fp8_32x32x64(const u32x4 (&a)[2], const u32x4 (&b)[2], f32x16 c) {
+  typedef int i32x8 __attribute__((ext_vector_type(8)));
+  const i32x8 av = {(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3],
+                    (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]};
+  const i32x8 bv = {(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3],
+                    (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]};
+  // format 0/0 = e4m3 x e4m3; E8M0 scale 127 = 2^0 on both sides
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
+}
+
+// ---- INT4 code conversion (8-bit MFMA operands) ---------------------------------
+// Both operands of the W4A4 GEMM are 8-bit per element in LDS.  A packed dword holds 8
+// offset-binary nibbles u = q + 8 for k0..k7 (k0 in the low nibble); it becomes two
+// dwords [k0,k2,k4,k6] and [k1,k3,k5,k7].  The activation pass writes its operand bytes in
+// the same order, so the k permutation cancels in the dot product.
+//
+// e4m3 (OCP, bias 7) holds every q in [-8, 7] exactly.  v_perm_b32 is a byte table
+// lookup over 8 bytes; two tables (u < 8: q = u - 8 < 0, u >= 8: q = u - 8 >= 0) and a
+// per-byte select on bit 3 of u cover all 16 codes.
+__device__ __forceinline__ uint32_t nib4_to_e4m3(uint32_t u) {
+  const uint32_t j = u & 0x07070707u;
+  const uint32_t pos = __builtin_amdgcn_perm(0x4e4c4a48u, 0x44403800u, j);  // q = 0..7
+  const uint32_t neg = __builtin_amdgcn_perm(0xb8c0c4c8u, 0xcaccced0u, j);  // q = -8..-1
+  const uint32_t mask = __builtin_amdgcn_perm(0u, 0u, ((u >> 3) & 0x01010101u) | 0x0c0c0c0cu);
+  return (pos & mask) | (neg & ~mask);
+}
+__device__ __forceinline__ void nib8_to_e4m3(uint32_t x, uint32_t& lo, uint32_t& hi) {
+  lo = nib4_to_e4m3(x);
+  hi = nib4_to_e4m3(x >> 4);
+}
+// Same bytes as int8 16*q (two's complement nibble moved to the high half of the byte).
+__device__ __forceinline__ void nib8_to_i8x16(uint32_t x, uint32_t& lo, uint32_t& hi) {
+  const uint32_t t = x ^ 0x88888888u;
+  lo = (t << 4) & 0xF0F0F0F0u;
+  hi = t & 0xF0F0F0F0u;
+}
+
+// gfx950 v_permlane32_swap: exchange lanes 32..63 of `a` with lanes 0..31 of `b`.
+__device__ __forceinline__ void permlane32_swap(uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
+}
+
 // Split 8 floats into bf16 hi + bf16 lo parts (x ~= hi + lo to ~2^-17 relative).
 __device__ __forceinline__ void split_hi_lo(const float* v, u32x4& hi, u32x4& lo) {
 #pragma unroll

@@ -2,21 +2,17 @@
 //
 // W4A4 (replaces the residual GEMM of quant/svd.py:158 with activation codes, and the
 // low-rank add of kernels/triton/generic_int4.py:84-133):
-//   y[m,n] = sum_g sx[m,g] sw[n,g] sum_{k in g} qx[m,k] qw[n,k]      (INT8 MFMA, exact int32
-//            per group, rescaled into an fp32 accumulator)
+//   y[m,n] = sum_g sx[m,g] sw[n,g] sum_{k in g} qx[m,k] qw[n,k]      (exact integer group sums
+//            on the FP8 (e4m3) or INT8 MFMA, rescaled into an fp32 accumulator)
 //          + mid[m,:] . l1cat[n,:]  + bias[n]                       (bf16 MFMA, mid split
 //                                                                    into bf16 hi + lo)
 // W4A16 (the pytorch_sim math, quant/svd.py:119-163):
 //   y = x_hat @ W^T with W = bf16(q * bf16(sw)) dequantized in registers while staging the
 //   tile into LDS (pack.py:26-44 with dtype=bf16), same epilogue.
 //
-// Tiling: 128x128 block tile, 4 waves in a 2x2 grid, each wave a 64x64 tile = 2x2 MFMA
-// 32x32 sub-tiles; one K-group per pipeline stage, LDS double buffered: the next stage's
-// global loads are issued before the current stage's MFMAs and written to the other LDS
-// buffer afterwards.  Packed INT4 is unpacked to int8 while staging: the nibbles of a dword
-// are XORed with 8 (offset binary -> two's complement) and moved to the high half of each
-// byte, i.e. the MFMA sees 16*q, and the 1/256 is folded into the weight scale.  This
-// also permutes k inside each 8-element chunk (even k first); A and B are permuted alike.
+// Both kernels permute k inside each chunk of 8 columns (even k first) when they unpack
+// INT4 nibbles; the activation operand is written in the same order, so the permutation
+// cancels in every dot product.
 #include "svdq_common.h"
 #include "svdq_kernels.h"
 
@@ -28,31 +24,33 @@ constexpr int BM = 128, BN = 128, NTHR = 256;
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
-// acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store.
+
+
+// acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store.  mid holds one
+// partial per K split of the activation pass; they are added here in split order.
 template <bool OUT_F32>
 __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2], int m0, int n0,
                                          int lr, int h) {
+  const long split_stride = (long)p.M * p.RTp;
   for (int s = 0; s < p.RTp / 16; ++s) {
     u32x4 ahi[2], alo[2], b[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int m = m0 + 32 * i + lr;
-      float v[8];
-      if (m < p.M) {
-        const f32x4 v0 = *reinterpret_cast<const f32x4*>(p.mid + (long)m * p.RTp + 16 * s + 8 * h);
-        const f32x4 v1 = *reinterpret_cast<const f32x4*>(p.mid + (long)m * p.RTp + 16 * s + 8 * h + 4);
-        v[0] = v0[0]; v[1] = v0[1]; v[2] = v0[2]; v[3] = v0[3];
-        v[4] = v1[0]; v[5] = v1[1]; v[6] = v1[2]; v[7] = v1[3];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+      const int m = min(m0 + 32 * i + lr, p.M - 1);
+      const float* src = p.mid + (long)m * p.RTp + 16 * s + 8 * h;
+      f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
+      f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
+      for (int sp = 1; sp < p.splits; ++sp) {
+        v0 += *reinterpret_cast<const f32x4*>(src + sp * split_stride);
+        v1 += *reinterpret_cast<const f32x4*>(src + sp * split_stride + 4);
       }
+      const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
       split_hi_lo(v, ahi[i], alo[i]);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int n = n0 + 32 * j + lr;
-      b[j] = n < p.N ? ld16(p.l1cat + (long)n * p.RTp + 16 * s + 8 * h) : u32x4{};
+      const int n = min(n0 + 32 * j + lr, p.N - 1);
+      b[j] = ld16(p.l1cat + (long)n * p.RTp + 16 * s + 8 * h);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -83,71 +81,145 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
 }
 
 // --------------------------------------------------------------------------- W4A4
-template <int G, bool OUT_F32>
-__global__ void __launch_bounds__(NTHR) w4a4_kernel(GemmParams p) {
-  constexpr int ROWB = G + 16;               // LDS bytes per row of unpacked int8 (padded)
-  constexpr int LPR = G / 32;                // 16-byte packed loads per row per stage
-  constexpr int LPT = BM * LPR / NTHR;       // packed loads per thread per operand
-  constexpr int KS = G / 32;                 // K=32 MFMA steps per group
-  __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * ROWB];
-  __shared__ __attribute__((aligned(16))) int8_t sB[2][BN * ROWB];
-  __shared__ __attribute__((aligned(16))) float sSX[2][BM];
-  __shared__ __attribute__((aligned(16))) float sSW[2][BN];
+// Block tile 256x128, 8 waves in a 4x2 grid (64x64 per wave = 2x2 MFMA 32x32 tiles), one
+// K-group per stage.  Per group and output element the accumulator update is one FMA,
+// acc += P * S, where P is the exact group dot product from the 8-bit MFMA and S = sx * sw
+// comes from a bf16 MFMA whose K=2 operand pairs are (sx, sx) and (bf16 hi, bf16 lo) of the
+// fp16 weight scale, i.e. the scale product is exact too.
+//   MODE 0: operands e4m3, v_mfma_f32_32x32x64_f8f6f4 (P already float32);
+//   MODE 1: operands int8 16*q, 2x v_mfma_i32_32x32x32_i8 (P int32, converted; 1/256 in S).
+// Operand A (activation codes, 8-bit) comes from the activation pass; operand B is the
+// packed INT4 weight, converted while staging into LDS.  Global loads run two groups ahead
+// in two register sets; LDS is double buffered.
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane L
+// of the wave writes LDS bytes [lds + 16 L, lds + 16 L + 16) from base + off.  Issued as
+// inline asm so that the compiler does not order every later LDS read after it (it cannot
+// tell the two LDS stages apart); the kernel waits for it explicitly before its barrier.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// W4A4 GEMM (FP8 or INT8 MFMA on exact integer codes).
+//
+// Block tile 256 x 128, 8 waves in a 4 x 2 grid, wave tile 64 x 64 = 2 x 2 sub-tiles of
+// 32 x 32.  K advances 128 columns per pipeline stage (two groups of 64 or one of 128), two
+// LDS stages.  Operand A (8-bit codes from the activation pass) goes global -> LDS by DMA;
+// operand B (packed INT4) goes through registers and is converted to 8-bit codes on the way.
+//
+// LDS operand tiles: rows of 128 bytes = 8 chunks of 16; chunk c of row r sits at chunk
+// position c ^ ((r >> 1) & 7).  The 16 lanes of a ds_read_b128 phase read one logical chunk
+// of 16 consecutive rows and hit 16 distinct 4-bank groups.
+//
+// Per group and sub-tile: P = codes_x . codes_w (exact integer sums, fp32) on the FP8 MFMA,
+// S = sx (x) sw on a bf16 MFMA with K = 2 ((sx, sx) . (hi(sw), lo(sw)) exact), acc += P * S.
+template <int G, int MODE, bool OUT_F32>
+__global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
+  constexpr int TBM = 256, TBN = 128, NT = 512;
+  constexpr int KB = 128;                     // K columns per pipeline stage
+  constexpr int GPS = KB / G;                 // groups per stage
+  constexpr int KS = G / 64;                  // 64-column MFMA steps per group
+  constexpr int ADMA = TBM * KB / (16 * NT);  // A: 16-byte DMA chunks per thread per stage (4)
+  constexpr int BCH = TBN * KB / (16 * NT);   // B: 16-column chunks per thread per stage (2)
+  constexpr int XS = TBM + 1, WS = TBN + 1;   // scale rows per group (+1 zero row)
+  static_assert(GPS * TBM <= NT && GPS * TBN <= NT, "one scale of each kind per thread");
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[2][TBM * KB];
+  __shared__ __attribute__((aligned(1024))) uint8_t sB[2][TBN * KB];
+  // Scale-MFMA operands, 4 words per row: (pair, 0, 0, 0); the last row is all zero.
+  __shared__ __attribute__((aligned(16))) uint32_t sX[2][GPS][XS * 4];   // pair = (sx, sx)
+  __shared__ __attribute__((aligned(16))) uint32_t sW[2][GPS][WS * 4];   // pair = (hi, lo) of sw
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, h = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
-  const int nbm = (p.M + BM - 1) / BM, nbn = (p.N + BN - 1) / BN;
+  const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
   int bm, bn;
-  tile_coords(blockIdx.x, nbm, nbn, 8, bm, bn);
-  const int m0 = bm * BM, n0 = bn * BN;
-  const int K = p.K, ngroups = K / G, kp = K / 2;
+  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
+  const int m0 = bm * TBM, n0 = bn * TBN;
+  const int K = p.K, ngroups = K / G, nstages = (K + KB - 1) / KB, kp = K / 2;
 
-  u32x4 ra[LPT], rb[LPT];
-  float xs = 0.0f, ws = 0.0f;
+  // A by DMA: wave w, chunk i covers LDS bytes [(ADMA w + i) KB, +1 KB) of the stage tile,
+  // i.e. 8 rows; lane L lands at row 8 (ADMA w + i) + L / 8, chunk position L % 8.  Columns
+  // past K (a last stage holding a single group of 64) are clamped to the row's last chunk;
+  // that group's scale is zero.  Offsets are 32-bit (the host bounds the operand sizes).
+  uint32_t aoff[ADMA];
+  int alim[ADMA];
+#pragma unroll
+  for (int i = 0; i < ADMA; ++i) {
+    const int row = 8 * (ADMA * wave + i) + lane / 8;
+    const int c = (lane % 8) ^ ((row >> 1) & 7);
+    aoff[i] = (uint32_t)min(m0 + row, p.M - 1) * (uint32_t)K + 16 * c;
+    alim[i] = K - 16 - 16 * c;
+  }
+  // B through registers (packed nibbles -> 8-bit codes): chunk index tid + NT i -> row, position.
+  uint32_t boff[BCH];
+  int blim[BCH], bdst[BCH];
+#pragma unroll
+  for (int i = 0; i < BCH; ++i) {
+    const int idx = tid + NT * i, row = idx / 8, pc = idx % 8, c = pc ^ ((row >> 1) & 7);
+    boff[i] = (uint32_t)min(n0 + row, p.N - 1) * (uint32_t)kp + 8 * c;
+    blim[i] = kp - 8 - 8 * c;
+    bdst[i] = row * 128 + 16 * pc;
+  }
+  // Scales: thread t stages sx of row t % TBM for group t / TBM of the stage and sw of
+  // column t % TBN for group t / TBN (threads past GPS * TBN load a duplicate, not stored).
+  const int xj = (tid / TBM) % GPS, xr = tid % TBM, wj = (tid / TBN) % GPS, wr = tid % TBN;
+  const uint32_t xoff = (uint32_t)min(m0 + xr, p.M - 1) * (uint32_t)ngroups;
+  const uint32_t woff = (uint32_t)min(n0 + wr, p.N - 1) * (uint32_t)ngroups;
+  const bool x_live = tid < GPS * TBM, w_live = tid < GPS * TBN;
+  // Zero the padding words 1-3 of every row and the whole last row, once (the pair words of
+  // rows < TBM / TBN are written every stage, by other threads: never touched here).
+  for (int t = tid; t < 2 * GPS * XS; t += NT) {
+    uint32_t* r = &sX[t / (GPS * XS)][(t / XS) % GPS][(t % XS) * 4];
+    if (t % XS == TBM) r[0] = 0u;
+    r[1] = 0u; r[2] = 0u; r[3] = 0u;
+  }
+  for (int t = tid; t < 2 * GPS * WS; t += NT) {
+    uint32_t* r = &sW[t / (GPS * WS)][(t / WS) % GPS][(t % WS) * 4];
+    if (t % WS == TBN) r[0] = 0u;
+    r[1] = 0u; r[2] = 0u; r[3] = 0u;
+  }
 
-  auto gload = [&](int g) {
+  // Fragment addresses (bytes within a stage tile): row base + the lane's chunk pair.
+  const int sw_ = (lr >> 1) & 7;
+  const int arow = (64 * wm + lr) * 128, brow = (64 * wn + lr) * 128;
+  // Scale-MFMA operand rows: lanes 32-63 (the second half of K) read the zero row.
+  const int xrow = h ? TBM : 64 * wm + lr, wrow = h ? TBN : 64 * wn + lr;
+
+  u32x2 rb[BCH];
+  uint32_t rx, rw;
+  int xg;
+  // Issue the loads of stage `s`: B and scales into registers, then A into LDS buffer `buf`.
+  // The DMA goes last: the compiler does not count it, so any wait it places for its own
+  // loads is ordered before the DMA and never waits for it.
+  auto gload = [&](int s, int buf) {
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int idx = tid + NTHR * i, row = idx / LPR, part = idx % LPR;
-      const int m = m0 + row, n = n0 + row;
-      const u32x4 zero8 = {0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
-      ra[i] = m < p.M ? ld16(p.qx + (long)m * kp + g * (G / 2) + 16 * part) : zero8;
-      rb[i] = n < p.N ? ld16(p.qw + (long)n * kp + g * (G / 2) + 16 * part) : zero8;
-    }
-    if (tid < BM) {
-      const int m = m0 + tid;
-      xs = m < p.M ? bf16f(p.sx[(long)m * ngroups + g]) : 0.0f;
-    } else {
-      const int n = n0 + tid - BM;
-      ws = n < p.N ? half_bits_to_float(p.sw[(long)n * ngroups + g]) * (1.0f / 256.0f) : 0.0f;
-    }
-  };
-  auto unpack16 = [](u32x4 v, u32x4& lo4, u32x4& hi4) {
-    // 8 nibbles per dword -> two dwords of int8 (16*q): [k0,k2,k4,k6], [k1,k3,k5,k7]
-    uint32_t o[8];
+    for (int i = 0; i < BCH; ++i)
+      rb[i] = *reinterpret_cast<const u32x2*>(p.qw + (boff[i] + (uint32_t)min(s * (KB / 2), blim[i])));
+    xg = s * GPS + xj;
+    rx = p.sx[xoff + (uint32_t)min(xg, ngroups - 1)];
+    rw = p.swp[woff + (uint32_t)min(s * GPS + wj, ngroups - 1)];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t t = v[d] ^ 0x88888888u;
-      o[2 * d] = (t << 4) & 0xF0F0F0F0u;
-      o[2 * d + 1] = t & 0xF0F0F0F0u;
-    }
-    lo4 = u32x4{o[0], o[1], o[2], o[3]};
-    hi4 = u32x4{o[4], o[5], o[6], o[7]};
+    for (int i = 0; i < ADMA; ++i)
+      dma16(p.qa, aoff[i] + (uint32_t)min(s * KB, alim[i]),
+            __builtin_amdgcn_readfirstlane(lds_offset(&sA[buf][(ADMA * wave + i) * 1024])));
   };
   auto lstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < LPT; ++i) {
-      const int idx = tid + NTHR * i, row = idx / LPR, part = idx % LPR;
-      u32x4 a0, a1, b0, b1;
-      unpack16(ra[i], a0, a1);
-      unpack16(rb[i], b0, b1);
-      st16(&sA[buf][row * ROWB + 32 * part], a0);
-      st16(&sA[buf][row * ROWB + 32 * part + 16], a1);
-      st16(&sB[buf][row * ROWB + 32 * part], b0);
-      st16(&sB[buf][row * ROWB + 32 * part + 16], b1);
+    for (int i = 0; i < BCH; ++i) {
+      uint32_t o0, o1, o2, o3;
+      if (MODE == 0) {
+        nib8_to_e4m3(rb[i][0], o0, o1);
+        nib8_to_e4m3(rb[i][1], o2, o3);
+      } else {
+        nib8_to_i8x16(rb[i][0], o0, o1);
+        nib8_to_i8x16(rb[i][1], o2, o3);
+      }
+      st16(&sB[buf][bdst[i]], u32x4{o0, o1, o2, o3});
     }
-    if (tid < BM) sSX[buf][tid] = xs;
-    else sSW[buf][tid - BM] = ws;
+    if (x_live) sX[buf][xj][4 * xr] = xg < ngroups ? rx * 0x10001u : 0u;
+    if (w_live) sW[buf][wj][4 * wr] = rw;
   };
 
   f32x16 acc[2][2];
@@ -156,52 +228,122 @@ __global__ void __launch_bounds__(NTHR) w4a4_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  gload(0);
+  // Operands of one group: A/B fragments of the wave's 2x2 sub-tiles and the scale-MFMA
+  // operands.
+  struct Frag {
+    u32x4 a[2][KS][2], b[2][KS][2];
+    u32x4 x[2], w[2];
+  };
+  auto read_frag = [&](Frag& f, int buf, int gi) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        // logical chunk c = G/16 gi + 4 ks + 2 h + t of the lane's rows, stored at c ^ sw_
+        const int pc = 16 * ((G / 16 * gi + 4 * ks + 2 * h + t) ^ sw_);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          f.a[i][ks][t] = ld16(&sA[buf][arow + 4096 * i + pc]);
+          f.b[i][ks][t] = ld16(&sB[buf][brow + 4096 * i + pc]);
+        }
+      }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      f.x[i] = ld16(&sX[buf][gi][4 * (xrow + (h ? 0 : 32 * i))]);
+      f.w[i] = ld16(&sW[buf][gi][4 * (wrow + (h ? 0 : 32 * i))]);
+    }
+  };
+  auto mfma_p = [&](const Frag& f, int i, int j) {
+    f32x16 pf;
+    if (MODE == 0) {
+      pf = mfma_fp8_32x32x64(f.a[i][0], f.b[j][0], f32x16{});
+#pragma unroll
+      for (int ks = 1; ks < KS; ++ks) pf = mfma_fp8_32x32x64(f.a[i][ks], f.b[j][ks], pf);
+    } else {
+      i32x16 pi = i32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          pi = mfma_i8_32x32x32(__builtin_bit_cast(i32x4, f.a[i][ks][t]), __builtin_bit_cast(i32x4, f.b[j][ks][t]), pi);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pf[r] = (float)pi[r];
+    }
+    return pf;
+  };
+  auto fma16 = [&](f32x16& a, const f32x16& pf, const f32x16& sf) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a[r] = __builtin_fmaf(pf[r], sf[r], a[r]);
+  };
+  // Issue order per group, sub-tiles t = (0,0) (0,1) (1,0) (1,1):
+  //   P_t, S_t (MFMAs) | rescale of sub-tile t-1 (16 VALU FMAs) | fence
+  // The fences (empty asm on the values) pin the order the compiler would otherwise
+  // rearrange: each MFMA pair waits for the fence after the previous rescale, so the VALU
+  // work of one sub-tile runs under the MFMAs of the next and at most two sub-tiles of
+  // products are live.  Sub-tile (1,1) of a group is rescaled under the next group's first
+  // MFMAs (`pp`, `ps` carry it).
+  f32x16 pp = f32x16{}, ps = f32x16{};
+  auto group = [&](Frag& f) {
+    constexpr int TI[4] = {0, 0, 1, 1}, TJ[4] = {0, 1, 0, 1};
+    f32x16 cp[4], cs[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int i = TI[t], j = TJ[t];
+      cp[t] = mfma_p(f, i, j);
+      cs[t] = mfma_bf16_32x32x16(f.x[i], f.w[j], f32x16{});
+      f32x16& a = t == 0 ? acc[1][1] : acc[TI[t - 1]][TJ[t - 1]];
+      fma16(a, t == 0 ? pp : cp[t - 1], t == 0 ? ps : cs[t - 1]);
+      if (t < 3) {
+        const int ni = TI[t + 1], nj = TJ[t + 1];
+        asm volatile("" : "+v"(a), "+v"(f.a[ni][0][0]), "+v"(f.a[ni][0][1]), "+v"(f.b[nj][0][0]),
+                     "+v"(f.b[nj][0][1]), "+v"(f.x[ni]), "+v"(f.w[nj]));
+      } else {
+        asm volatile("" : "+v"(a));
+      }
+    }
+    pp = cp[3];
+    ps = cs[3];
+  };
+
+  // Two LDS stages: stage s + 1 is loaded (A by DMA, B and scales through registers) while
+  // stage s computes.  Loads are unconditional (stage index clamped).
+  gload(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   lstore(0);
   __syncthreads();
-
-  for (int g = 0; g < ngroups; ++g) {
-    const int buf = g & 1;
-    if (g + 1 < ngroups) gload(g + 1);
-
-    i32x16 pacc[2][2];
+  for (int s = 0; s < nstages; ++s) {
+    const int buf = s & 1;
+    gload(min(s + 1, nstages - 1), buf ^ 1);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      i32x4 a[2], b[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = __builtin_bit_cast(i32x4, ld16(&sA[buf][(64 * wm + 32 * i + lr) * ROWB + 32 * ks + 16 * h]));
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        b[j] = __builtin_bit_cast(i32x4, ld16(&sB[buf][(64 * wn + 32 * j + lr) * ROWB + 32 * ks + 16 * h]));
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          pacc[i][j] = mfma_i8_32x32x32(a[i], b[j], ks == 0 ? i32x16{} : pacc[i][j]);
+    for (int gi = 0; gi < GPS; ++gi) {
+      Frag f;
+      read_frag(f, buf, gi);
+      group(f);
     }
-    f32x4 sxv[2][4];
-    float swv[2];
+    // All of stage s + 1 has to land before the barrier; the B conversion stays here (an
+    // earlier compiler-placed wait for B would also wait for the DMA issued after it).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        sxv[i][q] = *reinterpret_cast<const f32x4*>(&sSX[buf][64 * wm + 32 * i + 8 * q + 4 * h]);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) swv[j] = sSW[buf][64 * wn + 32 * j + lr];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          acc[i][j][r] = __builtin_fmaf((float)pacc[i][j][r], sxv[i][r >> 2][r & 3] * swv[j], acc[i][j][r]);
-
-    if (g + 1 < ngroups) lstore(buf ^ 1);
+    for (int i = 0; i < BCH; ++i) asm volatile("" : "+v"(rb[i]));
+    lstore(buf ^ 1);
     __syncthreads();
   }
+  fma16(acc[1][1], pp, ps);
 
   epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h);
+}
+
+// Weight-scale operand of the W4A4 scale MFMA, once per layer: (bf16 hi, bf16 lo) of the fp16
+// scale, hi + lo == scale exactly; MODE 1 (int8 16*q operands) folds in 1/256.
+__global__ void weight_scale_pairs_kernel(const uint16_t* __restrict__ sw, uint32_t* __restrict__ out, long n,
+                                          float mult) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const float f = half_bits_to_float(sw[i]) * mult;
+    const uint32_t hi = pack_bf16x2(f, 0.0f) & 0xFFFFu;
+    const uint32_t lo = pack_bf16x2(f - bf16lo(hi), 0.0f) & 0xFFFFu;
+    out[i] = hi | (lo << 16);
+  }
 }
 
 // --------------------------------------------------------------------------- W4A16
@@ -231,15 +373,14 @@ __global__ void __launch_bounds__(NTHR) w4a16_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < ALPT; ++i) {
       const int idx = tid + NTHR * i, row = idx / ALPR, part = idx % ALPR;
-      const int m = m0 + row;
-      ra[i] = m < p.M ? ld16(p.xhat + (long)m * p.ldxh + g * G + 8 * part) : u32x4{};
+      ra[i] = ld16(p.xhat + (long)min(m0 + row, p.M - 1) * p.ldxh + g * G + 8 * part);
     }
 #pragma unroll
     for (int i = 0; i < BLPT; ++i) {
       const int idx = tid + NTHR * i, row = idx / BLPR, part = idx % BLPR;
-      const int n = n0 + row;
-      rb[i] = n < p.N ? ld16(p.qw + (long)n * kp + g * (G / 2) + 16 * part) : u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
-      wsc[i] = n < p.N ? round_bf16(half_bits_to_float(p.sw[(long)n * ngroups + g])) : 0.0f;
+      const int n = min(n0 + row, p.N - 1);
+      rb[i] = ld16(p.qw + (long)n * kp + g * (G / 2) + 16 * part);
+      wsc[i] = round_bf16(half_bits_to_float(p.sw[(long)n * ngroups + g]));
     }
   };
   auto lstore = [&](int buf) {
@@ -305,17 +446,24 @@ __global__ void __launch_bounds__(NTHR) w4a16_kernel(GemmParams p) {
 
 }  // namespace
 
-hipError_t launch_w4a4(const GemmParams& p, int G, bool out_f32, hipStream_t st) {
-  const dim3 grid(((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN));
-  if (G == 64) {
-    if (out_f32) w4a4_kernel<64, true><<<grid, NTHR, 0, st>>>(p);
-    else w4a4_kernel<64, false><<<grid, NTHR, 0, st>>>(p);
-  } else if (G == 128) {
-    if (out_f32) w4a4_kernel<128, true><<<grid, NTHR, 0, st>>>(p);
-    else w4a4_kernel<128, false><<<grid, NTHR, 0, st>>>(p);
-  } else {
-    return hipErrorInvalidValue;
+hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st) {
+  const dim3 grid(((p.M + 255) / 256) * ((p.N + 127) / 128));
+#define SVDQ_W4A4(GG, MM)                                                        \
+  if (G == GG && mode == MM) {                                                   \
+    if (out_f32) w4a4_kernel<GG, MM, true><<<grid, 512, 0, st>>>(p);              \
+    else w4a4_kernel<GG, MM, false><<<grid, 512, 0, st>>>(p);                     \
+    return hipGetLastError();                                                    \
   }
+  SVDQ_W4A4(64, 0)
+  SVDQ_W4A4(128, 0)
+  SVDQ_W4A4(64, 1)
+  SVDQ_W4A4(128, 1)
+#undef SVDQ_W4A4
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, long n, int mode, hipStream_t st) {
+  weight_scale_pairs_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(sw, out, n, mode == 0 ? 1.0f : 1.0f / 256.0f);
   return hipGetLastError();
 }
 

@@ -14,25 +14,26 @@ struct ActParams {
   const float* lora_mult;   // [rl]
   int r, rl;
   int M, K, RTp;            // RTp: row stride of mid (>= r + rl, multiple of 32)
-  uint8_t* qx;              // [M, K/2]
+  uint8_t* qx;              // [M, K/2] canonical packed codes (optional)
+  uint8_t* qa;              // [M, K] 8-bit GEMM operand codes (quantizing modes)
   uint16_t* sx;             // [M, K/G] bf16
   uint16_t* xhat;           // [M, ldxh] bf16 (null unless requested)
   long ldxh;
-  float* mid;               // [M, RTp]
-  float* midp;              // [S, M, RTp] split partials (S > 1)
-  int* counters;            // [ceil(M/64)] arrival counters, zero between launches
+  float* mid;               // [S, M, RTp]: one partial per K split (summed by the GEMM)
   int gps;                  // K-groups per split
   int exact;                // 1: IEEE division for x / s everywhere
 };
 
 struct GemmParams {
-  const uint8_t* qx;        // W4A4: [M, K/2] packed activation codes
+  const uint8_t* qa;        // W4A4: [M, K] 8-bit activation operand codes
   const uint16_t* sx;       // W4A4: [M, K/G] bf16 activation scales
   const uint16_t* xhat;     // W4A16: [M, ldxh] bf16 smoothed activations
   long ldxh;
   const uint8_t* qw;        // [N, K/2] packed weight codes
-  const uint16_t* sw;       // [N, K/G] fp16 weight scales
-  const float* mid;         // [M, RTp] f32 low-rank/LoRA down projections
+  const uint16_t* sw;       // [N, K/G] fp16 weight scales (W4A16)
+  const uint32_t* swp;      // [N, K/G] (bf16 hi, bf16 lo) pairs of the weight scales (W4A4)
+  const float* mid;         // [S, M, RTp] f32 low-rank/LoRA down projections, per K split
+  int splits;               // S
   const uint16_t* l1cat;    // [N, RTp] bf16 up projections (zero padded)
   int RTp;
   const uint16_t* bias;     // [N] bf16 or null
@@ -42,9 +43,12 @@ struct GemmParams {
 };
 
 int act_splits(int M, int K, int G);
-hipError_t launch_act(const ActParams& p, int G, int nt, bool quant, bool xhat, int splits, hipStream_t st);
+// oper: 0 = no codes (x_hat only), 1 = e4m3 operand codes, 2 = int8 16*q operand codes
+hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, int splits, hipStream_t st);
 hipError_t launch_prepare_smooth(const uint16_t* s, float* srs, int K, hipStream_t st);
-hipError_t launch_w4a4(const GemmParams& p, int G, bool out_f32, hipStream_t st);
+// mode: 0 = e4m3 operands on the FP8 MFMA, 1 = int8 operands on the INT8 MFMA
+hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st);
+hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, long n, int mode, hipStream_t st);
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st);
 
 }  // namespace svdq

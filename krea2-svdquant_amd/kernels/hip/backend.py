@@ -38,6 +38,7 @@ class PreparedLayer:
     lora_mult: Optional[Tensor]  # f32 [rl]
     qweight: Tensor              # uint8 [N, Kp/2]
     weight_scales: Tensor        # fp16 [N, Kp/G]
+    scale_pairs: dict            # operand code -> int32 [N, Kp/G] W4A4 scale-MFMA operand (lazy)
     bias: Optional[Tensor]       # bf16 [N]
     group_size: int
     n: int
@@ -48,6 +49,12 @@ class PreparedLayer:
     @property
     def device(self) -> torch.device:
         return self.qweight.device
+
+    def weight_scale_pairs(self, operand: int) -> Tensor:
+        pairs = self.scale_pairs.get(operand)
+        if pairs is None:
+            pairs = self.scale_pairs[operand] = ops.prepare_weight_scales(self.weight_scales, operand)
+        return pairs
 
 
 def _pad_cols(t: Tensor, kp: int, value: float = 0.0) -> Tensor:
@@ -113,6 +120,7 @@ def prepare_layer(state: SVDQuantLinearState, adapters: Sequence = (),
         lora_mult=torch.cat(mults, 0).contiguous() if mults else None,
         qweight=qweight,
         weight_scales=scales.contiguous(),
+        scale_pairs={},
         bias=bias,
         group_size=g, n=n, k=k, kp=kp, rtp=rtp,
     )
@@ -125,8 +133,12 @@ def _flatten(x: Tensor) -> tuple[Tensor, tuple[int, ...]]:
 
 
 def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_f32: bool = False,
-                     exact_div: bool = False) -> Tensor:
-    """One SVDQuantLinear forward on prepared operands; returns [..., N]."""
+                     exact_div: bool = False, operand: str = "e4m3") -> Tensor:
+    """One SVDQuantLinear forward on prepared operands; returns [..., N].
+
+    ``operand`` picks the W4A4 MFMA: ``"e4m3"`` (FP8 MFMA, default) or ``"i8"`` (INT8 MFMA);
+    both compute the same exact integer group sums.
+    """
     if not x.is_cuda:
         raise RuntimeError("HIP gfx950 backend needs a GPU tensor")
     if x.dtype != torch.bfloat16:
@@ -140,13 +152,17 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
     if k != prep.kp:
         x2 = _pad_cols(x2, prep.kp)
     if mode == "w4a4":
-        qx, sx, _, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
-                                       prep.group_size, prep.rtp, True, False, exact_div)
-        y = ops.w4a4_gemm(qx, sx, prep.qweight, prep.weight_scales, mid, prep.l1cat, prep.bias,
-                          prep.group_size, out_f32)
+        if operand not in ops.OPERAND_NAMES:
+            raise ValueError(f"operand must be 'e4m3' or 'i8', got {operand!r}")
+        opc = ops.OPERAND_NAMES[operand]
+        qa, sx, _, _, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
+                                          prep.group_size, prep.rtp, opc, False, False, exact_div)
+        y = ops.w4a4_gemm(qa, sx, prep.qweight, prep.weight_scale_pairs(opc), mid, prep.l1cat, prep.bias,
+                          prep.group_size, opc, out_f32)
     elif mode == "w4a16":
-        _, _, xhat, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
-                                        prep.group_size, prep.rtp, False, True, exact_div)
+        _, _, _, xhat, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
+                                           prep.group_size, prep.rtp, ops.OPERAND_NONE, False, True,
+                                           exact_div)
         y = ops.w4a16_gemm(xhat, prep.qweight, prep.weight_scales, mid, prep.l1cat, prep.bias,
                            prep.group_size, out_f32)
     else:
@@ -155,9 +171,10 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
 
 
 def svdquant_linear_hip_gfx950(x: Tensor, state: SVDQuantLinearState, *, adapters: Sequence = (),
-                               mode: str = "w4a4", out_f32: bool = False) -> Tensor:
+                               mode: str = "w4a4", out_f32: bool = False, operand: str = "e4m3") -> Tensor:
     """Stateless backend entry (prepares the layer on every call; modules cache it)."""
-    return forward_prepared(x, prepare_layer(state, adapters, x.device), mode=mode, out_f32=out_f32)
+    return forward_prepared(x, prepare_layer(state, adapters, x.device), mode=mode, out_f32=out_f32,
+                            operand=operand)
 
 
 def svdquant_linear_hip_gfx950_w4a16(x: Tensor, state: SVDQuantLinearState, *, adapters: Sequence = (),

@@ -16,9 +16,11 @@ import torch  # noqa: F401  (must precede the library load: HIP runtime binding)
 PKG_DIR = Path(__file__).resolve().parents[2]
 LIB_PATH = Path(os.environ.get("SVDQ_GFX950_LIB", PKG_DIR / "_lib" / "libsvdq_gfx950.so"))
 
-SVDQ_ACT_QUANT = 1
+SVDQ_ACT_PACKED = 1
 SVDQ_ACT_XHAT = 2
 SVDQ_ACT_EXACT_DIV = 4
+SVDQ_ACT_OPERAND_E4M3 = 8
+SVDQ_ACT_OPERAND_I8 = 16
 
 STATUS = {0: "SVDQ_OK", -1: "SVDQ_ERR_ARG", -2: "SVDQ_ERR_SHAPE", -3: "SVDQ_ERR_ALIGN",
           -4: "SVDQ_ERR_UNSUPPORTED", -5: "SVDQ_ERR_LAUNCH"}
@@ -34,12 +36,12 @@ SIGNATURES = {
     "svdq_last_error": (ctypes.c_char_p, []),
     "svdq_group_supported": (_I, [_I]),
     "svdq_prepare_smooth": (_I, [_P, _P, _I, _P]),
-    "svdq_act_quant_workspace": (_I, [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_L),
-                                      ctypes.POINTER(_L)]),
-    "svdq_act_quant": (_I, [_P, _L, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _U, _P, _P, _P, _L,
-                            _P, _P, _P, _I, _P]),
-    "svdq_w4a4_gemm": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
-    "svdq_w4a16_gemm": (_I, [_P, _L, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
+    "svdq_act_quant_workspace": (_I, [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_L)]),
+    "svdq_act_quant": (_I, [_P, _L, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _U, _P, _P, _P, _P, _L,
+                            _P, _I, _P]),
+    "svdq_prepare_weight_scales": (_I, [_P, _P, _L, _I, _P]),
+    "svdq_w4a4_gemm": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
+    "svdq_w4a16_gemm": (_I, [_P, _L, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
 }
 
 _lock = threading.Lock()

@@ -14,9 +14,6 @@ from torch import Tensor
 
 from . import lib
 
-_counters: dict[tuple[int, int], Tensor] = {}
-
-
 def _vp(t: Optional[Tensor]):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
@@ -34,19 +31,6 @@ def _check_dev(name: str, t: Tensor, device: torch.device, dtype: torch.dtype) -
     _need(t.device == device, ValueError, f"{name} is on {t.device}, expected {device}")
     _need(t.dtype == dtype, TypeError, f"{name} must be {dtype}, got {t.dtype}")
     _need(t.is_contiguous(), ValueError, f"{name} must be contiguous")
-
-
-def _arrival_counters(device: torch.device, n: int) -> Tensor:
-    """Zero-initialised arrival counters of the split reduction (per device and stream).
-
-    The kernel leaves them zero after every completed launch, so they are allocated once.
-    """
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
-    buf = _counters.get(key)
-    if buf is None or buf.numel() < n:
-        buf = torch.zeros(max(n, 64), dtype=torch.int32, device=device)
-        _counters[key] = buf
-    return buf
 
 
 def rank_padded(total_rank: int) -> int:
@@ -70,14 +54,38 @@ def _(smooth):
     return smooth.new_empty(2 * smooth.numel(), dtype=torch.float32)
 
 
+OPERAND_NONE, OPERAND_E4M3, OPERAND_I8 = -1, 0, 1
+
+
+@torch.library.custom_op("svdq::prepare_weight_scales", mutates_args=())
+def prepare_weight_scales(weight_scales: Tensor, operand: int) -> Tensor:
+    """[N, K/G] uint32 (bf16 hi | bf16 lo << 16) operand of the W4A4 scale MFMA, per layer."""
+    _need(weight_scales.is_cuda, RuntimeError, "svdq::prepare_weight_scales needs a GPU tensor")
+    _check_dev("weight_scales", weight_scales, weight_scales.device, torch.float16)
+    _need(operand in (OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
+    out = torch.empty(weight_scales.shape, dtype=torch.int32, device=weight_scales.device)
+    lib.call("svdq_prepare_weight_scales", _vp(weight_scales), _vp(out), weight_scales.numel(), operand,
+             _stream(weight_scales.device))
+    return out
+
+
+@prepare_weight_scales.register_fake
+def _(weight_scales, operand):
+    return weight_scales.new_empty(weight_scales.shape, dtype=torch.int32)
+OPERAND_NAMES = {"e4m3": OPERAND_E4M3, "fp8": OPERAND_E4M3, "i8": OPERAND_I8, "int8": OPERAND_I8}
+
+
 @torch.library.custom_op("svdq::act_quant", mutates_args=())
 def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
-              lora_mult: Optional[Tensor], group_size: int, rtp: int, quant: bool, want_xhat: bool,
-              exact: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """Smoothing + A4 quantization + packing + low-rank / LoRA down projections, one pass.
+              lora_mult: Optional[Tensor], group_size: int, rtp: int, operand: int, packed: bool,
+              want_xhat: bool, exact: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Smoothing + A4 quantization + low-rank / LoRA down projections, one pass over x.
 
-    Returns ``(qx uint8 [M, K/2], sx bf16 [M, K/G], xhat bf16 [M, K], mid f32 [M, rtp])``;
-    outputs not requested (``quant`` / ``want_xhat``) are empty tensors.
+    ``operand`` selects the W4A4 GEMM operand codes written (``OPERAND_E4M3`` / ``OPERAND_I8``)
+    or none (``OPERAND_NONE``: x_hat only, the W4A16 path).  Returns
+    ``(qa uint8 [M, K], sx bf16 [M, K/G], qx uint8 [M, K/2], xhat bf16 [M, K], mid f32 [S, M, rtp])``
+    where ``mid`` holds one partial per K split (the GEMM adds them); outputs not requested are
+    empty tensors (``qx`` needs ``packed``, ``xhat`` ``want_xhat``).
     """
     _need(x.is_cuda, RuntimeError, "svdq::act_quant needs a GPU tensor")
     dev = x.device
@@ -98,34 +106,49 @@ def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
         _need(lora_mult is not None and lora_mult.numel() == rl, ValueError, "lora_mult must have rl entries")
         _check_dev("lora_mult", lora_mult, dev, torch.float32)
     _need(k % group_size == 0, ValueError, f"K={k} must be a multiple of group_size={group_size}")
+    _need(operand in (OPERAND_NONE, OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
+    quant = operand != OPERAND_NONE
 
-    splits = ctypes.c_int()
-    midp_n = ctypes.c_int64()
-    cnt_n = ctypes.c_int64()
-    lib.call("svdq_act_quant_workspace", m, k, group_size, rtp, ctypes.byref(splits),
-             ctypes.byref(midp_n), ctypes.byref(cnt_n))
-    qx = torch.empty((m, k // 2) if quant else (0,), dtype=torch.uint8, device=dev)
+    splits = _splits(m, k, group_size, rtp)
+    qa = torch.empty((m, k) if quant else (0,), dtype=torch.uint8, device=dev)
     sx = torch.empty((m, k // group_size) if quant else (0,), dtype=torch.bfloat16, device=dev)
+    qx = torch.empty((m, k // 2) if packed else (0,), dtype=torch.uint8, device=dev)
     xhat = torch.empty((m, k) if want_xhat else (0,), dtype=torch.bfloat16, device=dev)
-    mid = torch.empty((m, rtp), dtype=torch.float32, device=dev)
-    midp = torch.empty(midp_n.value, dtype=torch.float32, device=dev) if midp_n.value else None
-    counters = _arrival_counters(dev, cnt_n.value) if splits.value > 1 else None
-    flags = ((lib.SVDQ_ACT_QUANT if quant else 0) | (lib.SVDQ_ACT_XHAT if want_xhat else 0)
+    mid = torch.empty((splits, m, rtp), dtype=torch.float32, device=dev)
+    flags = ((lib.SVDQ_ACT_OPERAND_E4M3 if operand == OPERAND_E4M3 else 0)
+             | (lib.SVDQ_ACT_OPERAND_I8 if operand == OPERAND_I8 else 0)
+             | (lib.SVDQ_ACT_PACKED if packed else 0) | (lib.SVDQ_ACT_XHAT if want_xhat else 0)
              | (lib.SVDQ_ACT_EXACT_DIV if exact else 0))
     lib.call("svdq_act_quant", _vp(x), k, _vp(srs), _vp(l2), r, _vp(lora_down), rl, _vp(lora_mult),
-             m, k, group_size, rtp, flags, _vp(qx) if quant else None, _vp(sx) if quant else None,
-             _vp(xhat) if want_xhat else None, k, _vp(mid), _vp(midp), _vp(counters), splits.value,
+             m, k, group_size, rtp, flags, _vp(qa) if quant else None, _vp(sx) if quant else None,
+             _vp(qx) if packed else None, _vp(xhat) if want_xhat else None, k, _vp(mid), splits,
              _stream(dev))
-    return qx, sx, xhat, mid
+    return qa, sx, qx, xhat, mid
 
 
 @act_quant.register_fake
-def _(x, srs, l2, lora_down, lora_mult, group_size, rtp, quant, want_xhat, exact):
+def _(x, srs, l2, lora_down, lora_mult, group_size, rtp, operand, packed, want_xhat, exact):
     m, k = x.shape
-    qx = x.new_empty((m, k // 2) if quant else (0,), dtype=torch.uint8)
+    quant = operand != OPERAND_NONE
+    qa = x.new_empty((m, k) if quant else (0,), dtype=torch.uint8)
     sx = x.new_empty((m, k // group_size) if quant else (0,), dtype=torch.bfloat16)
+    qx = x.new_empty((m, k // 2) if packed else (0,), dtype=torch.uint8)
     xhat = x.new_empty((m, k) if want_xhat else (0,), dtype=torch.bfloat16)
-    return qx, sx, xhat, x.new_empty((m, rtp), dtype=torch.float32)
+    return qa, sx, qx, xhat, x.new_empty((_splits(m, k, group_size, rtp), m, rtp), dtype=torch.float32)
+
+
+_split_cache: dict[tuple[int, int, int, int], int] = {}
+
+
+def _splits(m: int, k: int, group_size: int, rtp: int) -> int:
+    """Number of K splits the activation pass uses for this shape (leading dim of ``mid``)."""
+    key = (m, k, group_size, rtp)
+    hit = _split_cache.get(key)
+    if hit is None:
+        splits, mid_n = ctypes.c_int(), ctypes.c_int64()
+        lib.call("svdq_act_quant_workspace", m, k, group_size, rtp, ctypes.byref(splits), ctypes.byref(mid_n))
+        hit = _split_cache[key] = splits.value
+    return hit
 
 
 def _check_gemm(qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tensor, bias: Optional[Tensor],
@@ -134,14 +157,15 @@ def _check_gemm(qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tens
     _need(qweight.dim() == 2 and qweight.shape[1] * 2 == k, ValueError,
           f"qweight must be [N, {k // 2}], got {tuple(qweight.shape)}")
     n = qweight.shape[0]
-    _check_dev("weight_scales", weight_scales, dev, torch.float16)
-    _need(tuple(weight_scales.shape) == (n, k // group_size), ValueError,
-          f"weight_scales must be [{n}, {k // group_size}], got {tuple(weight_scales.shape)}")
+    if weight_scales is not None:
+        _check_dev("weight_scales", weight_scales, dev, torch.float16)
+        _need(tuple(weight_scales.shape) == (n, k // group_size), ValueError,
+              f"weight_scales must be [{n}, {k // group_size}], got {tuple(weight_scales.shape)}")
     _check_dev("mid", mid, dev, torch.float32)
-    _need(mid.dim() == 2 and mid.shape[0] == m, ValueError, f"mid must be [{m}, RTp]")
+    _need(mid.dim() == 3 and mid.shape[1] == m, ValueError, f"mid must be [splits, {m}, RTp]")
     _check_dev("l1cat", l1cat, dev, torch.bfloat16)
-    _need(tuple(l1cat.shape) == (n, mid.shape[1]), ValueError,
-          f"l1cat must be [{n}, {mid.shape[1]}], got {tuple(l1cat.shape)}")
+    _need(tuple(l1cat.shape) == (n, mid.shape[2]), ValueError,
+          f"l1cat must be [{n}, {mid.shape[2]}], got {tuple(l1cat.shape)}")
     if bias is not None:
         _check_dev("bias", bias, dev, torch.bfloat16)
         _need(bias.numel() == n, ValueError, f"bias must have {n} entries")
@@ -149,25 +173,33 @@ def _check_gemm(qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tens
 
 
 @torch.library.custom_op("svdq::w4a4_gemm", mutates_args=())
-def w4a4_gemm(qx: Tensor, sx: Tensor, qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tensor,
-              bias: Optional[Tensor], group_size: int, out_f32: bool) -> Tensor:
-    """``y = sum_g sx sw (qx . qw)_g + mid @ l1cat^T + bias`` (bf16 or float32 output)."""
-    _need(qx.is_cuda, RuntimeError, "svdq::w4a4_gemm needs GPU tensors")
-    dev = qx.device
-    _check_dev("qx", qx, dev, torch.uint8)
-    m, k = qx.shape[0], qx.shape[1] * 2
+def w4a4_gemm(qa: Tensor, sx: Tensor, qweight: Tensor, weight_scale_pairs: Tensor, mid: Tensor, l1cat: Tensor,
+              bias: Optional[Tensor], group_size: int, operand: int, out_f32: bool) -> Tensor:
+    """``y = sum_g sx sw (qa . qw)_g + mid @ l1cat^T + bias`` (bf16 or float32 output).
+
+    ``weight_scale_pairs`` comes from ``prepare_weight_scales`` with the same ``operand``.
+    """
+    _need(qa.is_cuda, RuntimeError, "svdq::w4a4_gemm needs GPU tensors")
+    dev = qa.device
+    _check_dev("qa", qa, dev, torch.uint8)
+    m, k = qa.shape
     _check_dev("sx", sx, dev, torch.bfloat16)
     _need(tuple(sx.shape) == (m, k // group_size), ValueError, "sx must be [M, K/G]")
-    n = _check_gemm(qweight, weight_scales, mid, l1cat, bias, m, k, group_size, dev)
+    _need(operand in (OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
+    _check_dev("weight_scale_pairs", weight_scale_pairs, dev, torch.int32)
+    n = _check_gemm(qweight, None, mid, l1cat, bias, m, k, group_size, dev)
+    _need(tuple(weight_scale_pairs.shape) == (n, k // group_size), ValueError,
+          f"weight_scale_pairs must be [{n}, {k // group_size}], got {tuple(weight_scale_pairs.shape)}")
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
-    lib.call("svdq_w4a4_gemm", _vp(qx), _vp(sx), _vp(qweight), _vp(weight_scales), _vp(mid), _vp(l1cat),
-             mid.shape[1], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32), _stream(dev))
+    lib.call("svdq_w4a4_gemm", _vp(qa), operand, _vp(sx), _vp(qweight), _vp(weight_scale_pairs), _vp(mid),
+             mid.shape[0], _vp(l1cat), mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32),
+             _stream(dev))
     return y
 
 
 @w4a4_gemm.register_fake
-def _(qx, sx, qweight, weight_scales, mid, l1cat, bias, group_size, out_f32):
-    return qx.new_empty((qx.shape[0], qweight.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)
+def _(qa, sx, qweight, weight_scale_pairs, mid, l1cat, bias, group_size, operand, out_f32):
+    return qa.new_empty((qa.shape[0], qweight.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)
 
 
 @torch.library.custom_op("svdq::w4a16_gemm", mutates_args=())
@@ -180,8 +212,8 @@ def w4a16_gemm(xhat: Tensor, qweight: Tensor, weight_scales: Tensor, mid: Tensor
     m, k = xhat.shape
     n = _check_gemm(qweight, weight_scales, mid, l1cat, bias, m, k, group_size, dev)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
-    lib.call("svdq_w4a16_gemm", _vp(xhat), k, _vp(qweight), _vp(weight_scales), _vp(mid), _vp(l1cat),
-             mid.shape[1], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32), _stream(dev))
+    lib.call("svdq_w4a16_gemm", _vp(xhat), k, _vp(qweight), _vp(weight_scales), _vp(mid), mid.shape[0],
+             _vp(l1cat), mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32), _stream(dev))
     return y
 
 

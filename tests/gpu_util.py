@@ -50,5 +50,20 @@ def from_device_state(ds: SVDQuantLinearState) -> sim.LayerState:
                           shape=tuple(ds.original_shape))
 
 
+PERM8 = [0, 2, 4, 6, 1, 3, 5, 7]
+"""GEMM operand byte order inside each chunk of 8 columns: byte j holds column PERM8[j]."""
+
+
+def operand_bytes(q: np.ndarray, fmt: str) -> np.ndarray:
+    """Expected W4A4 operand codes [M, K] for int codes q: OCP e4m3 (torch's float8_e4m3fn
+    encoder) or int8 16*q, in the PERM8 byte order."""
+    m, k = q.shape
+    if fmt == "e4m3":
+        codes = torch.from_numpy(q.astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    else:
+        codes = (q.astype(np.int16) * 16).astype(np.int8).view(np.uint8)
+    return codes.reshape(m, k // 8, 8)[:, :, PERM8].reshape(m, k)
+
+
 def rel_l2(a, b) -> float:
     return sim.rel_l2(a, b)

@@ -29,11 +29,10 @@ def test_group_support_and_workspace_sizing():
     h = lib.load()
     assert h.svdq_group_supported(64) == 1 and h.svdq_group_supported(128) == 1
     assert h.svdq_group_supported(32) == 0
-    s, mp, ct = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64()
-    lib.call("svdq_act_quant_workspace", 4096, 6144, 64, 32, ctypes.byref(s), ctypes.byref(mp), ctypes.byref(ct))
-    assert s.value >= 1 and ct.value == 64
-    assert mp.value == (s.value * 4096 * 32 if s.value > 1 else 0)
-    lib.call("svdq_act_quant_workspace", 256, 6144, 64, 32, ctypes.byref(s), ctypes.byref(mp), ctypes.byref(ct))
+    s, mp = ctypes.c_int(), ctypes.c_int64()
+    lib.call("svdq_act_quant_workspace", 4096, 6144, 64, 32, ctypes.byref(s), ctypes.byref(mp))
+    assert s.value >= 1 and mp.value == s.value * 4096 * 32
+    lib.call("svdq_act_quant_workspace", 256, 6144, 64, 32, ctypes.byref(s), ctypes.byref(mp))
     assert 1 < s.value <= 6144 // 64 // 4
 
 
@@ -44,26 +43,31 @@ def test_group_support_and_workspace_sizing():
     ((0, 6144, 64, 32), -1, "M=0"),
 ])
 def test_workspace_rejects_bad_arguments(args, status, needle):
-    s, mp, ct = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64()
+    s, mp = ctypes.c_int(), ctypes.c_int64()
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_act_quant_workspace", *args, ctypes.byref(s), ctypes.byref(mp), ctypes.byref(ct))
+        lib.call("svdq_act_quant_workspace", *args, ctypes.byref(s), ctypes.byref(mp))
     assert ei.value.status == status and needle in str(ei.value)
 
 
 def test_gemm_rejects_null_and_misaligned_pointers_before_any_launch():
     nul = None
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_w4a4_gemm", nul, nul, nul, nul, nul, nul, 32, nul, 128, 128, 128, 64, nul, 128, 0, nul)
+        lib.call("svdq_w4a4_gemm", nul, 0, nul, nul, nul, nul, 1, nul, 32, nul, 128, 128, 128, 64, nul, 128, 0, nul)
     assert ei.value.status == -1
     fake = ctypes.c_void_p(0x1000)
     odd = ctypes.c_void_p(0x1008)
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_w4a4_gemm", fake, fake, odd, fake, fake, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0, nul)
+        lib.call("svdq_w4a4_gemm", fake, 0, fake, odd, fake, fake, 1, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0,
+                 nul)
     assert ei.value.status == -3
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_w4a16_gemm", fake, 100, fake, fake, fake, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0, nul)
+        lib.call("svdq_w4a16_gemm", fake, 100, fake, fake, fake, 1, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0, nul)
     assert ei.value.status == -3
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_act_quant", fake, 128, fake, fake, 200, nul, 0, nul, 64, 128, 64, 224, 1, fake, fake, nul, 0,
-                 fake, nul, nul, 1, nul)
+        lib.call("svdq_act_quant", fake, 128, fake, fake, 200, nul, 0, nul, 64, 128, 64, 224, lib.SVDQ_ACT_OPERAND_E4M3,
+                 fake, fake, nul, nul, 0, fake, 1, nul)
     assert ei.value.status == -4  # ceil(200/32) = 7 MFMA column tiles > 4
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_act_quant", fake, 128, fake, fake, 32, nul, 0, nul, 64, 128, 64, 32,
+                 lib.SVDQ_ACT_OPERAND_E4M3 | lib.SVDQ_ACT_OPERAND_I8, fake, fake, nul, nul, 0, fake, 1, nul)
+    assert ei.value.status == -1 and "two operand formats" in str(ei.value)

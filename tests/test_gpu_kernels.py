@@ -15,7 +15,8 @@ import torch
 from oracle import numerics as nm
 from oracle import pack as op
 from oracle import sim, synth
-from tests.gpu_util import (bf16_bits_of, bf16_tensor, device_adapters, rel_l2, to_device_state)
+from tests.gpu_util import (bf16_bits_of, bf16_tensor, device_adapters, operand_bytes, rel_l2,
+                            to_device_state)
 from tests.golden_io import load_layer_fixture
 
 pytestmark = pytest.mark.gpu
@@ -28,12 +29,14 @@ def _ops():
     return backend, ops
 
 
-def _run_act(x_np, st, dev, quant=True, xhat=False, exact=False, adapters=True):
+def _run_act(x_np, st, dev, operand="e4m3", packed=True, xhat=False, exact=False, adapters=True):
+    """Returns (qa, sx, qx, xhat, mid) from svdq::act_quant."""
     backend, ops = _ops()
     prep = backend.prepare_layer(to_device_state(st, dev), device_adapters(st, dev) if adapters else (), dev)
     x = bf16_tensor(x_np, dev)
+    opc = ops.OPERAND_NONE if operand is None else ops.OPERAND_NAMES[operand]
     out = ops.act_quant(x, prep.srs, prep.l2, prep.lora_down, prep.lora_mult, st.group_size, prep.rtp,
-                        quant, xhat, exact)
+                        opc, packed, xhat, exact)
     torch.cuda.synchronize()
     return out, prep
 
@@ -45,31 +48,40 @@ def test_w4a4_gemm_layout_identity(dev):
     q = np.zeros((m, k), np.int8)
     q[np.arange(m), np.arange(m)] = 1
     qw = ((np.arange(n)[:, None] * 7 + np.arange(k)[None, :] * 3) % 15 - 7).astype(np.int8)
-    qx = torch.from_numpy(op.pack_int4(q)).to(dev)
     sx = bf16_tensor(np.ones((m, 1), np.float32), dev)
     qwt = torch.from_numpy(op.pack_int4(qw)).to(dev)
     sw = torch.ones((n, 1), dtype=torch.float16, device=dev)
-    mid = torch.zeros((m, 32), dtype=torch.float32, device=dev)
+    mid = torch.zeros((1, m, 32), dtype=torch.float32, device=dev)
     l1 = torch.zeros((n, 32), dtype=torch.bfloat16, device=dev)
-    y = ops.w4a4_gemm(qx, sx, qwt, sw, mid, l1, None, 64, True).cpu().numpy()
     expect = qw[:, :m].T.astype(np.float32)
-    if not np.array_equal(y, expect):
-        bad = np.argwhere(y != expect)
-        rows = {int(r): [int(rr) for rr in np.where((expect == y[r]).all(1))[0]] for r in range(m)}
-        pytest.fail(f"{len(bad)} mismatches, first {bad[:4].tolist()}; row matches {rows}")
+    for fmt in ("e4m3", "i8"):
+        qa = torch.from_numpy(operand_bytes(q, fmt)).to(dev)
+        opc = ops.OPERAND_NAMES[fmt]
+        y = ops.w4a4_gemm(qa, sx, qwt, ops.prepare_weight_scales(sw, opc), mid, l1, None, 64, opc, True).cpu().numpy()
+        if not np.array_equal(y, expect):
+            bad = np.argwhere(y != expect)
+            rows = {int(r): [int(rr) for rr in np.where((expect == y[r]).all(1))[0]] for r in range(m)}
+            pytest.fail(f"{fmt}: {len(bad)} mismatches, first {bad[:4].tolist()}; row matches {rows}")
 
 
 @pytest.mark.parametrize("name", ["w4a4_small_g64.npz", "w4a4_small_g128.npz"])
 def test_act_quant_golden_bit_exact(dev, name):
     fx, x, st = load_layer_fixture(GOLDEN / name)
-    (qx, sx, xh, mid), _ = _run_act(x, st, dev, quant=True, xhat=True)
+    (qa, sx, qx, xh, mid), _ = _run_act(x, st, dev, operand="e4m3", packed=True, xhat=True)
     assert np.array_equal(qx.cpu().numpy(), fx["qx_packed"])
     assert np.array_equal(bf16_bits_of(sx), fx["sx"])
     assert np.array_equal(bf16_bits_of(xh), fx["xhat"])
+    codes = op.unpack_int4(fx["qx_packed"])
+    assert np.array_equal(qa.cpu().numpy(), operand_bytes(codes, "e4m3"))
+    (qa8, sx8, qx8, _, _), _ = _run_act(x, st, dev, operand="i8", packed=True)
+    assert np.array_equal(qa8.cpu().numpy(), operand_bytes(codes, "i8"))
+    assert np.array_equal(qx8.cpu().numpy(), fx["qx_packed"]) and np.array_equal(bf16_bits_of(sx8), fx["sx"])
+    (_, _, _, xh16, _), _ = _run_act(x, st, dev, operand=None, packed=False, xhat=True)
+    assert np.array_equal(bf16_bits_of(xh16), fx["xhat"])
     r = st.l2.shape[0]
     ad = st.adapters[0]
     lmid = ad.multiplier * (x.astype(np.float64) @ ad.down.astype(np.float64).T)
-    got = mid.cpu().numpy()
+    got = mid.double().sum(0).cpu().numpy()
     assert rel_l2(got[:, :r], fx["mid"]) < 1e-5
     assert rel_l2(got[:, r:r + ad.rank], lmid) < 1e-5
     assert (got[:, r + ad.rank:] == 0).all()
@@ -82,13 +94,16 @@ def test_act_quant_edge_rows_bit_exact(dev):
     st = sim.LayerState(smooth=nm.from_bf16_bits(fx["smooth"]), qweight=np.full((32, k // 2), 0x88, np.uint8),
                         weight_scales=np.ones((32, k // 64), np.float32), l1=np.zeros((32, 32), np.float32),
                         l2=np.zeros((32, k), np.float32), bias=None, group_size=64, shape=(32, k))
+    codes = op.unpack_int4(fx["qx_packed"])
     for exact in (False, True):
-        (qx, sx, xh, _), _ = _run_act(x, st, dev, quant=True, xhat=True, exact=exact)
+        (qa, sx, qx, xh, _), _ = _run_act(x, st, dev, packed=True, xhat=True, exact=exact)
         assert np.array_equal(qx.cpu().numpy(), fx["qx_packed"]), f"exact={exact}"
         assert np.array_equal(bf16_bits_of(sx), fx["sx"]), f"exact={exact}"
         assert np.array_equal(bf16_bits_of(xh), fx["xhat"]), f"exact={exact}"
-        (qx2, sx2, _, _), _ = _run_act(x, st, dev, quant=True, xhat=False, exact=exact)
+        assert np.array_equal(qa.cpu().numpy(), operand_bytes(codes, "e4m3")), f"exact={exact}"
+        (qa2, sx2, qx2, _, _), _ = _run_act(x, st, dev, packed=True, xhat=False, exact=exact)
         assert np.array_equal(qx2.cpu().numpy(), fx["qx_packed"]) and np.array_equal(bf16_bits_of(sx2), fx["sx"])
+        assert np.array_equal(qa2.cpu().numpy(), operand_bytes(codes, "e4m3"))
 
 
 @pytest.mark.parametrize("m,k,g", [(1, 64, 64), (5, 448, 64), (64, 1024, 64), (100, 768, 128), (257, 1536, 64),
@@ -96,28 +111,30 @@ def test_act_quant_edge_rows_bit_exact(dev):
 def test_act_quant_random_shapes_bit_exact(dev, m, k, g):
     x = synth.make_activation(m, k, seed=m + k)
     st = synth.make_layer(64, k, x, rank=32, group_size=g, seed=3)
-    (qx, sx, _, mid), _ = _run_act(x, st, dev, adapters=False)
-    xh, packed, sxo, _ = sim.quantize_activations(x, st)
+    (qa, sx, qx, _, mid), _ = _run_act(x, st, dev, adapters=False)
+    xh, packed, sxo, codes = sim.quantize_activations(x, st)
     assert np.array_equal(qx.cpu().numpy(), packed)
+    assert np.array_equal(qa.cpu().numpy(), operand_bytes(codes, "e4m3"))
     assert np.array_equal(bf16_bits_of(sx), nm.bf16_bits(sxo))
     ref_mid = xh.astype(np.float64) @ st.l2.astype(np.float64).T
-    assert rel_l2(mid.cpu().numpy()[:, :32], ref_mid) < 1e-5
+    assert rel_l2(mid.double().sum(0).cpu().numpy()[:, :32], ref_mid) < 1e-5
 
 
-def _layer_outputs(x_np, st, dev, mode, out_f32):
+def _layer_outputs(x_np, st, dev, mode, out_f32, operand="e4m3"):
     backend, _ = _ops()
     prep = backend.prepare_layer(to_device_state(st, dev), device_adapters(st, dev), dev)
-    y = backend.forward_prepared(bf16_tensor(x_np, dev), prep, mode=mode, out_f32=out_f32)
+    y = backend.forward_prepared(bf16_tensor(x_np, dev), prep, mode=mode, out_f32=out_f32, operand=operand)
     return y.float().cpu().numpy()
 
 
 def _check_layer(x, st, dev, mode, ref):
-    y32 = _layer_outputs(x, st, dev, mode, True)
-    e32 = rel_l2(y32, ref)
-    y16 = _layer_outputs(x, st, dev, mode, False)
-    e16 = rel_l2(y16, nm.bf16(ref.astype(np.float32)))
-    print(f"  rel_l2 f32-out={e32:.3e} bf16-out vs bf16(ref)={e16:.3e}")
-    assert e32 < TOL_F32 and e16 < TOL
+    for operand in (("e4m3", "i8") if mode == "w4a4" else ("e4m3",)):
+        y32 = _layer_outputs(x, st, dev, mode, True, operand)
+        e32 = rel_l2(y32, ref)
+        y16 = _layer_outputs(x, st, dev, mode, False, operand)
+        e16 = rel_l2(y16, nm.bf16(ref.astype(np.float32)))
+        print(f"  {mode}/{operand}: rel_l2 f32-out={e32:.3e} bf16-out vs bf16(ref)={e16:.3e}")
+        assert e32 < TOL_F32 and e16 < TOL
 
 
 @pytest.mark.parametrize("name", ["w4a4_small_g64.npz", "w4a4_small_g128.npz"])

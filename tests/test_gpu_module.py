@@ -5,7 +5,8 @@ import torch
 
 from oracle import numerics as nm
 from oracle import sim, synth
-from tests.gpu_util import bf16_bits_of, bf16_tensor, from_device_state, rel_l2, to_device_state
+from tests.gpu_util import (bf16_bits_of, bf16_tensor, from_device_state, operand_bytes, rel_l2,
+                            to_device_state)
 
 pytestmark = pytest.mark.gpu
 
@@ -50,10 +51,11 @@ def test_config0_layer(dev):
     prep = backend.prepare_layer(to_device_state(st, dev), (), dev)
     xd = bf16_tensor(x, dev)
     r = sim.w4a4_eval(x, st)
-    y32 = backend.forward_prepared(xd, prep, mode="w4a4", out_f32=True).cpu().numpy()
-    e = rel_l2(y32, r["y"])
-    print(f"  config0 w4a4 rel_l2={e:.3e}")
-    assert e < 1e-4
+    for operand in ("e4m3", "i8"):
+        y32 = backend.forward_prepared(xd, prep, mode="w4a4", out_f32=True, operand=operand).cpu().numpy()
+        e = rel_l2(y32, r["y"])
+        print(f"  config0 w4a4/{operand} rel_l2={e:.3e}")
+        assert e < 1e-4
     y16 = backend.forward_prepared(xd, prep, mode="w4a16", out_f32=True).cpu().numpy()
     e16 = rel_l2(y16, sim.w4a16_eval(x, st)["y"])
     print(f"  config0 w4a16 rel_l2={e16:.3e}")
@@ -75,10 +77,12 @@ def test_full_size_ffup_codes_exact_and_rows_sampled(dev):
                         group_size=64, smooth_clamp=(None, None), seed=3)
     del w
     prep = backend.prepare_layer(ds, (), dev)
-    qx, sx, _, mid = ops.act_quant(xd, prep.srs, prep.l2, None, None, 64, prep.rtp, True, False, False)
+    qa, sx, qx, _, mid = ops.act_quant(xd, prep.srs, prep.l2, None, None, 64, prep.rtp, ops.OPERAND_E4M3,
+                                       True, False, False)
     st = from_device_state(ds)
-    xh, packed, sxo, _ = sim.quantize_activations(x, st)
+    xh, packed, sxo, codes = sim.quantize_activations(x, st)
     assert np.array_equal(qx.cpu().numpy(), packed)
+    assert np.array_equal(qa.cpu().numpy(), operand_bytes(codes, "e4m3"))
     assert np.array_equal(bf16_bits_of(sx), nm.bf16_bits(sxo))
     y = backend.forward_prepared(xd, prep, mode="w4a4", out_f32=True)
     rows = np.random.default_rng(1).choice(m, 48, replace=False)
