@@ -129,7 +129,7 @@ def main() -> int:
     qa, sx, _, _, mid = ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False)
     ms_act = time_loop(lambda: ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False,
                                              False), args.steps)
-    ms_gemm = time_loop(lambda: ops.w4a4_gemm(qa, sx, prep.qweight, prep.weight_scale_pairs(opc), mid, prep.l1cat,
+    ms_gemm = time_loop(lambda: ops.w4a4_gemm(qa, sx, prep.weight_operand(opc), prep.weight_scale_pairs(opc), mid, prep.l1cat,
                                               None, g, opc, False), args.steps)
     log(f"act {ms_act:.4f} ms, gemm {ms_gemm:.4f} ms")
     flops = 2.0 * m * n * k

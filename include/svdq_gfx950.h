@@ -97,17 +97,26 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
  *   sw : fp16 [count]      swp : u32 [count] (output) */
 int svdq_prepare_weight_scales(const void* sw, void* swp, int64_t count, int operand, hipStream_t stream);
 
+/* Per-layer weight operand of svdq_w4a4_gemm: the packed INT4 codes of the checkpoint
+ * (runtime/load.py:90-126, pack.py:47-56) expanded to one 8-bit MFMA operand code per weight,
+ * in the byte order and `operand` format of svdq_act_quant's qa.  No reference counterpart:
+ * the GEMM streams both operands into LDS without unpacking, trading N*K bytes of HBM for
+ * the per-tile conversion work.
+ *   qw : u8 [N, K/2]      qwe : u8 [N, K] (output);  K % 16 == 0 */
+int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int operand, hipStream_t stream);
+
 /* W4A4 GEMM with fused epilogue.  Replaces the residual product of reference
  * quant/svd.py:158 / kernels/triton/generic_int4.py:18-82 (with INT4 activations), the
  * low-rank add + bias of generic_int4.py:84-133 / svd.py:159-163 and the LoRA add of
  * runtime/linear.py:158-160:
  *   y = sum_g sx sw (qa . qw)_g + mid @ l1cat^T + bias
  *   qa : u8 [M, K] operand codes (svdq_act_quant) in `operand` format (SVDQ_OPERAND_*)
- *   sx : bf16 [M, K/group]   qw : u8 [N, K/2] (checkpoint layout)
+ *   sx : bf16 [M, K/group]   qwe: u8 [N, K] from svdq_prepare_weight_operand (same format)
  *   swp: u32 [N, K/group] from svdq_prepare_weight_scales (same operand format)
+ *   M*K and N*K below 2^31 (larger problems are split over rows by the caller)
  *   mid: f32 [splits, M, RTp] from svdq_act_quant    l1cat : bf16 [N, RTp] = [l1 | up_1 | ... | 0]
  *   bias: bf16 [N] or NULL     y : [M, ldy], bf16 (out_f32 = 0) or f32 (out_f32 = 1) */
-int svdq_w4a4_gemm(const void* qa, int operand, const void* sx, const void* qw, const void* swp,
+int svdq_w4a4_gemm(const void* qa, int operand, const void* sx, const void* qwe, const void* swp,
                    const float* mid, int splits, const void* l1cat, int RTp, const void* bias, int M, int N,
                    int K, int group, void* y, int64_t ldy, int out_f32, hipStream_t stream);
 

@@ -169,21 +169,33 @@ int svdq_prepare_weight_scales(const void* sw, void* swp, int64_t count, int ope
                   "prepare_weight_scales");
 }
 
-int svdq_w4a4_gemm(const void* qa, int operand, const void* sx, const void* qw, const void* swp,
+int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int operand, hipStream_t stream) {
+  if (!qw || !qwe) return fail(SVDQ_ERR_ARG, "prepare_weight_operand: null pointer");
+  if (N <= 0 || K <= 0 || K % 16) return fail(SVDQ_ERR_SHAPE, "prepare_weight_operand: N=%d K=%d (K %% 16 == 0)", N, K);
+  if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
+    return fail(SVDQ_ERR_ARG, "prepare_weight_operand: operand format %d", operand);
+  if (!aligned16(qw) || !aligned16(qwe)) return fail(SVDQ_ERR_ALIGN, "prepare_weight_operand: pointers must be 16-byte aligned");
+  return launched(svdq::launch_weight_operand(static_cast<const uint8_t*>(qw), static_cast<uint8_t*>(qwe),
+                                              (long)N * (K / 8), operand, stream),
+                  "prepare_weight_operand");
+}
+
+int svdq_w4a4_gemm(const void* qa, int operand, const void* sx, const void* qwe, const void* swp,
                    const float* mid, int splits, const void* l1cat, int RTp, const void* bias, int M, int N,
                    int K, int group, void* y, int64_t ldy, int out_f32, hipStream_t stream) {
   const void* sw = swp;
-  if (int e = gemm_common_checks("w4a4_gemm", qw, sw, mid, splits, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
+  if (int e = gemm_common_checks("w4a4_gemm", qwe, sw, mid, splits, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
     return e;
   if (!qa || !sx) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
   if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
     return fail(SVDQ_ERR_ARG, "w4a4_gemm: operand format %d", operand);
   if (!aligned16(qa)) return fail(SVDQ_ERR_ALIGN, "w4a4_gemm: qa must be 16-byte aligned");
-  // The kernel addresses qa and qw with 32-bit byte offsets.
-  if ((int64_t)M * K > INT32_MAX || (int64_t)N * (K / 2) > INT32_MAX)
-    return fail(SVDQ_ERR_SHAPE, "w4a4_gemm: M*K=%lld or N*K/2=%lld exceeds 2^31-1 bytes; split the call",
-                (long long)M * K, (long long)N * (K / 2));
-  svdq::GemmParams p = gemm_params(qw, sw, mid, splits, l1cat, RTp, bias, M, N, K, y, ldy);
+  // The kernel addresses qa and qwe with 32-bit byte offsets.
+  if ((int64_t)M * K > INT32_MAX || (int64_t)N * K > INT32_MAX)
+    return fail(SVDQ_ERR_SHAPE, "w4a4_gemm: M*K=%lld or N*K=%lld exceeds 2^31-1 bytes; split the call",
+                (long long)M * K, (long long)N * K);
+  svdq::GemmParams p = gemm_params(nullptr, sw, mid, splits, l1cat, RTp, bias, M, N, K, y, ldy);
+  p.qwe = static_cast<const uint8_t*>(qwe);
   p.qa = static_cast<const uint8_t*>(qa);
   p.sx = static_cast<const uint16_t*>(sx);
   p.swp = static_cast<const uint32_t*>(swp);

@@ -13,6 +13,8 @@
 // Both kernels permute k inside each chunk of 8 columns (even k first) when they unpack
 // INT4 nibbles; the activation operand is written in the same order, so the permutation
 // cancels in every dot product.
+#include <algorithm>
+
 #include "svdq_common.h"
 #include "svdq_kernels.h"
 
@@ -106,8 +108,9 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 //
 // Block tile 256 x 128, 8 waves in a 4 x 2 grid, wave tile 64 x 64 = 2 x 2 sub-tiles of
 // 32 x 32.  K advances 128 columns per pipeline stage (two groups of 64 or one of 128), two
-// LDS stages.  Operand A (8-bit codes from the activation pass) goes global -> LDS by DMA;
-// operand B (packed INT4) goes through registers and is converted to 8-bit codes on the way.
+// LDS stages.  Both operands are 8-bit codes in HBM (activations from the activation pass,
+// weights expanded once per layer) and go global -> LDS by DMA; only the scales pass
+// through registers.
 //
 // LDS operand tiles: rows of 128 bytes = 8 chunks of 16; chunk c of row r sits at chunk
 // position c ^ ((r >> 1) & 7).  The 16 lanes of a ds_read_b128 phase read one logical chunk
@@ -122,7 +125,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   constexpr int GPS = KB / G;                 // groups per stage
   constexpr int KS = G / 64;                  // 64-column MFMA steps per group
   constexpr int ADMA = TBM * KB / (16 * NT);  // A: 16-byte DMA chunks per thread per stage (4)
-  constexpr int BCH = TBN * KB / (16 * NT);   // B: 16-column chunks per thread per stage (2)
+  constexpr int BDMA = TBN * KB / (16 * NT);  // B: 16-byte DMA chunks per thread per stage (2)
   constexpr int XS = TBM + 1, WS = TBN + 1;   // scale rows per group (+1 zero row)
   static_assert(GPS * TBM <= NT && GPS * TBN <= NT, "one scale of each kind per thread");
   __shared__ __attribute__((aligned(1024))) uint8_t sA[2][TBM * KB];
@@ -137,30 +140,25 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   int bm, bn;
   tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
   const int m0 = bm * TBM, n0 = bn * TBN;
-  const int K = p.K, ngroups = K / G, nstages = (K + KB - 1) / KB, kp = K / 2;
+  const int K = p.K, ngroups = K / G, nstages = (K + KB - 1) / KB;
 
-  // A by DMA: wave w, chunk i covers LDS bytes [(ADMA w + i) KB, +1 KB) of the stage tile,
-  // i.e. 8 rows; lane L lands at row 8 (ADMA w + i) + L / 8, chunk position L % 8.  Columns
+  // DMA sources: wave w, chunk i covers LDS bytes [(DMA w + i) KB, +1 KB) of a stage tile,
+  // i.e. 8 rows; lane L lands at row 8 (DMA w + i) + L / 8, chunk position L % 8.  Columns
   // past K (a last stage holding a single group of 64) are clamped to the row's last chunk;
   // that group's scale is zero.  Offsets are 32-bit (the host bounds the operand sizes).
-  uint32_t aoff[ADMA];
-  int alim[ADMA];
+  uint32_t aoff[ADMA], boff[BDMA];
+  int alim[ADMA], blim[BDMA];
 #pragma unroll
   for (int i = 0; i < ADMA; ++i) {
-    const int row = 8 * (ADMA * wave + i) + lane / 8;
-    const int c = (lane % 8) ^ ((row >> 1) & 7);
+    const int row = 8 * (ADMA * wave + i) + lane / 8, c = (lane % 8) ^ ((row >> 1) & 7);
     aoff[i] = (uint32_t)min(m0 + row, p.M - 1) * (uint32_t)K + 16 * c;
     alim[i] = K - 16 - 16 * c;
   }
-  // B through registers (packed nibbles -> 8-bit codes): chunk index tid + NT i -> row, position.
-  uint32_t boff[BCH];
-  int blim[BCH], bdst[BCH];
 #pragma unroll
-  for (int i = 0; i < BCH; ++i) {
-    const int idx = tid + NT * i, row = idx / 8, pc = idx % 8, c = pc ^ ((row >> 1) & 7);
-    boff[i] = (uint32_t)min(n0 + row, p.N - 1) * (uint32_t)kp + 8 * c;
-    blim[i] = kp - 8 - 8 * c;
-    bdst[i] = row * 128 + 16 * pc;
+  for (int i = 0; i < BDMA; ++i) {
+    const int row = 8 * (BDMA * wave + i) + lane / 8, c = (lane % 8) ^ ((row >> 1) & 7);
+    boff[i] = (uint32_t)min(n0 + row, p.N - 1) * (uint32_t)K + 16 * c;
+    blim[i] = K - 16 - 16 * c;
   }
   // Scales: thread t stages sx of row t % TBM for group t / TBM of the stage and sw of
   // column t % TBN for group t / TBN (threads past GPS * TBN load a duplicate, not stored).
@@ -181,22 +179,18 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
     r[1] = 0u; r[2] = 0u; r[3] = 0u;
   }
 
-  // Fragment addresses (bytes within a stage tile): row base + the lane's chunk pair.
+  // Fragment addresses (bytes within a stage tile): the lane's row; chunk c at c ^ sw_.
   const int sw_ = (lr >> 1) & 7;
   const int arow = (64 * wm + lr) * 128, brow = (64 * wn + lr) * 128;
   // Scale-MFMA operand rows: lanes 32-63 (the second half of K) read the zero row.
   const int xrow = h ? TBM : 64 * wm + lr, wrow = h ? TBN : 64 * wn + lr;
 
-  u32x2 rb[BCH];
   uint32_t rx, rw;
   int xg;
-  // Issue the loads of stage `s`: B and scales into registers, then A into LDS buffer `buf`.
+  // Issue the loads of stage `s`: scales into registers, then A and B into LDS buffer `buf`.
   // The DMA goes last: the compiler does not count it, so any wait it places for its own
   // loads is ordered before the DMA and never waits for it.
   auto gload = [&](int s, int buf) {
-#pragma unroll
-    for (int i = 0; i < BCH; ++i)
-      rb[i] = *reinterpret_cast<const u32x2*>(p.qw + (boff[i] + (uint32_t)min(s * (KB / 2), blim[i])));
     xg = s * GPS + xj;
     rx = p.sx[xoff + (uint32_t)min(xg, ngroups - 1)];
     rw = p.swp[woff + (uint32_t)min(s * GPS + wj, ngroups - 1)];
@@ -204,20 +198,12 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
     for (int i = 0; i < ADMA; ++i)
       dma16(p.qa, aoff[i] + (uint32_t)min(s * KB, alim[i]),
             __builtin_amdgcn_readfirstlane(lds_offset(&sA[buf][(ADMA * wave + i) * 1024])));
+#pragma unroll
+    for (int i = 0; i < BDMA; ++i)
+      dma16(p.qwe, boff[i] + (uint32_t)min(s * KB, blim[i]),
+            __builtin_amdgcn_readfirstlane(lds_offset(&sB[buf][(BDMA * wave + i) * 1024])));
   };
   auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      uint32_t o0, o1, o2, o3;
-      if (MODE == 0) {
-        nib8_to_e4m3(rb[i][0], o0, o1);
-        nib8_to_e4m3(rb[i][1], o2, o3);
-      } else {
-        nib8_to_i8x16(rb[i][0], o0, o1);
-        nib8_to_i8x16(rb[i][1], o2, o3);
-      }
-      st16(&sB[buf][bdst[i]], u32x4{o0, o1, o2, o3});
-    }
     if (x_live) sX[buf][xj][4 * xr] = xg < ngroups ? rx * 0x10001u : 0u;
     if (w_live) sW[buf][wj][4 * wr] = rw;
   };
@@ -275,13 +261,13 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) a[r] = __builtin_fmaf(pf[r], sf[r], a[r]);
   };
+
   // Issue order per group, sub-tiles t = (0,0) (0,1) (1,0) (1,1):
-  //   P_t, S_t (MFMAs) | rescale of sub-tile t-1 (16 VALU FMAs) | fence
-  // The fences (empty asm on the values) pin the order the compiler would otherwise
-  // rearrange: each MFMA pair waits for the fence after the previous rescale, so the VALU
-  // work of one sub-tile runs under the MFMAs of the next and at most two sub-tiles of
-  // products are live.  Sub-tile (1,1) of a group is rescaled under the next group's first
-  // MFMAs (`pp`, `ps` carry it).
+  //   P_t (product MFMA) | rescale of sub-tile t-1 (16 VALU FMAs) | S_t (scale MFMA)
+  // The rescale of t-1 needs S_{t-1}, which completed before P_t could issue, so the FMAs
+  // run in the shadow of P_t.  Empty asm statements on the values pin this order (the
+  // compiler would otherwise issue all MFMAs of a stage first and run out of registers).
+  // Sub-tile (1,1) of a group is rescaled under the next group's first MFMA.
   f32x16 pp = f32x16{}, ps = f32x16{};
   auto group = [&](Frag& f) {
     constexpr int TI[4] = {0, 0, 1, 1}, TJ[4] = {0, 1, 0, 1};
@@ -290,23 +276,21 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
     for (int t = 0; t < 4; ++t) {
       const int i = TI[t], j = TJ[t];
       cp[t] = mfma_p(f, i, j);
-      cs[t] = mfma_bf16_32x32x16(f.x[i], f.w[j], f32x16{});
       f32x16& a = t == 0 ? acc[1][1] : acc[TI[t - 1]][TJ[t - 1]];
       fma16(a, t == 0 ? pp : cp[t - 1], t == 0 ? ps : cs[t - 1]);
+      asm volatile("" : "+v"(a), "+v"(f.x[i]), "+v"(f.w[j]));
+      cs[t] = mfma_bf16_32x32x16(f.x[i], f.w[j], f32x16{});
       if (t < 3) {
         const int ni = TI[t + 1], nj = TJ[t + 1];
-        asm volatile("" : "+v"(a), "+v"(f.a[ni][0][0]), "+v"(f.a[ni][0][1]), "+v"(f.b[nj][0][0]),
-                     "+v"(f.b[nj][0][1]), "+v"(f.x[ni]), "+v"(f.w[nj]));
-      } else {
-        asm volatile("" : "+v"(a));
+        asm volatile("" : "+v"(f.a[ni][0][0]), "+v"(f.a[ni][0][1]), "+v"(f.b[nj][0][0]), "+v"(f.b[nj][0][1]));
       }
     }
     pp = cp[3];
     ps = cs[3];
   };
 
-  // Two LDS stages: stage s + 1 is loaded (A by DMA, B and scales through registers) while
-  // stage s computes.  Loads are unconditional (stage index clamped).
+  // Two LDS stages: stage s + 1 is loaded while stage s computes.  Loads are unconditional
+  // (stage index clamped).
   gload(0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   lstore(0);
@@ -320,17 +304,25 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
       read_frag(f, buf, gi);
       group(f);
     }
-    // All of stage s + 1 has to land before the barrier; the B conversion stays here (an
-    // earlier compiler-placed wait for B would also wait for the DMA issued after it).
+    // All of stage s + 1 has to land before the barrier.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) asm volatile("" : "+v"(rb[i]));
     lstore(buf ^ 1);
     __syncthreads();
   }
   fma16(acc[1][1], pp, ps);
 
   epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h);
+}
+
+// Weight operand of the W4A4 GEMM, once per layer: each packed dword (8 nibbles, k0 in the
+// low nibble) becomes 8 operand bytes [k0 k2 k4 k6 k1 k3 k5 k7].
+__global__ void weight_operand_kernel(const uint32_t* __restrict__ qw, u32x2* __restrict__ out, long n, int mode) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    uint32_t lo, hi;
+    if (mode == 0) nib8_to_e4m3(qw[i], lo, hi);
+    else nib8_to_i8x16(qw[i], lo, hi);
+    out[i] = u32x2{lo, hi};
+  }
 }
 
 // Weight-scale operand of the W4A4 scale MFMA, once per layer: (bf16 hi, bf16 lo) of the fp16
@@ -464,6 +456,13 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
 
 hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, long n, int mode, hipStream_t st) {
   weight_scale_pairs_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(sw, out, n, mode == 0 ? 1.0f : 1.0f / 256.0f);
+  return hipGetLastError();
+}
+
+hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, long ndwords, int mode, hipStream_t st) {
+  const long blocks = std::min<long>((ndwords + 255) / 256, 8192);
+  weight_operand_kernel<<<(unsigned)blocks, 256, 0, st>>>(reinterpret_cast<const uint32_t*>(qw),
+                                                          reinterpret_cast<u32x2*>(qwe), ndwords, mode);
   return hipGetLastError();
 }
 

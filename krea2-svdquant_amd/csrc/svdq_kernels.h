@@ -29,7 +29,8 @@ struct GemmParams {
   const uint16_t* sx;       // W4A4: [M, K/G] bf16 activation scales
   const uint16_t* xhat;     // W4A16: [M, ldxh] bf16 smoothed activations
   long ldxh;
-  const uint8_t* qw;        // [N, K/2] packed weight codes
+  const uint8_t* qw;        // [N, K/2] packed weight codes (W4A16)
+  const uint8_t* qwe;       // [N, K] 8-bit weight operand codes (W4A4)
   const uint16_t* sw;       // [N, K/G] fp16 weight scales (W4A16)
   const uint32_t* swp;      // [N, K/G] (bf16 hi, bf16 lo) pairs of the weight scales (W4A4)
   const float* mid;         // [S, M, RTp] f32 low-rank/LoRA down projections, per K split
@@ -49,6 +50,7 @@ hipError_t launch_prepare_smooth(const uint16_t* s, float* srs, int K, hipStream
 // mode: 0 = e4m3 operands on the FP8 MFMA, 1 = int8 operands on the INT8 MFMA
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st);
 hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, long n, int mode, hipStream_t st);
+hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, long ndwords, int mode, hipStream_t st);
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st);
 
 }  // namespace svdq

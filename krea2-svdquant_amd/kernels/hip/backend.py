@@ -39,6 +39,7 @@ class PreparedLayer:
     qweight: Tensor              # uint8 [N, Kp/2]
     weight_scales: Tensor        # fp16 [N, Kp/G]
     scale_pairs: dict            # operand code -> int32 [N, Kp/G] W4A4 scale-MFMA operand (lazy)
+    operands: dict               # operand code -> uint8 [N, Kp] W4A4 weight operand codes (lazy)
     bias: Optional[Tensor]       # bf16 [N]
     group_size: int
     n: int
@@ -49,6 +50,12 @@ class PreparedLayer:
     @property
     def device(self) -> torch.device:
         return self.qweight.device
+
+    def weight_operand(self, operand: int) -> Tensor:
+        codes = self.operands.get(operand)
+        if codes is None:
+            codes = self.operands[operand] = ops.prepare_weight_operand(self.qweight, operand)
+        return codes
 
     def weight_scale_pairs(self, operand: int) -> Tensor:
         pairs = self.scale_pairs.get(operand)
@@ -121,6 +128,7 @@ def prepare_layer(state: SVDQuantLinearState, adapters: Sequence = (),
         qweight=qweight,
         weight_scales=scales.contiguous(),
         scale_pairs={},
+        operands={},
         bias=bias,
         group_size=g, n=n, k=k, kp=kp, rtp=rtp,
     )
@@ -157,8 +165,8 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
         opc = ops.OPERAND_NAMES[operand]
         qa, sx, _, _, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
                                           prep.group_size, prep.rtp, opc, False, False, exact_div)
-        y = ops.w4a4_gemm(qa, sx, prep.qweight, prep.weight_scale_pairs(opc), mid, prep.l1cat, prep.bias,
-                          prep.group_size, opc, out_f32)
+        y = ops.w4a4_gemm(qa, sx, prep.weight_operand(opc), prep.weight_scale_pairs(opc), mid, prep.l1cat,
+                          prep.bias, prep.group_size, opc, out_f32)
     elif mode == "w4a16":
         _, _, _, xhat, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
                                            prep.group_size, prep.rtp, ops.OPERAND_NONE, False, True,

@@ -72,6 +72,25 @@ def prepare_weight_scales(weight_scales: Tensor, operand: int) -> Tensor:
 @prepare_weight_scales.register_fake
 def _(weight_scales, operand):
     return weight_scales.new_empty(weight_scales.shape, dtype=torch.int32)
+
+
+@torch.library.custom_op("svdq::prepare_weight_operand", mutates_args=())
+def prepare_weight_operand(qweight: Tensor, operand: int) -> Tensor:
+    """[N, K] uint8 W4A4 weight operand: the packed INT4 codes [N, K/2] expanded to one MFMA
+    operand code per weight (same byte order and format as ``act_quant``'s ``qa``), per layer."""
+    _need(qweight.is_cuda, RuntimeError, "svdq::prepare_weight_operand needs a GPU tensor")
+    _check_dev("qweight", qweight, qweight.device, torch.uint8)
+    _need(qweight.dim() == 2, ValueError, f"qweight must be [N, K/2], got {tuple(qweight.shape)}")
+    _need(operand in (OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
+    n, k = qweight.shape[0], qweight.shape[1] * 2
+    out = torch.empty((n, k), dtype=torch.uint8, device=qweight.device)
+    lib.call("svdq_prepare_weight_operand", _vp(qweight), _vp(out), n, k, operand, _stream(qweight.device))
+    return out
+
+
+@prepare_weight_operand.register_fake
+def _(qweight, operand):
+    return qweight.new_empty((qweight.shape[0], qweight.shape[1] * 2), dtype=torch.uint8)
 OPERAND_NAMES = {"e4m3": OPERAND_E4M3, "fp8": OPERAND_E4M3, "i8": OPERAND_I8, "int8": OPERAND_I8}
 
 
@@ -151,16 +170,7 @@ def _splits(m: int, k: int, group_size: int, rtp: int) -> int:
     return hit
 
 
-def _check_gemm(qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tensor, bias: Optional[Tensor],
-                m: int, k: int, group_size: int, dev: torch.device) -> int:
-    _check_dev("qweight", qweight, dev, torch.uint8)
-    _need(qweight.dim() == 2 and qweight.shape[1] * 2 == k, ValueError,
-          f"qweight must be [N, {k // 2}], got {tuple(qweight.shape)}")
-    n = qweight.shape[0]
-    if weight_scales is not None:
-        _check_dev("weight_scales", weight_scales, dev, torch.float16)
-        _need(tuple(weight_scales.shape) == (n, k // group_size), ValueError,
-              f"weight_scales must be [{n}, {k // group_size}], got {tuple(weight_scales.shape)}")
+def _check_epilogue(mid: Tensor, l1cat: Tensor, bias: Optional[Tensor], m: int, n: int, dev: torch.device) -> None:
     _check_dev("mid", mid, dev, torch.float32)
     _need(mid.dim() == 3 and mid.shape[1] == m, ValueError, f"mid must be [splits, {m}, RTp]")
     _check_dev("l1cat", l1cat, dev, torch.bfloat16)
@@ -169,15 +179,28 @@ def _check_gemm(qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tens
     if bias is not None:
         _check_dev("bias", bias, dev, torch.bfloat16)
         _need(bias.numel() == n, ValueError, f"bias must have {n} entries")
+
+
+def _check_gemm(qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tensor, bias: Optional[Tensor],
+                m: int, k: int, group_size: int, dev: torch.device) -> int:
+    _check_dev("qweight", qweight, dev, torch.uint8)
+    _need(qweight.dim() == 2 and qweight.shape[1] * 2 == k, ValueError,
+          f"qweight must be [N, {k // 2}], got {tuple(qweight.shape)}")
+    n = qweight.shape[0]
+    _check_dev("weight_scales", weight_scales, dev, torch.float16)
+    _need(tuple(weight_scales.shape) == (n, k // group_size), ValueError,
+          f"weight_scales must be [{n}, {k // group_size}], got {tuple(weight_scales.shape)}")
+    _check_epilogue(mid, l1cat, bias, m, n, dev)
     return n
 
 
 @torch.library.custom_op("svdq::w4a4_gemm", mutates_args=())
-def w4a4_gemm(qa: Tensor, sx: Tensor, qweight: Tensor, weight_scale_pairs: Tensor, mid: Tensor, l1cat: Tensor,
-              bias: Optional[Tensor], group_size: int, operand: int, out_f32: bool) -> Tensor:
+def w4a4_gemm(qa: Tensor, sx: Tensor, weight_operand: Tensor, weight_scale_pairs: Tensor, mid: Tensor,
+              l1cat: Tensor, bias: Optional[Tensor], group_size: int, operand: int, out_f32: bool) -> Tensor:
     """``y = sum_g sx sw (qa . qw)_g + mid @ l1cat^T + bias`` (bf16 or float32 output).
 
-    ``weight_scale_pairs`` comes from ``prepare_weight_scales`` with the same ``operand``.
+    ``weight_operand`` and ``weight_scale_pairs`` come from ``prepare_weight_operand`` and
+    ``prepare_weight_scales`` with the same ``operand``.
     """
     _need(qa.is_cuda, RuntimeError, "svdq::w4a4_gemm needs GPU tensors")
     dev = qa.device
@@ -186,20 +209,24 @@ def w4a4_gemm(qa: Tensor, sx: Tensor, qweight: Tensor, weight_scale_pairs: Tenso
     _check_dev("sx", sx, dev, torch.bfloat16)
     _need(tuple(sx.shape) == (m, k // group_size), ValueError, "sx must be [M, K/G]")
     _need(operand in (OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
+    _check_dev("weight_operand", weight_operand, dev, torch.uint8)
+    _need(weight_operand.dim() == 2 and weight_operand.shape[1] == k, ValueError,
+          f"weight_operand must be [N, {k}], got {tuple(weight_operand.shape)}")
     _check_dev("weight_scale_pairs", weight_scale_pairs, dev, torch.int32)
-    n = _check_gemm(qweight, None, mid, l1cat, bias, m, k, group_size, dev)
+    n = weight_operand.shape[0]
     _need(tuple(weight_scale_pairs.shape) == (n, k // group_size), ValueError,
           f"weight_scale_pairs must be [{n}, {k // group_size}], got {tuple(weight_scale_pairs.shape)}")
+    _check_epilogue(mid, l1cat, bias, m, n, dev)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
-    lib.call("svdq_w4a4_gemm", _vp(qa), operand, _vp(sx), _vp(qweight), _vp(weight_scale_pairs), _vp(mid),
+    lib.call("svdq_w4a4_gemm", _vp(qa), operand, _vp(sx), _vp(weight_operand), _vp(weight_scale_pairs), _vp(mid),
              mid.shape[0], _vp(l1cat), mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32),
              _stream(dev))
     return y
 
 
 @w4a4_gemm.register_fake
-def _(qa, sx, qweight, weight_scale_pairs, mid, l1cat, bias, group_size, operand, out_f32):
-    return qa.new_empty((qa.shape[0], qweight.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)
+def _(qa, sx, weight_operand, weight_scale_pairs, mid, l1cat, bias, group_size, operand, out_f32):
+    return qa.new_empty((qa.shape[0], weight_operand.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)
 
 
 @torch.library.custom_op("svdq::w4a16_gemm", mutates_args=())

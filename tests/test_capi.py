@@ -71,3 +71,30 @@ def test_gemm_rejects_null_and_misaligned_pointers_before_any_launch():
         lib.call("svdq_act_quant", fake, 128, fake, fake, 32, nul, 0, nul, 64, 128, 64, 32,
                  lib.SVDQ_ACT_OPERAND_E4M3 | lib.SVDQ_ACT_OPERAND_I8, fake, fake, nul, nul, 0, fake, 1, nul)
     assert ei.value.status == -1 and "two operand formats" in str(ei.value)
+
+
+def test_prepare_entry_points_reject_bad_arguments_before_any_launch():
+    nul, fake = None, ctypes.c_void_p(0x1000)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_prepare_weight_operand", nul, fake, 128, 128, 0, nul)
+    assert ei.value.status == -1
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_prepare_weight_operand", fake, fake, 128, 120, 0, nul)
+    assert ei.value.status == -2 and "K % 16" in str(ei.value)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_prepare_weight_operand", fake, fake, 128, 128, 7, nul)
+    assert ei.value.status == -1 and "operand format" in str(ei.value)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_prepare_weight_operand", fake, ctypes.c_void_p(0x1004), 128, 128, 0, nul)
+    assert ei.value.status == -3
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_prepare_weight_scales", fake, fake, 0, 0, nul)
+    assert ei.value.status == -1
+
+
+def test_w4a4_gemm_rejects_operands_beyond_32bit_offsets():
+    fake = ctypes.c_void_p(0x1000)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a4_gemm", fake, 0, fake, fake, fake, fake, 1, fake, 32, None, 65536, 128, 65536, 64, fake,
+                 128, 0, None)
+    assert ei.value.status == -2 and "2^31" in str(ei.value)

@@ -57,11 +57,22 @@ def test_w4a4_gemm_layout_identity(dev):
     for fmt in ("e4m3", "i8"):
         qa = torch.from_numpy(operand_bytes(q, fmt)).to(dev)
         opc = ops.OPERAND_NAMES[fmt]
-        y = ops.w4a4_gemm(qa, sx, qwt, ops.prepare_weight_scales(sw, opc), mid, l1, None, 64, opc, True).cpu().numpy()
+        y = ops.w4a4_gemm(qa, sx, ops.prepare_weight_operand(qwt, opc), ops.prepare_weight_scales(sw, opc), mid, l1,
+                          None, 64, opc, True).cpu().numpy()
         if not np.array_equal(y, expect):
             bad = np.argwhere(y != expect)
             rows = {int(r): [int(rr) for rr in np.where((expect == y[r]).all(1))[0]] for r in range(m)}
             pytest.fail(f"{fmt}: {len(bad)} mismatches, first {bad[:4].tolist()}; row matches {rows}")
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "i8"])
+def test_weight_operand_matches_unpacked_codes(dev, fmt):
+    """The per-layer expanded weight operand holds exactly the oracle's unpacked codes."""
+    _, ops = _ops()
+    rng = np.random.default_rng(5)
+    packed = rng.integers(0, 256, size=(300, 448), dtype=np.uint8)   # every nibble value, K = 896
+    out = ops.prepare_weight_operand(torch.from_numpy(packed).to(dev), ops.OPERAND_NAMES[fmt]).cpu().numpy()
+    assert np.array_equal(out, operand_bytes(op.unpack_int4(packed), fmt))
 
 
 @pytest.mark.parametrize("name", ["w4a4_small_g64.npz", "w4a4_small_g128.npz"])
