@@ -126,9 +126,10 @@ def main() -> int:
 
     # per-kernel averages, each kernel timed alone on the same (current) stream
     opc = ops.OPERAND_E4M3
-    qa, sx, _, _, mid = ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False)
+    qa, sx, _, _, mid = ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False,
+                                      True)
     ms_act = time_loop(lambda: ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False,
-                                             False), args.steps)
+                                             False, True), args.steps)
     ms_gemm = time_loop(lambda: ops.w4a4_gemm(qa, sx, prep.weight_operand(opc), prep.weight_scale_pairs(opc), mid, prep.l1cat,
                                               None, g, opc, False), args.steps)
     log(f"act {ms_act:.4f} ms, gemm {ms_gemm:.4f} ms")

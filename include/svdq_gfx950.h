@@ -43,6 +43,8 @@ typedef enum svdq_status {
 #define SVDQ_ACT_EXACT_DIV 4u     /* IEEE division for x / s everywhere (slow reference mode)   */
 #define SVDQ_ACT_OPERAND_E4M3 8u  /* quantize: write scales sx and e4m3 operand codes qa        */
 #define SVDQ_ACT_OPERAND_I8 16u   /* quantize: write scales sx and int8 (16*q) operand codes qa */
+#define SVDQ_ACT_SX_PAIRS 32u     /* quantize: write sx as u32 bf16 pairs (sx | sx << 16), the
+                                     form svdq_w4a4_gemm takes (its scale-MFMA operand)        */
 
 /* Operand formats of svdq_w4a4_gemm (must match the SVDQ_ACT_OPERAND_* flag used). */
 #define SVDQ_OPERAND_E4M3 0    /* FP8 MFMA (v_mfma_f32_32x32x64_f8f6f4): every INT4 code is exact */
@@ -76,7 +78,8 @@ int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int6
  *   l2       : bf16 [r, K]            lora_down : bf16 [rl, K] or NULL (rl = 0)
  *   lora_mult: f32 [rl]: per-column multiplier scale * alpha / rank of the owning adapter
  *   Quantizing (one SVDQ_ACT_OPERAND_* flag):
- *     sx : bf16 [M, K/group] scales, bit-exact bf16(max(amax, bf16(1e-8)) / 7)
+ *     sx : bf16 [M, K/group] scales, bit-exact bf16(max(amax, bf16(1e-8)) / 7); with
+ *          SVDQ_ACT_SX_PAIRS u32 [K/group, M] (group-major) holding (bits | bits << 16)
  *     qa : u8 [M, K] operand codes of the W4A4 GEMM: the code of k sits at byte
  *          8*(k/8) + perm(k%8), perm = {0,4,1,5,2,6,3,7} (even k of a chunk of 8, then odd k);
  *          e4m3(q) or int8 16*q
@@ -90,12 +93,12 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
                    int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
                    float* mid, int splits, hipStream_t stream);
 
-/* Per-layer weight-scale operand of svdq_w4a4_gemm: swp[i] = bf16 hi | bf16 lo << 16 with
- * hi + lo == float(sw[i]) exactly (times 1/256 for SVDQ_OPERAND_I8).  No reference
- * counterpart: it splits the checkpoint's fp16 weight_scales (runtime/load.py:116) for the
- * bf16 MFMA that forms the per-group scale products.
- *   sw : fp16 [count]      swp : u32 [count] (output) */
-int svdq_prepare_weight_scales(const void* sw, void* swp, int64_t count, int operand, hipStream_t stream);
+/* Per-layer weight-scale operand of svdq_w4a4_gemm: swp[g][n] = bf16 hi | bf16 lo << 16 with
+ * hi + lo == float(sw[n][g]) exactly (times 1/256 for SVDQ_OPERAND_I8), group-major.  No
+ * reference counterpart: it splits the checkpoint's fp16 weight_scales (runtime/load.py:116)
+ * for the bf16 MFMA that forms the per-group scale products.
+ *   sw : fp16 [N, ngroups]      swp : u32 [ngroups, N] (output) */
+int svdq_prepare_weight_scales(const void* sw, void* swp, int N, int ngroups, int operand, hipStream_t stream);
 
 /* Per-layer weight operand of svdq_w4a4_gemm: the packed INT4 codes of the checkpoint
  * (runtime/load.py:90-126, pack.py:47-56) expanded to one 8-bit MFMA operand code per weight,
@@ -111,12 +114,13 @@ int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int ope
  * runtime/linear.py:158-160:
  *   y = sum_g sx sw (qa . qw)_g + mid @ l1cat^T + bias
  *   qa : u8 [M, K] operand codes (svdq_act_quant) in `operand` format (SVDQ_OPERAND_*)
- *   sx : bf16 [M, K/group]   qwe: u8 [N, K] from svdq_prepare_weight_operand (same format)
- *   swp: u32 [N, K/group] from svdq_prepare_weight_scales (same operand format)
+ *   sxp: u32 [K/group, M] bf16 pairs (svdq_act_quant with SVDQ_ACT_SX_PAIRS)
+ *   qwe: u8 [N, K] from svdq_prepare_weight_operand (same format)
+ *   swp: u32 [K/group, N] from svdq_prepare_weight_scales (same operand format)
  *   M*K and N*K below 2^31 (larger problems are split over rows by the caller)
  *   mid: f32 [splits, M, RTp] from svdq_act_quant    l1cat : bf16 [N, RTp] = [l1 | up_1 | ... | 0]
  *   bias: bf16 [N] or NULL     y : [M, ldy], bf16 (out_f32 = 0) or f32 (out_f32 = 1) */
-int svdq_w4a4_gemm(const void* qa, int operand, const void* sx, const void* qwe, const void* swp,
+int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
                    const float* mid, int splits, const void* l1cat, int RTp, const void* bias, int M, int N,
                    int K, int group, void* y, int64_t ldy, int out_f32, hipStream_t stream);
 

@@ -179,7 +179,11 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
           }
         }
       }
-      if (rok) p.sx[rowc * ngroups + g] = (uint16_t)(__float_as_uint(sc) >> 16);
+      if (rok) {
+        const uint32_t sb = __float_as_uint(sc) >> 16;
+        if (p.sx_pairs) reinterpret_cast<uint32_t*>(p.sx)[(long)g * p.M + rowc] = sb * 0x10001u;
+        else p.sx[rowc * ngroups + g] = (uint16_t)sb;
+      }
     }
     if (XHAT && rok) {
 #pragma unroll

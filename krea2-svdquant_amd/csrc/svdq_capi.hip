@@ -73,13 +73,15 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
                    int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
                    float* mid, int splits, hipStream_t stream) {
   const unsigned known = SVDQ_ACT_PACKED | SVDQ_ACT_XHAT | SVDQ_ACT_EXACT_DIV | SVDQ_ACT_OPERAND_E4M3 |
-                         SVDQ_ACT_OPERAND_I8;
+                         SVDQ_ACT_OPERAND_I8 | SVDQ_ACT_SX_PAIRS;
   if (flags & ~known) return fail(SVDQ_ERR_ARG, "act_quant: unknown flags 0x%x", flags);
   const bool e4m3 = flags & SVDQ_ACT_OPERAND_E4M3, i8 = flags & SVDQ_ACT_OPERAND_I8;
   const bool quant = e4m3 || i8, want_xhat = flags & SVDQ_ACT_XHAT, packed = flags & SVDQ_ACT_PACKED;
   if (e4m3 && i8) return fail(SVDQ_ERR_ARG, "act_quant: two operand formats requested");
   if (!quant && !want_xhat) return fail(SVDQ_ERR_ARG, "act_quant: neither an operand format nor XHAT requested");
   if (packed && !quant) return fail(SVDQ_ERR_ARG, "act_quant: PACKED needs an operand format");
+  const bool pairs = flags & SVDQ_ACT_SX_PAIRS;
+  if (pairs && !quant) return fail(SVDQ_ERR_ARG, "act_quant: SX_PAIRS needs an operand format");
   if (i8 && want_xhat) return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: XHAT with int8 operands has no kernel");
   if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant: M=%d", M);
   if (int e = check_group(group, K)) return e;
@@ -95,6 +97,7 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
                 (long long)ldx, (long long)ldxh);
   if (!aligned16(x) || !aligned16(srs) || !aligned16(l2) || !aligned16(mid) ||
       (rl > 0 && !aligned16(lora_down)) || (quant && !aligned16(qa)) || (packed && !aligned16(qx)) ||
+      (pairs && reinterpret_cast<uintptr_t>(sx) % 4) ||
       (want_xhat && !aligned16(xhat)))
     return fail(SVDQ_ERR_ALIGN, "act_quant: device pointers must be 16-byte aligned");
   const int expect = svdq::act_splits(M, K, group);
@@ -121,6 +124,7 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
   const int ngroups = K / group;
   p.gps = (ngroups + splits - 1) / splits;
   p.exact = (flags & SVDQ_ACT_EXACT_DIV) ? 1 : 0;
+  p.sx_pairs = pairs ? 1 : 0;
   return launched(svdq::launch_act(p, group, nt, e4m3 ? 1 : (i8 ? 2 : 0), want_xhat, splits, stream),
                   "act_quant");
 }
@@ -159,13 +163,13 @@ static svdq::GemmParams gemm_params(const void* qw, const void* sw, const float*
   return p;
 }
 
-int svdq_prepare_weight_scales(const void* sw, void* swp, int64_t count, int operand, hipStream_t stream) {
+int svdq_prepare_weight_scales(const void* sw, void* swp, int N, int ngroups, int operand, hipStream_t stream) {
   if (!sw || !swp) return fail(SVDQ_ERR_ARG, "prepare_weight_scales: null pointer");
-  if (count <= 0) return fail(SVDQ_ERR_ARG, "prepare_weight_scales: count=%lld", (long long)count);
+  if (N <= 0 || ngroups <= 0) return fail(SVDQ_ERR_ARG, "prepare_weight_scales: N=%d ngroups=%d", N, ngroups);
   if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
     return fail(SVDQ_ERR_ARG, "prepare_weight_scales: operand format %d", operand);
-  return launched(svdq::launch_weight_scale_pairs(static_cast<const uint16_t*>(sw), static_cast<uint32_t*>(swp),
-                                                  (long)count, operand, stream),
+  return launched(svdq::launch_weight_scale_pairs(static_cast<const uint16_t*>(sw), static_cast<uint32_t*>(swp), N,
+                                                  ngroups, operand, stream),
                   "prepare_weight_scales");
 }
 
@@ -180,24 +184,26 @@ int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int ope
                   "prepare_weight_operand");
 }
 
-int svdq_w4a4_gemm(const void* qa, int operand, const void* sx, const void* qwe, const void* swp,
+int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
                    const float* mid, int splits, const void* l1cat, int RTp, const void* bias, int M, int N,
                    int K, int group, void* y, int64_t ldy, int out_f32, hipStream_t stream) {
   const void* sw = swp;
   if (int e = gemm_common_checks("w4a4_gemm", qwe, sw, mid, splits, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
     return e;
-  if (!qa || !sx) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
+  if (!qa || !sxp) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
   if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
     return fail(SVDQ_ERR_ARG, "w4a4_gemm: operand format %d", operand);
-  if (!aligned16(qa)) return fail(SVDQ_ERR_ALIGN, "w4a4_gemm: qa must be 16-byte aligned");
+  if (!aligned16(qa) || !aligned16(qwe) || reinterpret_cast<uintptr_t>(sxp) % 4 || reinterpret_cast<uintptr_t>(swp) % 4)
+    return fail(SVDQ_ERR_ALIGN, "w4a4_gemm: qa, qwe must be 16-byte aligned, sxp, swp 4-byte aligned");
   // The kernel addresses qa and qwe with 32-bit byte offsets.
-  if ((int64_t)M * K > INT32_MAX || (int64_t)N * K > INT32_MAX)
+  if ((int64_t)M * K > INT32_MAX || (int64_t)N * K > INT32_MAX || (int64_t)M * (K / group) * 4 > INT32_MAX ||
+      (int64_t)N * (K / group) * 4 > INT32_MAX)
     return fail(SVDQ_ERR_SHAPE, "w4a4_gemm: M*K=%lld or N*K=%lld exceeds 2^31-1 bytes; split the call",
                 (long long)M * K, (long long)N * K);
   svdq::GemmParams p = gemm_params(nullptr, sw, mid, splits, l1cat, RTp, bias, M, N, K, y, ldy);
   p.qwe = static_cast<const uint8_t*>(qwe);
   p.qa = static_cast<const uint8_t*>(qa);
-  p.sx = static_cast<const uint16_t*>(sx);
+  p.sxp = static_cast<const uint32_t*>(sxp);
   p.swp = static_cast<const uint32_t*>(swp);
   return launched(svdq::launch_w4a4(p, group, operand, out_f32 == 1, stream), "w4a4_gemm");
 }

@@ -93,31 +93,37 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
 // Operand A (activation codes, 8-bit) comes from the activation pass; operand B is the
 // packed INT4 weight, converted while staging into LDS.  Global loads run two groups ahead
 // in two register sets; LDS is double buffered.
-// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane L
-// of the wave writes LDS bytes [lds + 16 L, lds + 16 L + 16) from base + off.  Issued as
-// inline asm so that the compiler does not order every later LDS read after it (it cannot
-// tell the two LDS stages apart); the kernel waits for it explicitly before its barrier.
+// Global -> LDS DMA (global_load_lds_dword / _dwordx4): lane L of the wave writes its 4 (16)
+// bytes from base + off at LDS address lds + 4 L (16 L); `lds` must be wave-uniform.  Issued
+// as inline asm so that the compiler neither orders later LDS reads after it (it cannot tell
+// the pipeline stages apart) nor counts it in its own waits: the kernel waits explicitly.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
 }
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
 }
 
 // W4A4 GEMM (FP8 or INT8 MFMA on exact integer codes).
 //
 // Block tile 256 x 128, 8 waves in a 4 x 2 grid, wave tile 64 x 64 = 2 x 2 sub-tiles of
-// 32 x 32.  K advances 128 columns per pipeline stage (two groups of 64 or one of 128), two
-// LDS stages.  Both operands are 8-bit codes in HBM (activations from the activation pass,
-// weights expanded once per layer) and go global -> LDS by DMA; only the scales pass
-// through registers.
+// 32 x 32.  K advances 128 columns per pipeline stage (two groups of 64 or one of 128).  A
+// stage is moved global -> LDS entirely by DMA (activation codes, expanded weight codes,
+// both scale operands) into one of two LDS buffers while the other one feeds the MFMAs; each
+// wave issues the same number of DMA instructions per stage and waits for them (vmcnt(0))
+// before the stage barrier.  The hot loop carries almost no address arithmetic: global bases
+// are scalars advanced per stage, per-lane offsets are constants, LDS offsets immediates.
 //
 // LDS operand tiles: rows of 128 bytes = 8 chunks of 16; chunk c of row r sits at chunk
 // position c ^ ((r >> 1) & 7).  The 16 lanes of a ds_read_b128 phase read one logical chunk
 // of 16 consecutive rows and hit 16 distinct 4-bank groups.
 //
 // Per group and sub-tile: P = codes_x . codes_w (exact integer sums, fp32) on the FP8 MFMA,
-// S = sx (x) sw on a bf16 MFMA with K = 2 ((sx, sx) . (hi(sw), lo(sw)) exact), acc += P * S.
+// S = sx (x) sw on a bf16 MFMA with K = 2: A = (sx, sx | finite filler), B = (hi(sw), lo(sw)
+// | zeros), so S = sx hi + sx lo exactly; acc += P * S.
 template <int G, int MODE, bool OUT_F32>
 __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   constexpr int TBM = 256, TBN = 128, NT = 512;
@@ -126,15 +132,15 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   constexpr int KS = G / 64;                  // 64-column MFMA steps per group
   constexpr int ADMA = TBM * KB / (16 * NT);  // A: 16-byte DMA chunks per thread per stage (4)
   constexpr int BDMA = TBN * KB / (16 * NT);  // B: 16-byte DMA chunks per thread per stage (2)
-  constexpr int XS = TBM + 1, WS = TBN + 1;   // scale rows per group (+1 zero row)
-  static_assert(GPS * TBM <= NT && GPS * TBN <= NT, "one scale of each kind per thread");
-  __shared__ __attribute__((aligned(1024))) uint8_t sA[2][TBM * KB];
-  __shared__ __attribute__((aligned(1024))) uint8_t sB[2][TBN * KB];
-  // Scale-MFMA operands, 4 words per row: (pair, 0, 0, 0); the last row is all zero.
-  __shared__ __attribute__((aligned(16))) uint32_t sX[2][GPS][XS * 4];   // pair = (sx, sx)
-  __shared__ __attribute__((aligned(16))) uint32_t sW[2][GPS][WS * 4];   // pair = (hi, lo) of sw
+  constexpr int XS = TBM + 4, WS = TBN + 4;   // scale words per group; the last 4 are zero
+  constexpr int ABUF = TBM * KB, BBUF = TBN * KB;
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[2 * ABUF];
+  __shared__ __attribute__((aligned(1024))) uint8_t sB[2 * BBUF];
+  __shared__ __attribute__((aligned(16))) uint32_t sX[2][GPS][XS];   // (sx, sx) bf16 pairs
+  __shared__ __attribute__((aligned(16))) uint32_t sW[2][GPS][WS];   // (hi, lo) of sw
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
   int bm, bn;
@@ -142,70 +148,68 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   const int m0 = bm * TBM, n0 = bn * TBN;
   const int K = p.K, ngroups = K / G, nstages = (K + KB - 1) / KB;
 
-  // DMA sources: wave w, chunk i covers LDS bytes [(DMA w + i) KB, +1 KB) of a stage tile,
-  // i.e. 8 rows; lane L lands at row 8 (DMA w + i) + L / 8, chunk position L % 8.  Columns
-  // past K (a last stage holding a single group of 64) are clamped to the row's last chunk;
-  // that group's scale is zero.  Offsets are 32-bit (the host bounds the operand sizes).
-  uint32_t aoff[ADMA], boff[BDMA];
-  int alim[ADMA], blim[BDMA];
+  // Operand DMA: wave w, chunk i covers LDS bytes [(DMA w + i) KB, +1 KB) of a stage tile,
+  // i.e. 8 rows; lane L lands at row 8 (DMA w + i) + L / 8, chunk position L % 8 (logical
+  // chunk c = position ^ swizzle).  Per-lane byte offsets: row (clamped to M / N) and chunk.
+  // A last stage holding a single group of 64 clamps its columns to the row's last chunk
+  // (that group is not computed).  Offsets are 32-bit (the host bounds the operand sizes).
+  uint32_t arow_o[ADMA], brow_o[BDMA];
+  int ac16[ADMA], bc16[BDMA];
 #pragma unroll
   for (int i = 0; i < ADMA; ++i) {
-    const int row = 8 * (ADMA * wave + i) + lane / 8, c = (lane % 8) ^ ((row >> 1) & 7);
-    aoff[i] = (uint32_t)min(m0 + row, p.M - 1) * (uint32_t)K + 16 * c;
-    alim[i] = K - 16 - 16 * c;
+    const int row = 8 * (ADMA * wave + i) + lane / 8;
+    ac16[i] = 16 * ((lane % 8) ^ ((row >> 1) & 7));
+    arow_o[i] = (uint32_t)min(m0 + row, p.M - 1) * (uint32_t)K;
   }
 #pragma unroll
   for (int i = 0; i < BDMA; ++i) {
-    const int row = 8 * (BDMA * wave + i) + lane / 8, c = (lane % 8) ^ ((row >> 1) & 7);
-    boff[i] = (uint32_t)min(n0 + row, p.N - 1) * (uint32_t)K + 16 * c;
-    blim[i] = K - 16 - 16 * c;
+    const int row = 8 * (BDMA * wave + i) + lane / 8;
+    bc16[i] = 16 * ((lane % 8) ^ ((row >> 1) & 7));
+    brow_o[i] = (uint32_t)min(n0 + row, p.N - 1) * (uint32_t)K;
   }
-  // Scales: thread t stages sx of row t % TBM for group t / TBM of the stage and sw of
-  // column t % TBN for group t / TBN (threads past GPS * TBN load a duplicate, not stored).
-  const int xj = (tid / TBM) % GPS, xr = tid % TBM, wj = (tid / TBN) % GPS, wr = tid % TBN;
-  const uint32_t xoff = (uint32_t)min(m0 + xr, p.M - 1) * (uint32_t)ngroups;
-  const uint32_t woff = (uint32_t)min(n0 + wr, p.N - 1) * (uint32_t)ngroups;
-  const bool x_live = tid < GPS * TBM, w_live = tid < GPS * TBN;
-  // Zero the padding words 1-3 of every row and the whole last row, once (the pair words of
-  // rows < TBM / TBN are written every stage, by other threads: never touched here).
-  for (int t = tid; t < 2 * GPS * XS; t += NT) {
-    uint32_t* r = &sX[t / (GPS * XS)][(t / XS) % GPS][(t % XS) * 4];
-    if (t % XS == TBM) r[0] = 0u;
-    r[1] = 0u; r[2] = 0u; r[3] = 0u;
+  // Scale DMA (both scale operands are group-major, [K/G, rows]): word slot
+  // t = (64 wave + lane) mod (GPS rows) -> group t / rows, row t % rows; waves past the slot
+  // count load duplicates of the same words into the same places.
+  const int xs = (64 * wave + lane) % (GPS * TBM), ws = (64 * wave + lane) % (GPS * TBN);
+  const int xj = xs / TBM, wj = ws / TBN;
+  const uint32_t xrowc = (uint32_t)min(m0 + xs % TBM, p.M - 1), wrowc = (uint32_t)min(n0 + ws % TBN, p.N - 1);
+  const int xjs = ((64 * wave) % (GPS * TBM)) / TBM, wjs = ((64 * wave) % (GPS * TBN)) / TBN;  // = xj, wj
+  const int xbase = (64 * wave) % (GPS * TBM) % TBM, wbase = (64 * wave) % (GPS * TBN) % TBN;
+  if (tid < 2 * GPS * 4) {
+    sX[tid / (4 * GPS)][(tid / 4) % GPS][TBM + tid % 4] = 0u;
+    sW[tid / (4 * GPS)][(tid / 4) % GPS][TBN + tid % 4] = 0u;
   }
-  for (int t = tid; t < 2 * GPS * WS; t += NT) {
-    uint32_t* r = &sW[t / (GPS * WS)][(t / WS) % GPS][(t % WS) * 4];
-    if (t % WS == TBN) r[0] = 0u;
-    r[1] = 0u; r[2] = 0u; r[3] = 0u;
-  }
+  const uint32_t ldsA = lds_offset(sA), ldsB = lds_offset(sB), ldsX = lds_offset(&sX[0][0][0]),
+                 ldsW = lds_offset(&sW[0][0][0]);
 
-  // Fragment addresses (bytes within a stage tile): the lane's row; chunk c at c ^ sw_.
-  const int sw_ = (lr >> 1) & 7;
-  const int arow = (64 * wm + lr) * 128, brow = (64 * wn + lr) * 128;
-  // Scale-MFMA operand rows: lanes 32-63 (the second half of K) read the zero row.
-  const int xrow = h ? TBM : 64 * wm + lr, wrow = h ? TBN : 64 * wn + lr;
-
-  uint32_t rx, rw;
-  int xg;
-  // Issue the loads of stage `s`: scales into registers, then A and B into LDS buffer `buf`.
-  // The DMA goes last: the compiler does not count it, so any wait it places for its own
-  // loads is ordered before the DMA and never waits for it.
+  // Issue every DMA of stage `s` into buffer `buf`.
   auto gload = [&](int s, int buf) {
-    xg = s * GPS + xj;
-    rx = p.sx[xoff + (uint32_t)min(xg, ngroups - 1)];
-    rw = p.swp[woff + (uint32_t)min(s * GPS + wj, ngroups - 1)];
+    const int col0 = s * KB;
+    const bool tail = col0 + KB > K;   // a last stage with a single group of 64
+    const uint8_t* qa_s = p.qa + col0;
+    const uint8_t* qw_s = p.qwe + col0;
+    const int g0 = s * GPS;
+    const int jmax = ngroups - 1 - g0;   // >= 0
+    const uint32_t* sx_s = p.sxp + (long)g0 * p.M;
+    const uint32_t* sw_s = p.swp + (long)g0 * p.N;
+    dma4(sx_s, 4 * ((uint32_t)min(xj, jmax) * (uint32_t)p.M + xrowc),
+         ldsX + 4 * ((buf * GPS + xjs) * XS + xbase));
+    dma4(sw_s, 4 * ((uint32_t)min(wj, jmax) * (uint32_t)p.N + wrowc),
+         ldsW + 4 * ((buf * GPS + wjs) * WS + wbase));
+    if (!tail) {
 #pragma unroll
-    for (int i = 0; i < ADMA; ++i)
-      dma16(p.qa, aoff[i] + (uint32_t)min(s * KB, alim[i]),
-            __builtin_amdgcn_readfirstlane(lds_offset(&sA[buf][(ADMA * wave + i) * 1024])));
+      for (int i = 0; i < ADMA; ++i) dma16(qa_s, arow_o[i] + ac16[i], ldsA + buf * ABUF + (ADMA * wave + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < BDMA; ++i)
-      dma16(p.qwe, boff[i] + (uint32_t)min(s * KB, blim[i]),
-            __builtin_amdgcn_readfirstlane(lds_offset(&sB[buf][(BDMA * wave + i) * 1024])));
-  };
-  auto lstore = [&](int buf) {
-    if (x_live) sX[buf][xj][4 * xr] = xg < ngroups ? rx * 0x10001u : 0u;
-    if (w_live) sW[buf][wj][4 * wr] = rw;
+      for (int i = 0; i < BDMA; ++i) dma16(qw_s, brow_o[i] + bc16[i], ldsB + buf * BBUF + (BDMA * wave + i) * 1024);
+    } else {
+      const int lim = K - col0 - 16;
+#pragma unroll
+      for (int i = 0; i < ADMA; ++i)
+        dma16(qa_s, arow_o[i] + min(ac16[i], lim), ldsA + buf * ABUF + (ADMA * wave + i) * 1024);
+#pragma unroll
+      for (int i = 0; i < BDMA; ++i)
+        dma16(qw_s, brow_o[i] + min(bc16[i], lim), ldsB + buf * BBUF + (BDMA * wave + i) * 1024);
+    }
   };
 
   f32x16 acc[2][2];
@@ -214,30 +218,46 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  // Operands of one group: A/B fragments of the wave's 2x2 sub-tiles and the scale-MFMA
-  // operands.
+  // Fragment byte offsets within a stage tile: logical chunk c = u + 2h of the lane's row,
+  // u = 4 (G/64 gi + ks) + t in {0, 1, 4, 5}, stored at chunk position c ^ swizzle.
+  const int sw_ = (lr >> 1) & 7;
+  int fa[4], fb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int u = 4 * (q >> 1) + (q & 1);
+    fa[q] = (64 * wm + lr) * 128 + 16 * ((u + 2 * h) ^ sw_);
+    fb[q] = (64 * wn + lr) * 128 + 16 * ((u + 2 * h) ^ sw_);
+  }
+  // Scale-MFMA operands: A reads 4 words from the lane's row (word 0 = its pair, the rest
+  // finite filler); B holds the pair in word 0 for lanes 0-31 and is zero otherwise.
+  const int xo = 4 * (64 * wm + lr);
+  const int wo0 = 4 * (h ? TBN : 64 * wn + lr), wo1 = 4 * (h ? TBN : 64 * wn + 32 + lr);
+  u32x4 wop[2] = {u32x4{}, u32x4{}};
+
   struct Frag {
     u32x4 a[2][KS][2], b[2][KS][2];
-    u32x4 x[2], w[2];
+    u32x4 x[2];
   };
   auto read_frag = [&](Frag& f, int buf, int gi) {
+    const uint8_t* a0 = sA + buf * ABUF;
+    const uint8_t* b0 = sB + buf * BBUF;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        // logical chunk c = G/16 gi + 4 ks + 2 h + t of the lane's rows, stored at c ^ sw_
-        const int pc = 16 * ((G / 16 * gi + 4 * ks + 2 * h + t) ^ sw_);
+        const int q = 2 * (G / 64 * gi + ks) + t;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          f.a[i][ks][t] = ld16(&sA[buf][arow + 4096 * i + pc]);
-          f.b[i][ks][t] = ld16(&sB[buf][brow + 4096 * i + pc]);
+          f.a[i][ks][t] = ld16(a0 + fa[q] + 4096 * i);
+          f.b[i][ks][t] = ld16(b0 + fb[q] + 4096 * i);
         }
       }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      f.x[i] = ld16(&sX[buf][gi][4 * (xrow + (h ? 0 : 32 * i))]);
-      f.w[i] = ld16(&sW[buf][gi][4 * (wrow + (h ? 0 : 32 * i))]);
-    }
+    const uint8_t* x0 = reinterpret_cast<const uint8_t*>(&sX[buf][gi][0]);
+    const uint8_t* w0 = reinterpret_cast<const uint8_t*>(&sW[buf][gi][0]);
+    f.x[0] = ld16(x0 + xo);
+    f.x[1] = ld16(x0 + xo + 128);
+    wop[0][0] = *reinterpret_cast<const uint32_t*>(w0 + wo0);
+    wop[1][0] = *reinterpret_cast<const uint32_t*>(w0 + wo1);
   };
   auto mfma_p = [&](const Frag& f, int i, int j) {
     f32x16 pf;
@@ -278,8 +298,8 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
       cp[t] = mfma_p(f, i, j);
       f32x16& a = t == 0 ? acc[1][1] : acc[TI[t - 1]][TJ[t - 1]];
       fma16(a, t == 0 ? pp : cp[t - 1], t == 0 ? ps : cs[t - 1]);
-      asm volatile("" : "+v"(a), "+v"(f.x[i]), "+v"(f.w[j]));
-      cs[t] = mfma_bf16_32x32x16(f.x[i], f.w[j], f32x16{});
+      asm volatile("" : "+v"(a), "+v"(f.x[i]), "+v"(wop[j]));
+      cs[t] = mfma_bf16_32x32x16(f.x[i], wop[j], f32x16{});
       if (t < 3) {
         const int ni = TI[t + 1], nj = TJ[t + 1];
         asm volatile("" : "+v"(f.a[ni][0][0]), "+v"(f.a[ni][0][1]), "+v"(f.b[nj][0][0]), "+v"(f.b[nj][0][1]));
@@ -288,26 +308,26 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
     pp = cp[3];
     ps = cs[3];
   };
-
-  // Two LDS stages: stage s + 1 is loaded while stage s computes.  Loads are unconditional
-  // (stage index clamped).
-  gload(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  lstore(0);
-  __syncthreads();
-  for (int s = 0; s < nstages; ++s) {
-    const int buf = s & 1;
+  // One stage: prefetch stage s + 1 into the other buffer, compute stage s, wait, barrier.
+  auto stage = [&](int s, int buf) {
     gload(min(s + 1, nstages - 1), buf ^ 1);
 #pragma unroll
     for (int gi = 0; gi < GPS; ++gi) {
+      if (gi > 0 && s * GPS + gi >= ngroups) break;   // K has an odd number of groups of 64
       Frag f;
       read_frag(f, buf, gi);
       group(f);
     }
-    // All of stage s + 1 has to land before the barrier.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    lstore(buf ^ 1);
     __syncthreads();
+  };
+
+  gload(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int s = 0; s < nstages; s += 2) {   // unrolled by two: buffer offsets are immediates
+    stage(s, 0);
+    if (s + 1 < nstages) stage(s + 1, 1);
   }
   fma16(acc[1][1], pp, ps);
 
@@ -326,12 +346,14 @@ __global__ void weight_operand_kernel(const uint32_t* __restrict__ qw, u32x2* __
 }
 
 // Weight-scale operand of the W4A4 scale MFMA, once per layer: (bf16 hi, bf16 lo) of the fp16
-// scale, hi + lo == scale exactly; MODE 1 (int8 16*q operands) folds in 1/256.
-__global__ void weight_scale_pairs_kernel(const uint16_t* __restrict__ sw, uint32_t* __restrict__ out, long n,
-                                          float mult) {
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) {
-    const float f = half_bits_to_float(sw[i]) * mult;
+// scale, hi + lo == scale exactly; MODE 1 (int8 16*q operands) folds in 1/256.  Written
+// group-major, out[g][n] (the GEMM stages one group's scales of consecutive columns).
+__global__ void weight_scale_pairs_kernel(const uint16_t* __restrict__ sw, uint32_t* __restrict__ out, int n,
+                                          int ngroups, float mult) {
+  const long total = (long)n * ngroups;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    const long g = i / n, c = i % n;
+    const float f = half_bits_to_float(sw[c * ngroups + g]) * mult;
     const uint32_t hi = pack_bf16x2(f, 0.0f) & 0xFFFFu;
     const uint32_t lo = pack_bf16x2(f - bf16lo(hi), 0.0f) & 0xFFFFu;
     out[i] = hi | (lo << 16);
@@ -454,8 +476,9 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, long n, int mode, hipStream_t st) {
-  weight_scale_pairs_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(sw, out, n, mode == 0 ? 1.0f : 1.0f / 256.0f);
+hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, int n, int ngroups, int mode, hipStream_t st) {
+  const long blocks = std::min<long>(((long)n * ngroups + 255) / 256, 8192);
+  weight_scale_pairs_kernel<<<(unsigned)blocks, 256, 0, st>>>(sw, out, n, ngroups, mode == 0 ? 1.0f : 1.0f / 256.0f);
   return hipGetLastError();
 }
 

@@ -16,23 +16,24 @@ struct ActParams {
   int M, K, RTp;            // RTp: row stride of mid (>= r + rl, multiple of 32)
   uint8_t* qx;              // [M, K/2] canonical packed codes (optional)
   uint8_t* qa;              // [M, K] 8-bit GEMM operand codes (quantizing modes)
-  uint16_t* sx;             // [M, K/G] bf16
+  uint16_t* sx;             // [M, K/G] bf16, or [K/G, M] u32 (sx, sx) pairs when sx_pairs
   uint16_t* xhat;           // [M, ldxh] bf16 (null unless requested)
   long ldxh;
   float* mid;               // [S, M, RTp]: one partial per K split (summed by the GEMM)
   int gps;                  // K-groups per split
   int exact;                // 1: IEEE division for x / s everywhere
+  int sx_pairs;             // 1: sx as u32 bf16 pairs
 };
 
 struct GemmParams {
   const uint8_t* qa;        // W4A4: [M, K] 8-bit activation operand codes
-  const uint16_t* sx;       // W4A4: [M, K/G] bf16 activation scales
+  const uint32_t* sxp;      // W4A4: [K/G, M] activation scales as u32 bf16 pairs (sx, sx)
   const uint16_t* xhat;     // W4A16: [M, ldxh] bf16 smoothed activations
   long ldxh;
   const uint8_t* qw;        // [N, K/2] packed weight codes (W4A16)
   const uint8_t* qwe;       // [N, K] 8-bit weight operand codes (W4A4)
   const uint16_t* sw;       // [N, K/G] fp16 weight scales (W4A16)
-  const uint32_t* swp;      // [N, K/G] (bf16 hi, bf16 lo) pairs of the weight scales (W4A4)
+  const uint32_t* swp;      // [K/G, N] (bf16 hi, bf16 lo) pairs of the weight scales (W4A4)
   const float* mid;         // [S, M, RTp] f32 low-rank/LoRA down projections, per K split
   int splits;               // S
   const uint16_t* l1cat;    // [N, RTp] bf16 up projections (zero padded)
@@ -49,7 +50,7 @@ hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, in
 hipError_t launch_prepare_smooth(const uint16_t* s, float* srs, int K, hipStream_t st);
 // mode: 0 = e4m3 operands on the FP8 MFMA, 1 = int8 operands on the INT8 MFMA
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st);
-hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, long n, int mode, hipStream_t st);
+hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, int n, int ngroups, int mode, hipStream_t st);
 hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, long ndwords, int mode, hipStream_t st);
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st);
 

@@ -38,7 +38,7 @@ class PreparedLayer:
     lora_mult: Optional[Tensor]  # f32 [rl]
     qweight: Tensor              # uint8 [N, Kp/2]
     weight_scales: Tensor        # fp16 [N, Kp/G]
-    scale_pairs: dict            # operand code -> int32 [N, Kp/G] W4A4 scale-MFMA operand (lazy)
+    scale_pairs: dict            # operand code -> int32 [Kp/G, N] W4A4 scale-MFMA operand (lazy)
     operands: dict               # operand code -> uint8 [N, Kp] W4A4 weight operand codes (lazy)
     bias: Optional[Tensor]       # bf16 [N]
     group_size: int
@@ -164,7 +164,7 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
             raise ValueError(f"operand must be 'e4m3' or 'i8', got {operand!r}")
         opc = ops.OPERAND_NAMES[operand]
         qa, sx, _, _, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
-                                          prep.group_size, prep.rtp, opc, False, False, exact_div)
+                                          prep.group_size, prep.rtp, opc, False, False, exact_div, True)
         y = ops.w4a4_gemm(qa, sx, prep.weight_operand(opc), prep.weight_scale_pairs(opc), mid, prep.l1cat,
                           prep.bias, prep.group_size, opc, out_f32)
     elif mode == "w4a16":

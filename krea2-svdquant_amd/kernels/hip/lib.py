@@ -21,6 +21,7 @@ SVDQ_ACT_XHAT = 2
 SVDQ_ACT_EXACT_DIV = 4
 SVDQ_ACT_OPERAND_E4M3 = 8
 SVDQ_ACT_OPERAND_I8 = 16
+SVDQ_ACT_SX_PAIRS = 32
 
 STATUS = {0: "SVDQ_OK", -1: "SVDQ_ERR_ARG", -2: "SVDQ_ERR_SHAPE", -3: "SVDQ_ERR_ALIGN",
           -4: "SVDQ_ERR_UNSUPPORTED", -5: "SVDQ_ERR_LAUNCH"}
@@ -39,7 +40,7 @@ SIGNATURES = {
     "svdq_act_quant_workspace": (_I, [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_L)]),
     "svdq_act_quant": (_I, [_P, _L, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _U, _P, _P, _P, _P, _L,
                             _P, _I, _P]),
-    "svdq_prepare_weight_scales": (_I, [_P, _P, _L, _I, _P]),
+    "svdq_prepare_weight_scales": (_I, [_P, _P, _I, _I, _I, _P]),
     "svdq_prepare_weight_operand": (_I, [_P, _P, _I, _I, _I, _P]),
     "svdq_w4a4_gemm": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
     "svdq_w4a16_gemm": (_I, [_P, _L, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),

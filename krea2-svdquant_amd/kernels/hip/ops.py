@@ -59,19 +59,21 @@ OPERAND_NONE, OPERAND_E4M3, OPERAND_I8 = -1, 0, 1
 
 @torch.library.custom_op("svdq::prepare_weight_scales", mutates_args=())
 def prepare_weight_scales(weight_scales: Tensor, operand: int) -> Tensor:
-    """[N, K/G] uint32 (bf16 hi | bf16 lo << 16) operand of the W4A4 scale MFMA, per layer."""
+    """[K/G, N] uint32 (bf16 hi | bf16 lo << 16) operand of the W4A4 scale MFMA, per layer
+    (group-major: the transpose of the checkpoint's [N, K/G] fp16 ``weight_scales``)."""
     _need(weight_scales.is_cuda, RuntimeError, "svdq::prepare_weight_scales needs a GPU tensor")
     _check_dev("weight_scales", weight_scales, weight_scales.device, torch.float16)
+    _need(weight_scales.dim() == 2, ValueError, f"weight_scales must be [N, K/G], got {tuple(weight_scales.shape)}")
     _need(operand in (OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
-    out = torch.empty(weight_scales.shape, dtype=torch.int32, device=weight_scales.device)
-    lib.call("svdq_prepare_weight_scales", _vp(weight_scales), _vp(out), weight_scales.numel(), operand,
-             _stream(weight_scales.device))
+    n, ng = weight_scales.shape
+    out = torch.empty((ng, n), dtype=torch.int32, device=weight_scales.device)
+    lib.call("svdq_prepare_weight_scales", _vp(weight_scales), _vp(out), n, ng, operand, _stream(weight_scales.device))
     return out
 
 
 @prepare_weight_scales.register_fake
 def _(weight_scales, operand):
-    return weight_scales.new_empty(weight_scales.shape, dtype=torch.int32)
+    return weight_scales.new_empty((weight_scales.shape[1], weight_scales.shape[0]), dtype=torch.int32)
 
 
 @torch.library.custom_op("svdq::prepare_weight_operand", mutates_args=())
@@ -97,14 +99,16 @@ OPERAND_NAMES = {"e4m3": OPERAND_E4M3, "fp8": OPERAND_E4M3, "i8": OPERAND_I8, "i
 @torch.library.custom_op("svdq::act_quant", mutates_args=())
 def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
               lora_mult: Optional[Tensor], group_size: int, rtp: int, operand: int, packed: bool,
-              want_xhat: bool, exact: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+              want_xhat: bool, exact: bool, sx_pairs: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Smoothing + A4 quantization + low-rank / LoRA down projections, one pass over x.
 
     ``operand`` selects the W4A4 GEMM operand codes written (``OPERAND_E4M3`` / ``OPERAND_I8``)
     or none (``OPERAND_NONE``: x_hat only, the W4A16 path).  Returns
     ``(qa uint8 [M, K], sx bf16 [M, K/G], qx uint8 [M, K/2], xhat bf16 [M, K], mid f32 [S, M, rtp])``
     where ``mid`` holds one partial per K split (the GEMM adds them); outputs not requested are
-    empty tensors (``qx`` needs ``packed``, ``xhat`` ``want_xhat``).
+    empty tensors (``qx`` needs ``packed``, ``xhat`` ``want_xhat``).  With ``sx_pairs`` the
+    scales come as int32 [K/G, M] (group-major) bf16 pairs (bits | bits << 16), the form
+    ``w4a4_gemm`` takes.
     """
     _need(x.is_cuda, RuntimeError, "svdq::act_quant needs a GPU tensor")
     dev = x.device
@@ -127,17 +131,19 @@ def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
     _need(k % group_size == 0, ValueError, f"K={k} must be a multiple of group_size={group_size}")
     _need(operand in (OPERAND_NONE, OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
     quant = operand != OPERAND_NONE
+    _need(quant or not sx_pairs, ValueError, "sx_pairs needs an operand format")
 
     splits = _splits(m, k, group_size, rtp)
     qa = torch.empty((m, k) if quant else (0,), dtype=torch.uint8, device=dev)
-    sx = torch.empty((m, k // group_size) if quant else (0,), dtype=torch.bfloat16, device=dev)
+    sx_shape = ((k // group_size, m) if sx_pairs else (m, k // group_size)) if quant else (0,)
+    sx = torch.empty(sx_shape, dtype=torch.int32 if sx_pairs else torch.bfloat16, device=dev)
     qx = torch.empty((m, k // 2) if packed else (0,), dtype=torch.uint8, device=dev)
     xhat = torch.empty((m, k) if want_xhat else (0,), dtype=torch.bfloat16, device=dev)
     mid = torch.empty((splits, m, rtp), dtype=torch.float32, device=dev)
     flags = ((lib.SVDQ_ACT_OPERAND_E4M3 if operand == OPERAND_E4M3 else 0)
              | (lib.SVDQ_ACT_OPERAND_I8 if operand == OPERAND_I8 else 0)
              | (lib.SVDQ_ACT_PACKED if packed else 0) | (lib.SVDQ_ACT_XHAT if want_xhat else 0)
-             | (lib.SVDQ_ACT_EXACT_DIV if exact else 0))
+             | (lib.SVDQ_ACT_EXACT_DIV if exact else 0) | (lib.SVDQ_ACT_SX_PAIRS if sx_pairs else 0))
     lib.call("svdq_act_quant", _vp(x), k, _vp(srs), _vp(l2), r, _vp(lora_down), rl, _vp(lora_mult),
              m, k, group_size, rtp, flags, _vp(qa) if quant else None, _vp(sx) if quant else None,
              _vp(qx) if packed else None, _vp(xhat) if want_xhat else None, k, _vp(mid), splits,
@@ -146,11 +152,12 @@ def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
 
 
 @act_quant.register_fake
-def _(x, srs, l2, lora_down, lora_mult, group_size, rtp, operand, packed, want_xhat, exact):
+def _(x, srs, l2, lora_down, lora_mult, group_size, rtp, operand, packed, want_xhat, exact, sx_pairs=False):
     m, k = x.shape
     quant = operand != OPERAND_NONE
     qa = x.new_empty((m, k) if quant else (0,), dtype=torch.uint8)
-    sx = x.new_empty((m, k // group_size) if quant else (0,), dtype=torch.bfloat16)
+    sx_shape = ((k // group_size, m) if sx_pairs else (m, k // group_size)) if quant else (0,)
+    sx = x.new_empty(sx_shape, dtype=torch.int32 if sx_pairs else torch.bfloat16)
     qx = x.new_empty((m, k // 2) if packed else (0,), dtype=torch.uint8)
     xhat = x.new_empty((m, k) if want_xhat else (0,), dtype=torch.bfloat16)
     return qa, sx, qx, xhat, x.new_empty((_splits(m, k, group_size, rtp), m, rtp), dtype=torch.float32)
@@ -195,37 +202,38 @@ def _check_gemm(qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tens
 
 
 @torch.library.custom_op("svdq::w4a4_gemm", mutates_args=())
-def w4a4_gemm(qa: Tensor, sx: Tensor, weight_operand: Tensor, weight_scale_pairs: Tensor, mid: Tensor,
+def w4a4_gemm(qa: Tensor, sx_pairs: Tensor, weight_operand: Tensor, weight_scale_pairs: Tensor, mid: Tensor,
               l1cat: Tensor, bias: Optional[Tensor], group_size: int, operand: int, out_f32: bool) -> Tensor:
     """``y = sum_g sx sw (qa . qw)_g + mid @ l1cat^T + bias`` (bf16 or float32 output).
 
-    ``weight_operand`` and ``weight_scale_pairs`` come from ``prepare_weight_operand`` and
-    ``prepare_weight_scales`` with the same ``operand``.
+    ``sx_pairs`` comes from ``act_quant(..., sx_pairs=True)``; ``weight_operand`` and
+    ``weight_scale_pairs`` from ``prepare_weight_operand`` and ``prepare_weight_scales`` with
+    the same ``operand``.
     """
     _need(qa.is_cuda, RuntimeError, "svdq::w4a4_gemm needs GPU tensors")
     dev = qa.device
     _check_dev("qa", qa, dev, torch.uint8)
     m, k = qa.shape
-    _check_dev("sx", sx, dev, torch.bfloat16)
-    _need(tuple(sx.shape) == (m, k // group_size), ValueError, "sx must be [M, K/G]")
+    _check_dev("sx_pairs", sx_pairs, dev, torch.int32)
+    _need(tuple(sx_pairs.shape) == (k // group_size, m), ValueError, "sx_pairs must be [K/G, M]")
     _need(operand in (OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
     _check_dev("weight_operand", weight_operand, dev, torch.uint8)
     _need(weight_operand.dim() == 2 and weight_operand.shape[1] == k, ValueError,
           f"weight_operand must be [N, {k}], got {tuple(weight_operand.shape)}")
     _check_dev("weight_scale_pairs", weight_scale_pairs, dev, torch.int32)
     n = weight_operand.shape[0]
-    _need(tuple(weight_scale_pairs.shape) == (n, k // group_size), ValueError,
-          f"weight_scale_pairs must be [{n}, {k // group_size}], got {tuple(weight_scale_pairs.shape)}")
+    _need(tuple(weight_scale_pairs.shape) == (k // group_size, n), ValueError,
+          f"weight_scale_pairs must be [{k // group_size}, {n}], got {tuple(weight_scale_pairs.shape)}")
     _check_epilogue(mid, l1cat, bias, m, n, dev)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
-    lib.call("svdq_w4a4_gemm", _vp(qa), operand, _vp(sx), _vp(weight_operand), _vp(weight_scale_pairs), _vp(mid),
+    lib.call("svdq_w4a4_gemm", _vp(qa), operand, _vp(sx_pairs), _vp(weight_operand), _vp(weight_scale_pairs), _vp(mid),
              mid.shape[0], _vp(l1cat), mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32),
              _stream(dev))
     return y
 
 
 @w4a4_gemm.register_fake
-def _(qa, sx, weight_operand, weight_scale_pairs, mid, l1cat, bias, group_size, operand, out_f32):
+def _(qa, sx_pairs, weight_operand, weight_scale_pairs, mid, l1cat, bias, group_size, operand, out_f32):
     return qa.new_empty((qa.shape[0], weight_operand.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)
 
 

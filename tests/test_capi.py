@@ -88,7 +88,7 @@ def test_prepare_entry_points_reject_bad_arguments_before_any_launch():
         lib.call("svdq_prepare_weight_operand", fake, ctypes.c_void_p(0x1004), 128, 128, 0, nul)
     assert ei.value.status == -3
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_prepare_weight_scales", fake, fake, 0, 0, nul)
+        lib.call("svdq_prepare_weight_scales", fake, fake, 0, 96, 0, nul)
     assert ei.value.status == -1
 
 

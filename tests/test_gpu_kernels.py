@@ -29,14 +29,14 @@ def _ops():
     return backend, ops
 
 
-def _run_act(x_np, st, dev, operand="e4m3", packed=True, xhat=False, exact=False, adapters=True):
+def _run_act(x_np, st, dev, operand="e4m3", packed=True, xhat=False, exact=False, adapters=True, sx_pairs=False):
     """Returns (qa, sx, qx, xhat, mid) from svdq::act_quant."""
     backend, ops = _ops()
     prep = backend.prepare_layer(to_device_state(st, dev), device_adapters(st, dev) if adapters else (), dev)
     x = bf16_tensor(x_np, dev)
     opc = ops.OPERAND_NONE if operand is None else ops.OPERAND_NAMES[operand]
     out = ops.act_quant(x, prep.srs, prep.l2, prep.lora_down, prep.lora_mult, st.group_size, prep.rtp,
-                        opc, packed, xhat, exact)
+                        opc, packed, xhat, exact, sx_pairs)
     torch.cuda.synchronize()
     return out, prep
 
@@ -48,7 +48,7 @@ def test_w4a4_gemm_layout_identity(dev):
     q = np.zeros((m, k), np.int8)
     q[np.arange(m), np.arange(m)] = 1
     qw = ((np.arange(n)[:, None] * 7 + np.arange(k)[None, :] * 3) % 15 - 7).astype(np.int8)
-    sx = bf16_tensor(np.ones((m, 1), np.float32), dev)
+    sx = torch.full((1, m), 0x3F803F80, dtype=torch.int32, device=dev)   # bf16 pair (1.0, 1.0), [K/G, M]
     qwt = torch.from_numpy(op.pack_int4(qw)).to(dev)
     sw = torch.ones((n, 1), dtype=torch.float16, device=dev)
     mid = torch.zeros((1, m, 32), dtype=torch.float32, device=dev)
@@ -84,6 +84,9 @@ def test_act_quant_golden_bit_exact(dev, name):
     assert np.array_equal(bf16_bits_of(xh), fx["xhat"])
     codes = op.unpack_int4(fx["qx_packed"])
     assert np.array_equal(qa.cpu().numpy(), operand_bytes(codes, "e4m3"))
+    (_, sxp, _, _, _), _ = _run_act(x, st, dev, operand="e4m3", packed=False, sx_pairs=True)
+    bits = fx["sx"].astype(np.uint32)
+    assert np.array_equal(sxp.cpu().numpy().view(np.uint32), (bits | (bits << 16)).T)
     (qa8, sx8, qx8, _, _), _ = _run_act(x, st, dev, operand="i8", packed=True)
     assert np.array_equal(qa8.cpu().numpy(), operand_bytes(codes, "i8"))
     assert np.array_equal(qx8.cpu().numpy(), fx["qx_packed"]) and np.array_equal(bf16_bits_of(sx8), fx["sx"])
