@@ -1,24 +1,35 @@
-"""Benchmark of the W4A4 SVDQuantLinear forward on one MI355X (BASELINE metric).
+"""Benchmark of the W4A4 SVDQuantLinear forward on one MI355X (the BASELINE metric).
 
 Workload (the shape the metric is quoted on): the ff.up linear of a
 Krea-2 block, M=4096 tokens (1024x1024 latent), K=6144 -> N=16384, rank 32, group 64, W4A4.
 Synthetic inputs: X bf16 ~ N(0,1) with 1% outlier channels x20; W fp32 ~ N(0, 0.02) quantized
-on the GPU by the package converter (smoothing, rank-32 SVD, INT4 residual).
+on the GPU by the package converter (smoothing, rank-32 SVD, INT4 residual), random init.
 
-A step is one full layer forward (activation pass + W4A4 GEMM with the low-rank epilogue),
-inputs resident in HBM.  ``value`` = effective TOPS = 2*M*N*K / step time.  ``roofline``
-prices the dominant kernel (the W4A4 GEMM) against the INT8 dense MFMA peak, with its
-average duration measured by HIP events on the stream the kernel runs on.  ``cpu_baseline``
-times the oracle's restatement of the reference ``pytorch_sim`` forward on the host CPU on a
-bounded row sample of the same layer.
+A step is one full layer forward (activation pass + W4A4 GEMM with the low-rank epilogue)
+with its inputs resident in HBM.  ``value`` = effective TOPS = 2*M*N*K / step time.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+``roofline`` prices the dominant kernel, the W4A4 GEMM, against the MI355X dense FP8 / INT8
+MFMA peak (5.0 P(FL)OP/s; the GEMM runs exact INT4 codes on the FP8 MFMA).  Its average launch
+duration is measured here with HIP events on the stream the kernel is launched on (torch's
+current stream, which the custom ops use).  ``traffic`` (HBM bytes per launch) comes from the
+rocprofv3 FETCH_SIZE / WRITE_SIZE passes committed in profiles/w4a4_gemm_ffup_traffic.md
+(run ``bench.py --pmc-pass`` under rocprofv3), scaled by the copy-kernel calibration recorded
+there; it is null when that summary is absent.
+
+``cpu_baseline`` times the oracle's restatement of the reference ``pytorch_sim`` forward
+(quant/svd.py:119-163) on the host CPU for the whole layer (~10-30 s of CPU work), and the
+restated activation quantizer (quant/pack.py:6-23) on its own line.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu-baseline] [--no-block]
+    rocprofv3 --pmc FETCH_SIZE -- python bench.py --pmc-pass      (counter pass, no timing)
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -27,22 +38,30 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "W4A4 SVDQuantLinear eff. TOPS @M4096 K6144 N16384; ms/denoise step @1024px"
-INT8_PEAK_TOPS = 5000.0   # MI355X dense INT8 MFMA, 5.0 POP/s
+MFMA_PEAK_TFLOPS = 5000.0   # MI355X dense FP8 / INT8 MFMA
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_SUMMARY = ROOT / "profiles" / "w4a4_gemm_ffup_traffic.md"
+# (name, N, K) of the 8 quantized linears of one Krea-2 block
+BLOCK_SHAPES = [("to_q", 6144, 6144), ("to_gate", 6144, 6144), ("to_k", 1536, 6144), ("to_v", 1536, 6144),
+                ("to_out.0", 6144, 6144), ("ff.gate", 16384, 6144), ("ff.up", 16384, 6144),
+                ("ff.down", 6144, 16384)]
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--m", type=int, default=4096)
     ap.add_argument("--k", type=int, default=6144)
     ap.add_argument("--n", type=int, default=16384)
     ap.add_argument("--rank", type=int, default=32)
     ap.add_argument("--group", type=int, default=64)
-    ap.add_argument("--cpu-rows", type=int, default=256)
+    ap.add_argument("--cpu-reps", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-block", action="store_true", help="skip the 8-shape block line")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="counter pass for rocprofv3: one copy kernel of known size, then GEMM launches")
     return ap.parse_args()
 
 
@@ -50,68 +69,135 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_loop(fn, iters: int) -> float:
-    """Average ms per call of ``fn`` over ``iters`` calls, HIP events on the current stream."""
+def time_avg(fn, iters: int, reps: int = 3) -> float:
+    """ms per call of ``fn``: HIP events around ``iters`` back-to-back calls on torch's current
+    stream (where the ops launch), so host dispatch overlaps the GPU work; median of ``reps``."""
     import torch
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(iters):
-        fn()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / iters
+    out = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b) / iters)
+    return statistics.median(out)
 
 
-def cpu_baseline(ds, x_dev, rows: int) -> dict:
-    """The restated reference pytorch_sim forward (oracle) on the host CPU, bounded row sample."""
+def make_layer(n: int, k: int, m: int, r: int, g: int, dev, seed: int):
+    """Synthetic BASELINE layer: X with outlier channels, W ~ N(0, 0.02), converted on the GPU."""
+    import torch
+    from krea2_svdquant_amd.kernels.hip import backend
+    from krea2_svdquant_amd.quant.convert import convert_linear
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(m, k, device=dev, generator=gen)
+    outliers = torch.randperm(k, device=dev, generator=gen)[: round(0.01 * k)]
+    x[:, outliers] *= 20.0
+    x = x.to(torch.bfloat16)
+    w = torch.randn(n, k, device=dev, generator=gen) * 0.02
+    ds = convert_linear(w, None, x.float().abs().amax(0), rank=r, group_size=g, smooth_clamp=(None, None),
+                        seed=seed + 2)
+    del w
+    return x, ds, backend.prepare_layer(ds, (), dev)
+
+
+def read_traffic() -> int | None:
+    """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary, if present."""
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", TRAFFIC_SUMMARY.read_text())
+    return int(m.group(1)) if m else None
+
+
+def cpu_baseline(ds, x_dev, reps: int) -> dict:
+    """The restated reference pytorch_sim forward (oracle, bf16 CPU torch) over the whole layer."""
     import torch
     from oracle import sim
 
+    torch.set_num_threads(os.cpu_count() or 1)
     f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
     st = sim.LayerState(smooth=f(ds.smooth_scale), qweight=ds.qweight.cpu().numpy(),
                         weight_scales=f(ds.weight_scales), l1=f(ds.l1), l2=f(ds.l2), bias=None,
                         group_size=ds.group_size, shape=tuple(ds.original_shape))
-    x = x_dev[:rows].cpu()
-    threads = torch.get_num_threads()
-    sim.sim_forward_torch(x[:8], st)            # warm-up (allocations, thread pool)
+    x = x_dev.cpu()
+    m, k = x.shape
+    n = st.shape[0]
+    sim.sim_forward_torch(x[:64], st)            # warm-up (allocations, thread pool)
     times = []
-    for _ in range(2):
+    for _ in range(reps):
         t0 = time.perf_counter()
         sim.sim_forward_torch(x, st)
         times.append(time.perf_counter() - t0)
-    t = min(times)
-    m, k = x.shape
-    n = st.shape[0]
-    return {"value": round(2.0 * m * n * k / t / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"oracle sim_forward_torch (reference pytorch_sim, bf16 CPU torch) on {m} of the "
-                      f"{x_dev.shape[0]} rows, K={k} N={n}; best of 2 after warm-up; {t:.2f} s per call"}
+    t = statistics.median(times)
+    xq = x.float().numpy()
+    t0 = time.perf_counter()
+    sim.quantize_activations(xq, st)
+    tq = time.perf_counter() - t0
+    return {"value": round(2.0 * m * n * k / t / 1e12, 4), "unit": "TOPS", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"whole layer M={m} K={k} N={n}: oracle sim_forward_torch (restated reference pytorch_sim, "
+                      f"bf16 CPU torch), median of {reps} after warm-up = {t:.3f} s per forward; restated A4 "
+                      f"activation quantizer (numpy, 1 thread) {tq:.3f} s; os.cpu_count()={os.cpu_count()}",
+            "act_quant_s": round(tq, 3)}
+
+
+def block_line(args, dev) -> dict:
+    """ms per block of the 8 W4A4 linears of config 1 at M=4096 (each timed alone, summed)."""
+    import torch
+    from krea2_svdquant_amd.kernels.hip import backend
+    out, total, ops_total = {}, 0.0, 0.0
+    for i, (name, n, k) in enumerate(BLOCK_SHAPES):
+        x, _, prep = make_layer(n, k, args.m, args.rank, args.group, dev, seed=100 + 10 * i)
+        for _ in range(3):
+            backend.forward_prepared(x, prep, mode="w4a4")
+        ms = time_avg(lambda: backend.forward_prepared(x, prep, mode="w4a4"), 20)
+        out[name] = round(ms, 4)
+        total += ms
+        ops_total += 2.0 * args.m * n * k
+        del x, prep
+        torch.cuda.empty_cache()
+    return {"ms_per_layer": out, "ms_per_block_linears": round(total, 4),
+            "eff_TOPS": round(ops_total / (total * 1e-3) / 1e12, 2),
+            "linears_ms_per_denoise_step_28_blocks": round(28 * total, 3),
+            "note": "W4A4 linears only (M=4096, no text tokens, no attention / norms): the part of the "
+                    "denoise step this backend replaces"}
 
 
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: every GPU box of this build has a single MI355X, and the "
-              "SVDQuantLinear path has no collective (a multi-GPU layout is described in DESIGN.md).",
+              "SVDQuantLinear path has no collective (the multi-GPU layout is described in DESIGN.md).",
               file=sys.stderr)
         return 2
     import torch
     from krea2_svdquant_amd.kernels.hip import backend, ops
-    from krea2_svdquant_amd.quant.convert import convert_linear
 
     dev = torch.device("cuda:0")
     m, k, n, r, g = args.m, args.k, args.n, args.rank, args.group
     log(f"device {torch.cuda.get_device_name(dev)}; building state M={m} K={k} N={n} r={r} g={g}")
-    gen = torch.Generator(device=dev).manual_seed(1)
-    x = torch.randn(m, k, device=dev, generator=gen)
-    outliers = torch.randperm(k, device=dev, generator=gen)[: round(0.01 * k)]
-    x[:, outliers] *= 20.0
-    x = x.to(torch.bfloat16)
-    w = torch.randn(n, k, device=dev, generator=gen) * 0.02
-    ds = convert_linear(w, None, x.float().abs().amax(0), rank=r, group_size=g, smooth_clamp=(None, None), seed=3)
-    del w
-    prep = backend.prepare_layer(ds, (), dev)
+    x, ds, prep = make_layer(n, k, m, r, g, dev, seed=1)
+    opc = ops.OPERAND_E4M3
+    wop, wsp = prep.weight_operand(opc), prep.weight_scale_pairs(opc)
+    qa, sx, _, _, mid = ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False, True)
     torch.cuda.synchronize()
+
+    def gemm():
+        return ops.w4a4_gemm(qa, sx, wop, wsp, mid, prep.l1cat, None, g, opc, False)
+
+    if args.pmc_pass:
+        # copy kernel of known size first (calibrates FETCH_SIZE / WRITE_SIZE), then the GEMM
+        src = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        for _ in range(3):
+            gemm()
+        torch.cuda.synchronize()
+        log("pmc pass done: 1 copy of 256 MiB, 3 GEMM launches")
+        return 0
 
     def step():
         return backend.forward_prepared(x, prep, mode="w4a4")
@@ -121,21 +207,31 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps")
-    ms = time_loop(step, args.steps)
-    log(f"{ms:.4f} ms/step")
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record()
+    for _ in range(args.steps):
+        step()
+    b.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms = a.elapsed_time(b) / args.steps
+    log(f"{ms:.4f} ms/step (HIP events; host wall {wall:.4f} ms/step)")
 
-    # per-kernel averages, each kernel timed alone on the same (current) stream
-    opc = ops.OPERAND_E4M3
-    qa, sx, _, _, mid = ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False,
-                                      True)
-    ms_act = time_loop(lambda: ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False,
-                                             False, True), args.steps)
-    ms_gemm = time_loop(lambda: ops.w4a4_gemm(qa, sx, prep.weight_operand(opc), prep.weight_scale_pairs(opc), mid, prep.l1cat,
-                                              None, g, opc, False), args.steps)
+    # per-kernel launch durations, each kernel launched back to back on the stream it runs on
+    def act():
+        return ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False, True)
+    for _ in range(3):
+        act(), gemm()
+    ms_act = time_avg(act, args.steps)
+    ms_gemm = time_avg(gemm, args.steps)
     log(f"act {ms_act:.4f} ms, gemm {ms_gemm:.4f} ms")
     flops = 2.0 * m * n * k
-    act_bytes = 2 * m * k + 8 * k + 2 * r * k + m * k // 2 + 2 * m * (k // g) + 4 * m * prep.rtp
-    gemm_tops = flops / (ms_gemm * 1e-3) / 1e12
+    splits = mid.shape[0]
+    act_bytes = 2 * m * k + 8 * k + 2 * r * k + m * k + 4 * m * (k // g) + 4 * m * prep.rtp * splits
+    gemm_tflops = flops / (ms_gemm * 1e-3) / 1e12
+    traffic = read_traffic()
     result = {
         "metric": METRIC,
         "value": round(flops / (ms * 1e-3) / 1e12, 2),
@@ -147,21 +243,27 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": "e4m3",
         "data": "synthetic (X ~ N(0,1) with 1% x20 outlier channels; random-init W ~ N(0,0.02) quantized on device)",
-        "config": {"workload": "config1 ff.up: W4A4 SVDQuantLinear forward (act quant+pack+low-rank down, "
-                               "INT8-MFMA GEMM + low-rank up epilogue), M=4096 K=6144 N=16384 rank 32 group 64",
-                   "M": m, "K": k, "N": n, "rank": r, "group": g, "batch_tokens": m},
+        "config": {"workload": "config1 ff.up: W4A4 SVDQuantLinear forward (fused smooth + A4 quant + low-rank "
+                               "down; exact INT4-code GEMM on the FP8 MFMA + low-rank up epilogue, bf16 out)",
+                   "M": m, "K": k, "N": n, "rank": r, "group": g},
         "kernels": {"act_quant_ms": round(ms_act, 4), "w4a4_gemm_ms": round(ms_gemm, 4),
                     "act_quant_GBps": round(act_bytes / (ms_act * 1e-3) / 1e9, 1),
-                    "act_quant_hbm_frac": round(act_bytes / (ms_act * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": None,
-                     "kernel": "w4a4_kernel (INT8 MFMA)", "algorithmic_ops_per_launch": flops},
+                    "act_quant_hbm_frac": round(act_bytes / (ms_act * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "step_host_wall_ms": round(wall, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
+                     "kernel": "w4a4_kernel<64,0,false> (FP8 MFMA on exact INT4 codes)",
+                     "algorithmic_ops_per_launch": flops},
     }
+    if not args.no_block:
+        log("block line: 8 linears of config 1")
+        del qa, sx, mid
+        result["block_config1"] = block_line(args, dev)
     if not args.no_cpu_baseline:
-        log(f"cpu baseline on {args.cpu_rows} rows")
-        result["cpu_baseline"] = cpu_baseline(ds, x, args.cpu_rows)
+        log("cpu baseline (whole layer)")
+        result["cpu_baseline"] = cpu_baseline(ds, x, args.cpu_reps)
     print(json.dumps(result), flush=True)
     return 0
 
