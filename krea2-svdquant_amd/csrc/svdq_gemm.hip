@@ -94,65 +94,84 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
 // packed INT4 weight, converted while staging into LDS.  Global loads run two groups ahead
 // in two register sets; LDS is double buffered.
 // Global -> LDS DMA (global_load_lds_dword / _dwordx4): lane L of the wave writes its 4 (16)
-// bytes from base + off at LDS address lds + 4 L (16 L); `lds` must be wave-uniform.  Issued
-// as inline asm so that the compiler neither orders later LDS reads after it (it cannot tell
-// the pipeline stages apart) nor counts it in its own waits: the kernel waits explicitly.
+// bytes from base + off at LDS address lds + 4 L (16 L); `lds` (wave-uniform) goes in M0, as
+// an operand, so the compiler owns that register.  Issued as inline asm so that the compiler
+// neither orders later LDS reads after it (it cannot tell the pipeline stages apart) nor
+// counts it in its own waits: the kernel waits explicitly.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
 }
 
-// W4A4 GEMM (FP8 or INT8 MFMA on exact integer codes).
+// W4A4 GEMM (exact INT4-code products on the FP8 or INT8 MFMA).
 //
 // Block tile 256 x 128, 8 waves in a 4 x 2 grid, wave tile 64 x 64 = 2 x 2 sub-tiles of
 // 32 x 32.  K advances 128 columns per pipeline stage (two groups of 64 or one of 128).  A
-// stage is moved global -> LDS entirely by DMA (activation codes, expanded weight codes,
-// both scale operands) into one of two LDS buffers while the other one feeds the MFMAs; each
-// wave issues the same number of DMA instructions per stage and waits for them (vmcnt(0))
-// before the stage barrier.  The hot loop carries almost no address arithmetic: global bases
-// are scalars advanced per stage, per-lane offsets are constants, LDS offsets immediates.
+// stage is moved global -> LDS entirely by DMA (activation codes, expanded weight codes, both
+// scale operands) into a ring of three LDS buffers, two stages ahead of the MFMAs; each wave
+// issues the same number of DMA instructions per stage, so `s_waitcnt vmcnt(DMA)` retires
+// all but the newest stage.  Global bases are scalars advanced per stage; per-lane offsets
+// are constants.
 //
 // LDS operand tiles: rows of 128 bytes = 8 chunks of 16; chunk c of row r sits at chunk
 // position c ^ ((r >> 1) & 7).  The 16 lanes of a ds_read_b128 phase read one logical chunk
 // of 16 consecutive rows and hit 16 distinct 4-bank groups.
 //
-// Per group and sub-tile: P = codes_x . codes_w (exact integer sums, fp32) on the FP8 MFMA,
-// S = sx (x) sw on a bf16 MFMA with K = 2: A = (sx, sx | finite filler), B = (hi(sw), lo(sw)
-// | zeros), so S = sx hi + sx lo exactly; acc += P * S.
+// Per group and sub-tile: P = codes_x . codes_w (exact integer sums) on the FP8 MFMA (or the
+// INT8 MFMA, int32 converted to fp32), S = sx (x) sw on a bf16 MFMA with K = 2: A = (sx, sx)
+// then zeros, B = (hi(sw), lo(sw)) then zeros (zero for lanes 32-63), so S = sx hi + sx lo
+// exactly; acc += P * S (one VALU FMA per output and group).
+//
+// Ping-pong schedule: the two waves of each SIMD (waves w and w + 4) run offset by one slot.
+// In every slot between workgroup barriers one of them issues MFMAs (products and scales of
+// two sub-tiles, at raised priority) while the other rescales its previous two sub-tiles into
+// its accumulators.  A single wave barely overlaps its own VALU work with its own MFMAs on
+// this part (measured), so the overlap has to come from the pair.  With G == 64 the next
+// half-group's fragments are read from LDS at the top of the M slot, under the MFMAs, into a
+// second register set; with G == 128 (twice the fragment registers) they are read in the V
+// slot.
+//
+// Slots: the leading waves (0-3) run M(h) in slot 2h and V(h) in slot 2h + 1; the trailing
+// waves (4-7) run M(h) in slot 2h + 1 and V(h) in slot 2h + 2, where h counts half-groups.
+// Every wave passes the same 2H barriers.  Stage s + 2 is issued at the first V of stage s;
+// stage s + 1 is waited for before the barrier that ends the last slot before any wave reads
+// it (slot 2 HPS (s + 1) - 3 when reads happen in M slots, - 2 when in V slots).  The
+// placement of reads, waits and DMA issues was checked against a slot-by-slot simulation for
+// every group count up to 60 (no read before its stage landed, no buffer re-filled while a
+// slower wave still reads it, equal barrier counts).
 template <int G, int MODE, bool OUT_F32>
 __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
-  constexpr int TBM = 256, TBN = 128, NT = 512;
+  constexpr int TBM = 256, TBN = 128, NT = 512, NBUF = 3;
   constexpr int KB = 128;                     // K columns per pipeline stage
   constexpr int GPS = KB / G;                 // groups per stage
+  constexpr int HPS = 2 * GPS;                // half-groups per stage
   constexpr int KS = G / 64;                  // 64-column MFMA steps per group
   constexpr int ADMA = TBM * KB / (16 * NT);  // A: 16-byte DMA chunks per thread per stage (4)
   constexpr int BDMA = TBN * KB / (16 * NT);  // B: 16-byte DMA chunks per thread per stage (2)
+  constexpr int DMA = ADMA + BDMA + 2;        // DMA instructions per thread per stage
   constexpr int XS = TBM + 4, WS = TBN + 4;   // scale words per group; the last 4 are zero
   constexpr int ABUF = TBM * KB, BBUF = TBN * KB;
-  __shared__ __attribute__((aligned(1024))) uint8_t sA[2 * ABUF];
-  __shared__ __attribute__((aligned(1024))) uint8_t sB[2 * BBUF];
-  __shared__ __attribute__((aligned(16))) uint32_t sX[2][GPS][XS];   // (sx, sx) bf16 pairs
-  __shared__ __attribute__((aligned(16))) uint32_t sW[2][GPS][WS];   // (hi, lo) of sw
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[NBUF * ABUF];
+  __shared__ __attribute__((aligned(1024))) uint8_t sB[NBUF * BBUF];
+  __shared__ __attribute__((aligned(16))) uint32_t sX[NBUF][GPS][XS];   // (sx, sx) bf16 pairs
+  __shared__ __attribute__((aligned(16))) uint32_t sW[NBUF][GPS][WS];   // (hi, lo) of sw
 
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int trail = wave >> 2;                // 0: leading waves, 1: trailing waves
   const int wm = wave >> 1, wn = wave & 1;
   const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
   int bm, bn;
   tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
   const int m0 = bm * TBM, n0 = bn * TBN;
-  const int K = p.K, ngroups = K / G, nstages = (K + KB - 1) / KB;
+  const int K = p.K, ngroups = K / G, nstages = (K + KB - 1) / KB, H = 2 * ngroups;
 
-  // Operand DMA: wave w, chunk i covers LDS bytes [(DMA w + i) KB, +1 KB) of a stage tile,
-  // i.e. 8 rows; lane L lands at row 8 (DMA w + i) + L / 8, chunk position L % 8 (logical
-  // chunk c = position ^ swizzle).  Per-lane byte offsets: row (clamped to M / N) and chunk.
-  // A last stage holding a single group of 64 clamps its columns to the row's last chunk
-  // (that group is not computed).  Offsets are 32-bit (the host bounds the operand sizes).
+  // Operand DMA (as in w4a4_kernel): wave w, chunk i -> 8 rows of a stage tile.
   uint32_t arow_o[ADMA], brow_o[BDMA];
   int ac16[ADMA], bc16[BDMA];
 #pragma unroll
@@ -167,49 +186,36 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
     bc16[i] = 16 * ((lane % 8) ^ ((row >> 1) & 7));
     brow_o[i] = (uint32_t)min(n0 + row, p.N - 1) * (uint32_t)K;
   }
-  // Scale DMA (both scale operands are group-major, [K/G, rows]): word slot
-  // t = (64 wave + lane) mod (GPS rows) -> group t / rows, row t % rows; waves past the slot
-  // count load duplicates of the same words into the same places.
   const int xs = (64 * wave + lane) % (GPS * TBM), ws = (64 * wave + lane) % (GPS * TBN);
   const int xj = xs / TBM, wj = ws / TBN;
   const uint32_t xrowc = (uint32_t)min(m0 + xs % TBM, p.M - 1), wrowc = (uint32_t)min(n0 + ws % TBN, p.N - 1);
-  const int xjs = ((64 * wave) % (GPS * TBM)) / TBM, wjs = ((64 * wave) % (GPS * TBN)) / TBN;  // = xj, wj
+  const int xjs = ((64 * wave) % (GPS * TBM)) / TBM, wjs = ((64 * wave) % (GPS * TBN)) / TBN;
   const int xbase = (64 * wave) % (GPS * TBM) % TBM, wbase = (64 * wave) % (GPS * TBN) % TBN;
-  if (tid < 2 * GPS * 4) {
+  if (tid < NBUF * GPS * 4) {
     sX[tid / (4 * GPS)][(tid / 4) % GPS][TBM + tid % 4] = 0u;
     sW[tid / (4 * GPS)][(tid / 4) % GPS][TBN + tid % 4] = 0u;
   }
   const uint32_t ldsA = lds_offset(sA), ldsB = lds_offset(sB), ldsX = lds_offset(&sX[0][0][0]),
                  ldsW = lds_offset(&sW[0][0][0]);
 
-  // Issue every DMA of stage `s` into buffer `buf`.
   auto gload = [&](int s, int buf) {
     const int col0 = s * KB;
-    const bool tail = col0 + KB > K;   // a last stage with a single group of 64
+    const bool tail = col0 + KB > K;
     const uint8_t* qa_s = p.qa + col0;
     const uint8_t* qw_s = p.qwe + col0;
     const int g0 = s * GPS;
-    const int jmax = ngroups - 1 - g0;   // >= 0
+    const int jmax = ngroups - 1 - g0;
     const uint32_t* sx_s = p.sxp + (long)g0 * p.M;
     const uint32_t* sw_s = p.swp + (long)g0 * p.N;
-    dma4(sx_s, 4 * ((uint32_t)min(xj, jmax) * (uint32_t)p.M + xrowc),
-         ldsX + 4 * ((buf * GPS + xjs) * XS + xbase));
-    dma4(sw_s, 4 * ((uint32_t)min(wj, jmax) * (uint32_t)p.N + wrowc),
-         ldsW + 4 * ((buf * GPS + wjs) * WS + wbase));
-    if (!tail) {
+    dma4(sx_s, 4 * ((uint32_t)min(xj, jmax) * (uint32_t)p.M + xrowc), ldsX + 4 * ((buf * GPS + xjs) * XS + xbase));
+    dma4(sw_s, 4 * ((uint32_t)min(wj, jmax) * (uint32_t)p.N + wrowc), ldsW + 4 * ((buf * GPS + wjs) * WS + wbase));
+    const int lim = tail ? K - col0 - 16 : KB;
 #pragma unroll
-      for (int i = 0; i < ADMA; ++i) dma16(qa_s, arow_o[i] + ac16[i], ldsA + buf * ABUF + (ADMA * wave + i) * 1024);
+    for (int i = 0; i < ADMA; ++i)
+      dma16(qa_s, arow_o[i] + min(ac16[i], lim), ldsA + buf * ABUF + (ADMA * wave + i) * 1024);
 #pragma unroll
-      for (int i = 0; i < BDMA; ++i) dma16(qw_s, brow_o[i] + bc16[i], ldsB + buf * BBUF + (BDMA * wave + i) * 1024);
-    } else {
-      const int lim = K - col0 - 16;
-#pragma unroll
-      for (int i = 0; i < ADMA; ++i)
-        dma16(qa_s, arow_o[i] + min(ac16[i], lim), ldsA + buf * ABUF + (ADMA * wave + i) * 1024);
-#pragma unroll
-      for (int i = 0; i < BDMA; ++i)
-        dma16(qw_s, brow_o[i] + min(bc16[i], lim), ldsB + buf * BBUF + (BDMA * wave + i) * 1024);
-    }
+    for (int i = 0; i < BDMA; ++i)
+      dma16(qw_s, brow_o[i] + min(bc16[i], lim), ldsB + buf * BBUF + (BDMA * wave + i) * 1024);
   };
 
   f32x16 acc[2][2];
@@ -218,8 +224,6 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  // Fragment byte offsets within a stage tile: logical chunk c = u + 2h of the lane's row,
-  // u = 4 (G/64 gi + ks) + t in {0, 1, 4, 5}, stored at chunk position c ^ swizzle.
   const int sw_ = (lr >> 1) & 7;
   int fa[4], fb[4];
 #pragma unroll
@@ -228,108 +232,142 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
     fa[q] = (64 * wm + lr) * 128 + 16 * ((u + 2 * h) ^ sw_);
     fb[q] = (64 * wn + lr) * 128 + 16 * ((u + 2 * h) ^ sw_);
   }
-  // Scale-MFMA operands: A reads 4 words from the lane's row (word 0 = its pair, the rest
-  // finite filler); B holds the pair in word 0 for lanes 0-31 and is zero otherwise.
-  const int xo = 4 * (64 * wm + lr);
+  // Scale-MFMA operands: persistent tuples, word 0 reloaded from LDS, words 1-3 stay zero.
+  // A = (sx, sx) of the lane's row; B = (hi, lo) of the lane's column for lanes 0-31 and zero
+  // for lanes 32-63 (they read the zero word).
+  const int xo0 = 4 * (64 * wm + lr), xo1 = xo0 + 128;
   const int wo0 = 4 * (h ? TBN : 64 * wn + lr), wo1 = 4 * (h ? TBN : 64 * wn + 32 + lr);
-  u32x4 wop[2] = {u32x4{}, u32x4{}};
+  u32x4 xop[2] = {u32x4{}, u32x4{}};
 
-  struct Frag {
-    u32x4 a[2][KS][2], b[2][KS][2];
-    u32x4 x[2];
-  };
-  auto read_frag = [&](Frag& f, int buf, int gi) {
+  // Fragments.  G == 64 (RM): the next half-group's fragments are read at the start of the M
+  // slot, under the MFMAs, into the other set: A by half-group parity, B and the weight scales
+  // by group parity.  G == 128: one set, read in the V slot (the registers do not fit twice).
+  constexpr bool RM = G == 64;
+  constexpr int NS = RM ? 2 : 1;
+  u32x4 fa_[NS][KS][2], fb_[NS][2][KS][2], wop_[NS][2];
+#pragma unroll
+  for (int q = 0; q < NS; ++q) wop_[q][0] = wop_[q][1] = u32x4{};
+  // half-group (s, gi, i) -> fragment sets: A set ai, B / weight-scale set bi
+  auto read_half = [&](int s, int gi, int i, int ai, int bi) {
+    const int buf = s % NBUF;
     const uint8_t* a0 = sA + buf * ABUF;
     const uint8_t* b0 = sB + buf * BBUF;
+    const uint8_t* x0 = reinterpret_cast<const uint8_t*>(&sX[buf][gi][0]);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int q = 2 * (G / 64 * gi + ks) + t;
+        fa_[ai][ks][t] = ld16(a0 + fa[q] + 4096 * i);
+        if (i == 0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          f.a[i][ks][t] = ld16(a0 + fa[q] + 4096 * i);
-          f.b[i][ks][t] = ld16(b0 + fb[q] + 4096 * i);
+          for (int j = 0; j < 2; ++j) fb_[bi][j][ks][t] = ld16(b0 + fb[q] + 4096 * j);
         }
       }
-    const uint8_t* x0 = reinterpret_cast<const uint8_t*>(&sX[buf][gi][0]);
-    const uint8_t* w0 = reinterpret_cast<const uint8_t*>(&sW[buf][gi][0]);
-    f.x[0] = ld16(x0 + xo);
-    f.x[1] = ld16(x0 + xo + 128);
-    wop[0][0] = *reinterpret_cast<const uint32_t*>(w0 + wo0);
-    wop[1][0] = *reinterpret_cast<const uint32_t*>(w0 + wo1);
-  };
-  auto mfma_p = [&](const Frag& f, int i, int j) {
-    f32x16 pf;
-    if (MODE == 0) {
-      pf = mfma_fp8_32x32x64(f.a[i][0], f.b[j][0], f32x16{});
-#pragma unroll
-      for (int ks = 1; ks < KS; ++ks) pf = mfma_fp8_32x32x64(f.a[i][ks], f.b[j][ks], pf);
-    } else {
-      i32x16 pi = i32x16{};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          pi = mfma_i8_32x32x32(__builtin_bit_cast(i32x4, f.a[i][ks][t]), __builtin_bit_cast(i32x4, f.b[j][ks][t]), pi);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) pf[r] = (float)pi[r];
+    xop[i][0] = *reinterpret_cast<const uint32_t*>(x0 + (i ? xo1 : xo0));
+    if (i == 0) {
+      const uint8_t* w0 = reinterpret_cast<const uint8_t*>(&sW[buf][gi][0]);
+      wop_[bi][0][0] = *reinterpret_cast<const uint32_t*>(w0 + wo0);
+      wop_[bi][1][0] = *reinterpret_cast<const uint32_t*>(w0 + wo1);
     }
+  };
+  // Product of sub-tile (i, j): FP8 -> fp32 sums directly; INT8 -> int32 sums (converted in V).
+  auto mfma_p8 = [&](int ai, int bi, int j) {
+    f32x16 pf = mfma_fp8_32x32x64(fa_[ai][0], fb_[bi][j][0], f32x16{});
+#pragma unroll
+    for (int ks = 1; ks < KS; ++ks) pf = mfma_fp8_32x32x64(fa_[ai][ks], fb_[bi][j][ks], pf);
     return pf;
   };
-  auto fma16 = [&](f32x16& a, const f32x16& pf, const f32x16& sf) {
+  auto mfma_pi = [&](int ai, int bi, int j) {
+    i32x16 pi = i32x16{};
 #pragma unroll
-    for (int r = 0; r < 16; ++r) a[r] = __builtin_fmaf(pf[r], sf[r], a[r]);
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        pi = mfma_i8_32x32x32(__builtin_bit_cast(i32x4, fa_[ai][ks][t]), __builtin_bit_cast(i32x4, fb_[bi][j][ks][t]), pi);
+    return pi;
   };
-
-  // Issue order per group, sub-tiles t = (0,0) (0,1) (1,0) (1,1):
-  //   P_t (product MFMA) | rescale of sub-tile t-1 (16 VALU FMAs) | S_t (scale MFMA)
-  // The rescale of t-1 needs S_{t-1}, which completed before P_t could issue, so the FMAs
-  // run in the shadow of P_t.  Empty asm statements on the values pin this order (the
-  // compiler would otherwise issue all MFMAs of a stage first and run out of registers).
-  // Sub-tile (1,1) of a group is rescaled under the next group's first MFMA.
-  f32x16 pp = f32x16{}, ps = f32x16{};
-  auto group = [&](Frag& f) {
-    constexpr int TI[4] = {0, 0, 1, 1}, TJ[4] = {0, 1, 0, 1};
-    f32x16 cp[4], cs[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int i = TI[t], j = TJ[t];
-      cp[t] = mfma_p(f, i, j);
-      f32x16& a = t == 0 ? acc[1][1] : acc[TI[t - 1]][TJ[t - 1]];
-      fma16(a, t == 0 ? pp : cp[t - 1], t == 0 ? ps : cs[t - 1]);
-      asm volatile("" : "+v"(a), "+v"(f.x[i]), "+v"(wop[j]));
-      cs[t] = mfma_bf16_32x32x16(f.x[i], wop[j], f32x16{});
-      if (t < 3) {
-        const int ni = TI[t + 1], nj = TJ[t + 1];
-        asm volatile("" : "+v"(f.a[ni][0][0]), "+v"(f.a[ni][0][1]), "+v"(f.b[nj][0][0]), "+v"(f.b[nj][0][1]));
-      }
-    }
-    pp = cp[3];
-    ps = cs[3];
+  // Fence operands: every fragment register (both sets), so that reads issued before a fence
+  // have landed at it and nothing that reads them moves across it.
+#define SVDQ_FRAGS_1 "+v"(fa_[0][0][0]), "+v"(fa_[0][0][1]), "+v"(fb_[0][0][0][0]), "+v"(fb_[0][0][0][1]), \
+    "+v"(fb_[0][1][0][0]), "+v"(fb_[0][1][0][1]), "+v"(xop[0]), "+v"(xop[1]), "+v"(wop_[0][0]), "+v"(wop_[0][1])
+#define SVDQ_FRAGS_2 "+v"(fa_[NS - 1][0][0]), "+v"(fa_[NS - 1][0][1]), "+v"(fb_[NS - 1][0][0][0]), \
+    "+v"(fb_[NS - 1][0][0][1]), "+v"(fb_[NS - 1][1][0][0]), "+v"(fb_[NS - 1][1][0][1]), "+v"(wop_[NS - 1][0]), \
+    "+v"(wop_[NS - 1][1])
+#define SVDQ_FRAGS_K2 "+v"(fa_[0][KS - 1][0]), "+v"(fa_[0][KS - 1][1]), "+v"(fb_[0][0][KS - 1][0]), \
+    "+v"(fb_[0][0][KS - 1][1]), "+v"(fb_[0][1][KS - 1][0]), "+v"(fb_[0][1][KS - 1][1])
+  auto frag_fence = [&]() {
+    if (RM) asm volatile("" : SVDQ_FRAGS_1, SVDQ_FRAGS_2::"memory");
+    else if (KS == 2) asm volatile("" : SVDQ_FRAGS_1, SVDQ_FRAGS_K2::"memory");
+    else asm volatile("" : SVDQ_FRAGS_1::"memory");
   };
-  // One stage: prefetch stage s + 1 into the other buffer, compute stage s, wait, barrier.
-  auto stage = [&](int s, int buf) {
-    gload(min(s + 1, nstages - 1), buf ^ 1);
-#pragma unroll
-    for (int gi = 0; gi < GPS; ++gi) {
-      if (gi > 0 && s * GPS + gi >= ngroups) break;   // K has an odd number of groups of 64
-      Frag f;
-      read_frag(f, buf, gi);
-      group(f);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+  // End of an M slot: products complete (their registers are operands), priority back down.
+  auto end_m = [&](f32x16 (&P)[2], i32x16 (&PI)[2], f32x16 (&S)[2]) {
+    if (RM) frag_fence();   // next fragments, read at the top of this slot, have landed
+    if (MODE == 0)
+      asm volatile("s_setprio 0\n\ts_barrier" : "+v"(P[0]), "+v"(P[1]), "+v"(S[0]), "+v"(S[1])::"memory");
+    else
+      asm volatile("s_setprio 0\n\ts_barrier" : "+v"(PI[0]), "+v"(PI[1]), "+v"(S[0]), "+v"(S[1])::"memory");
+  };
+  // End of a V slot: accumulators written, fragments in place; priority up for the M slot.
+  auto end_v = [&]() {
+    frag_fence();
+    asm volatile("s_barrier\n\ts_setprio 1" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]),
+                 "+v"(acc[1][1])::"memory");
   };
 
   gload(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  gload(min(1, nstages - 1), 1);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
   __syncthreads();
-  for (int s = 0; s < nstages; s += 2) {   // unrolled by two: buffer offsets are immediates
-    stage(s, 0);
-    if (s + 1 < nstages) stage(s + 1, 1);
+  read_half(0, 0, 0, 0, 0);
+  if (trail) {
+    end_v();      // the trailing waves sit out slot 0
+  } else {
+    frag_fence();
+    asm volatile("s_setprio 1" ::: "memory");
   }
-  fma16(acc[1][1], pp, ps);
+  for (int s = 0; s < nstages; ++s) {
+#pragma unroll
+    for (int hh = 0; hh < HPS; ++hh) {
+      const int hg = s * HPS + hh;            // half-group index
+      if (hh > 0 && hg >= H) break;           // K has an odd number of groups of 64
+      const int i = hh & 1, gi = hh >> 1;
+      const int ai = RM ? i : 0, bi = RM ? gi : 0;
+      const int hn = hh + 1 == HPS ? 0 : hh + 1;   // next half-group's position in its stage
+      const int sn = hh + 1 == HPS ? s + 1 : s;
+      // ---- M slot: (RM) next fragments, then products and scales of sub-tiles (i, 0), (i, 1)
+      if (RM && hg + 1 < H) read_half(sn, hn >> 1, hn & 1, hn & 1, hn >> 1);
+      f32x16 P[2], S[2];
+      i32x16 PI[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (MODE == 0) P[j] = mfma_p8(ai, bi, j);
+        else PI[j] = mfma_pi(ai, bi, j);
+        S[j] = mfma_bf16_32x32x16(xop[i], wop_[bi][j], f32x16{});
+      }
+      // stage s + 1 must have landed before the barrier ending slot 2 HPS (s + 1) - (RM ? 3 : 2)
+      if (RM ? (trail && hh == HPS - 2) : (!trail && hh == HPS - 1))
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
+      end_m(P, PI, S);
+      // ---- V slot: issue stage s + 2, rescale, (not RM) read the next fragments
+      if (hh == 0) gload(min(s + 2, nstages - 1), (s + 2) % NBUF);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f32x16 pf = MODE == 0 ? P[j] : __builtin_convertvector(PI[j], f32x16);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(pf[r], S[j][r], acc[i][j][r]);
+      }
+      if (!RM && hg + 1 < H) read_half(sn, hn >> 1, hn & 1, 0, 0);
+      if (RM ? (!trail && hh == HPS - 2) : (trail && hh == HPS - 2))
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
+      if (!(trail && hg == H - 1)) end_v();
+    }
+  }
+#undef SVDQ_FRAGS_1
+#undef SVDQ_FRAGS_2
+#undef SVDQ_FRAGS_K2
+  asm volatile("s_setprio 0\n\ts_waitcnt vmcnt(0)" ::: "memory");
 
   epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h);
 }
@@ -462,10 +500,11 @@ __global__ void __launch_bounds__(NTHR) w4a16_kernel(GemmParams p) {
 
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st) {
   const dim3 grid(((p.M + 255) / 256) * ((p.N + 127) / 128));
+#define SVDQ_W4A4_KERNEL w4a4_kernel
 #define SVDQ_W4A4(GG, MM)                                                        \
   if (G == GG && mode == MM) {                                                   \
-    if (out_f32) w4a4_kernel<GG, MM, true><<<grid, 512, 0, st>>>(p);              \
-    else w4a4_kernel<GG, MM, false><<<grid, 512, 0, st>>>(p);                     \
+    if (out_f32) SVDQ_W4A4_KERNEL<GG, MM, true><<<grid, 512, 0, st>>>(p);         \
+    else SVDQ_W4A4_KERNEL<GG, MM, false><<<grid, 512, 0, st>>>(p);                \
     return hipGetLastError();                                                    \
   }
   SVDQ_W4A4(64, 0)
