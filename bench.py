@@ -59,7 +59,7 @@ def parse():
     ap.add_argument("--group", type=int, default=64)
     ap.add_argument("--cpu-reps", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-block", action="store_true", help="skip the 8-shape block line")
+    ap.add_argument("--no-block", action="store_true", help="skip the config 1/2/4 extra lines")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="counter pass for rocprofv3: one copy kernel of known size, then GEMM launches")
     return ap.parse_args()
@@ -165,6 +165,52 @@ def block_line(args, dev) -> dict:
                     "denoise step this backend replaces"}
 
 
+def w4a16_line(args, dev) -> dict:
+    """the 8 block shapes, W4A16 at M=2304 (768x768 latent), each timed alone."""
+    import torch
+    from krea2_svdquant_amd.kernels.hip import backend
+    out, total, flops_total = {}, 0.0, 0.0
+    for i, (name, n, k) in enumerate(BLOCK_SHAPES):
+        x, _, prep = make_layer(n, k, 2304, args.rank, args.group, dev, seed=200 + 10 * i)
+        for _ in range(3):
+            backend.forward_prepared(x, prep, mode="w4a16")
+        ms = time_avg(lambda: backend.forward_prepared(x, prep, mode="w4a16"), 20)
+        out[name] = round(ms, 4)
+        total += ms
+        flops_total += 2.0 * 2304 * n * k
+        del x, prep
+        torch.cuda.empty_cache()
+    tflops = flops_total / (total * 1e-3) / 1e12
+    return {"ms_per_layer": out, "ms_per_block_linears": round(total, 4), "TFLOPs": round(tflops, 1),
+            "bf16_peak_frac": round(tflops / 2500.0, 4),
+            "note": "W4A16 (bf16 x_hat x in-register dequantized INT4 weights, bf16 MFMA), M=2304, layer = "
+                    "x_hat pass + GEMM with low-rank epilogue"}
+
+
+def lora_line(args, dev) -> dict:
+    """batch-4 1024px (M=16384) ff.up and ff.down, W4A4, fused LoRA rank 64."""
+    import torch
+    from krea2_svdquant_amd.kernels.hip import backend
+    out = {}
+    for i, (name, n, k) in enumerate([("ff.up", 16384, 6144), ("ff.down", 6144, 16384)]):
+        x, ds, _ = make_layer(n, k, 16384, args.rank, args.group, dev, seed=300 + 10 * i)
+        gen = torch.Generator(device=dev).manual_seed(4 + i)
+
+        class _Ad:   # rank-64 LoRA, A, B ~ N(0, 0.01), scale 0.8, alpha = rank -> multiplier 0.8
+            down_weight = (torch.randn(64, k, device=dev, generator=gen) * 0.01).to(torch.bfloat16)
+            up_weight = (torch.randn(n, 64, device=dev, generator=gen) * 0.01).to(torch.bfloat16)
+            multiplier = 0.8
+        prep = backend.prepare_layer(ds, [_Ad()], dev)
+        for _ in range(3):
+            backend.forward_prepared(x, prep, mode="w4a4")
+        ms = time_avg(lambda: backend.forward_prepared(x, prep, mode="w4a4"), 10)
+        out[name] = {"ms": round(ms, 4), "eff_TOPS": round(2.0 * 16384 * n * k / (ms * 1e-3) / 1e12, 1)}
+        del x, ds, prep
+        torch.cuda.empty_cache()
+    return {"layers": out, "note": "W4A4 + rank-32 SVD branch + rank-64 LoRA fused (down in the activation pass, "
+                                   "up in the GEMM epilogue), M=16384"}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -261,6 +307,10 @@ def main() -> int:
         log("block line: 8 linears of config 1")
         del qa, sx, mid
         result["block_config1"] = block_line(args, dev)
+        log("config 2: W4A16 block at M=2304")
+        result["w4a16_config2"] = w4a16_line(args, dev)
+        log("config 4: M=16384 with fused LoRA r64")
+        result["lora_config4"] = lora_line(args, dev)
     if not args.no_cpu_baseline:
         log("cpu baseline (whole layer)")
         result["cpu_baseline"] = cpu_baseline(ds, x, args.cpu_reps)
