@@ -158,12 +158,20 @@ def test_layer_golden(dev, name, mode):
     _check_layer(x, st, dev, mode, fx["y_" + mode])
 
 
-@pytest.mark.parametrize("m,n,k,r,rl,bias", [(128, 128, 64, 32, 0, False), (200, 333, 640, 32, 64, True),
-                                              (7, 1536, 2048, 64, 0, True), (256, 512, 6144, 32, 64, False)])
+@pytest.mark.parametrize("m,n,k,g,r,rl,bias", [
+    (128, 128, 64, 64, 32, 0, False),     # one group: a single, half-filled pipeline stage
+    (200, 333, 640, 64, 32, 64, True),
+    (7, 1536, 2048, 64, 64, 0, True),
+    (256, 512, 6144, 64, 32, 64, False),
+    (130, 200, 448, 64, 32, 0, True),     # 7 groups: 4 stages, the last one a single group
+    (64, 256, 1152, 64, 32, 32, False),   # 18 groups: 9 stages
+    (96, 320, 384, 128, 32, 0, True),     # group 128: 3 stages
+    (33, 128, 896, 128, 64, 64, False),   # group 128: 7 stages
+])
 @pytest.mark.parametrize("mode", ["w4a4", "w4a16"])
-def test_layer_random_shapes(dev, m, n, k, r, rl, bias, mode):
+def test_layer_random_shapes(dev, m, n, k, g, r, rl, bias, mode):
     x = synth.make_activation(m, k, seed=11)
-    st = synth.make_layer(n, k, x, rank=r, group_size=64, seed=12, bias=bias)
+    st = synth.make_layer(n, k, x, rank=r, group_size=g, seed=12, bias=bias)
     if rl:
         st.adapters.append(synth.make_adapter(n, k, rank=rl, seed=13))
     ref = (sim.w4a4_eval if mode == "w4a4" else sim.w4a16_eval)(x, st)["y"]
