@@ -274,8 +274,11 @@ def main() -> int:
     ms_gemm = time_avg(gemm, args.steps)
     log(f"act {ms_act:.4f} ms, gemm {ms_gemm:.4f} ms")
     flops = 2.0 * m * n * k
-    splits = mid.shape[0]
-    act_bytes = 2 * m * k + 8 * k + 2 * r * k + m * k + 4 * m * (k // g) + 4 * m * prep.rtp * splits
+    splits = mid.shape[0] - 1
+    # x, srs, l2 read; codes, scales, split partials written; partials re-read and the final
+    # hi / lo operand written by the finalize kernel
+    act_bytes = (2 * m * k + 8 * k + 2 * r * k + m * k + 4 * m * (k // g) + 2 * 4 * m * prep.rtp * splits
+                 + 4 * m * prep.rtp)
     gemm_tflops = flops / (ms_gemm * 1e-3) / 1e12
     traffic = read_traffic()
     result = {

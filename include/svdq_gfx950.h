@@ -66,8 +66,8 @@ int svdq_group_supported(int group);
 int svdq_prepare_smooth(const void* smooth, float* srs, int K, hipStream_t stream);
 
 /* Output sizing of svdq_act_quant for (M, K, group, RTp): the number S of K splits the
- * activation pass uses and the floats of its `mid` output (S * M * RTp: one partial per
- * split, added by the GEMM epilogue in split order). */
+ * activation pass uses and the floats of its `mid` workspace, (S + 1) * M * RTp: the
+ * finalized GEMM operand (M * RTp floats' worth of bytes) followed by one partial per split. */
 int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int64_t* mid_floats);
 
 /* Fused activation pass.  Replaces reference quant/svd.py:121-122 (x_hat = x / smooth),
@@ -85,9 +85,12 @@ int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int6
  *          e4m3(q) or int8 16*q
  *     qx : u8 [M, K/2] canonical packed codes (pack.py:47-56), if SVDQ_ACT_PACKED
  *   xhat     : bf16 [M, ldxh] (SVDQ_ACT_XHAT; with a quantizing flag only for e4m3)
- *   mid      : f32 [S, M, RTp] split partials, summed over S: columns [0, r) = x_hat @ l2^T,
- *              [r, r+rl) = mult * (x @ A^T), [r+rl, RTp) = 0.   RTp % 32 == 0, RTp >= r + rl,
- *              ceil(r/32) + ceil(rl/32) <= 4;  S (`splits`) from svdq_act_quant_workspace. */
+ *   mid      : workspace of svdq_act_quant_workspace's mid_floats floats.  Output at its head:
+ *              bf16 [M, 2, RTp], per row the hi plane then the lo plane of the f32 low-rank
+ *              activations (hi + lo within 2^-18 relative), whose columns are [0, r) = x_hat @ l2^T,
+ *              [r, r+rl) = mult * (x @ A^T), [r+rl, RTp) = 0; the split partials behind it are
+ *              summed in split order.  RTp % 32 == 0, RTp >= r + rl, ceil(r/32) + ceil(rl/32) <= 4;
+ *              S (`splits`) from svdq_act_quant_workspace. */
 int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
                    const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
                    int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
@@ -118,19 +121,20 @@ int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int ope
  *   qwe: u8 [N, K] from svdq_prepare_weight_operand (same format)
  *   swp: u32 [K/group, N] from svdq_prepare_weight_scales (same operand format)
  *   M*K and N*K below 2^31 (larger problems are split over rows by the caller)
- *   mid: f32 [splits, M, RTp] from svdq_act_quant    l1cat : bf16 [N, RTp] = [l1 | up_1 | ... | 0]
+ *   mid: bf16 [M, 2, RTp] (hi, lo planes) = the head of svdq_act_quant's mid workspace
+ *   l1cat : bf16 [N, RTp] = [l1 | up_1 | ... | 0]
  *   bias: bf16 [N] or NULL     y : [M, ldy], bf16 (out_f32 = 0) or f32 (out_f32 = 1) */
 int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
-                   const float* mid, int splits, const void* l1cat, int RTp, const void* bias, int M, int N,
-                   int K, int group, void* y, int64_t ldy, int out_f32, hipStream_t stream);
+                   const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                   void* y, int64_t ldy, int out_f32, hipStream_t stream);
 
 /* W4A16 GEMM with fused epilogue: the reference pytorch_sim math (quant/svd.py:119-163;
  * dequantization pack.py:26-44 in bf16) and kernels/triton/generic_int4.py:18-133.
  *   xhat : bf16 [M, ldxh] (from svdq_act_quant with SVDQ_ACT_XHAT); other arguments as in
  *   svdq_w4a4_gemm. */
-int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const float* mid,
-                    int splits, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
-                    void* y, int64_t ldy, int out_f32, hipStream_t stream);
+int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const void* mid,
+                    const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group, void* y,
+                    int64_t ldy, int out_f32, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -270,6 +270,31 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
 
 }
 
+// Final low-rank operand of the GEMM epilogue: the split partials summed in split order
+// (a fixed order, so the result is deterministic), then split into bf16 hi and lo planes
+// [M, 2, RTp] (the bf16 MFMA operands of mid @ l1cat^T).  One thread per 8 columns of a row.
+__global__ void mid_finalize_kernel(const float* __restrict__ part, int S, int M, int RTp,
+                                    uint16_t* __restrict__ midp) {
+  const int chunks = RTp / 8;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)M * chunks) return;
+  const long m = idx / chunks;
+  const int c = (int)(idx % chunks);
+  const long plane = (long)M * RTp;
+  const float* src = part + m * RTp + 8 * c;
+  f32x4 v0 = *reinterpret_cast<const f32x4*>(src), v1 = *reinterpret_cast<const f32x4*>(src + 4);
+  for (int s = 1; s < S; ++s) {
+    v0 += *reinterpret_cast<const f32x4*>(src + s * plane);
+    v1 += *reinterpret_cast<const f32x4*>(src + s * plane + 4);
+  }
+  const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+  u32x4 hi, lo;
+  split_hi_lo(v, hi, lo);
+  uint16_t* dst = midp + m * 2 * RTp + 8 * c;
+  *reinterpret_cast<u32x4*>(dst) = hi;
+  *reinterpret_cast<u32x4*>(dst + RTp) = lo;
+}
+
 // (s, RN(1/s)) in float32 for a bf16 smoothing vector: computed once per layer.
 __global__ void prepare_smooth_kernel(const uint16_t* __restrict__ s, float* __restrict__ srs, int K) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -318,6 +343,12 @@ hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, in
   if (G == 64) return launch_act_g<64>(p, nt, oper, xhat, grid, st);
   if (G == 128) return launch_act_g<128>(p, nt, oper, xhat, grid, st);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_mid_finalize(const float* part, int S, int M, int RTp, uint16_t* midp, hipStream_t st) {
+  const long n = (long)M * (RTp / 8);
+  mid_finalize_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(part, S, M, RTp, midp);
+  return hipGetLastError();
 }
 
 hipError_t launch_prepare_smooth(const uint16_t* s, float* srs, int K, hipStream_t st) {

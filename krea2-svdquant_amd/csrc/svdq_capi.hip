@@ -64,7 +64,7 @@ int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int6
   if (RTp <= 0 || RTp % 32) return fail(SVDQ_ERR_SHAPE, "RTp=%d must be a positive multiple of 32", RTp);
   const int s = svdq::act_splits(M, K, group);
   if (splits) *splits = s;
-  if (mid_floats) *mid_floats = (int64_t)s * M * RTp;
+  if (mid_floats) *mid_floats = (int64_t)(s + 1) * M * RTp;
   return ok();
 }
 
@@ -120,23 +120,25 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
   p.sx = static_cast<uint16_t*>(sx);
   p.xhat = static_cast<uint16_t*>(xhat);
   p.ldxh = ldxh;
-  p.mid = mid;
+  p.mid = mid + (int64_t)M * RTp;   // split partials after the finalized operand
   const int ngroups = K / group;
   p.gps = (ngroups + splits - 1) / splits;
   p.exact = (flags & SVDQ_ACT_EXACT_DIV) ? 1 : 0;
   p.sx_pairs = pairs ? 1 : 0;
-  return launched(svdq::launch_act(p, group, nt, e4m3 ? 1 : (i8 ? 2 : 0), want_xhat, splits, stream),
-                  "act_quant");
+  if (int e = launched(svdq::launch_act(p, group, nt, e4m3 ? 1 : (i8 ? 2 : 0), want_xhat, splits, stream),
+                       "act_quant"))
+    return e;
+  return launched(svdq::launch_mid_finalize(p.mid, splits, M, RTp, reinterpret_cast<uint16_t*>(mid), stream),
+                  "act_quant (mid)");
 }
 
-static int gemm_common_checks(const char* who, const void* qw, const void* sw, const float* mid,
-                              int splits, const void* l1cat, int RTp, int M, int N, int K, int group,
-                              void* y, int64_t ldy, int out_f32) {
+static int gemm_common_checks(const char* who, const void* qw, const void* sw, const void* mid,
+                              const void* l1cat, int RTp, int M, int N, int K, int group, void* y, int64_t ldy,
+                              int out_f32) {
   if (M <= 0 || N <= 0) return fail(SVDQ_ERR_ARG, "%s: M=%d N=%d", who, M, N);
   if (int e = check_group(group, K)) return e;
   if (!qw || !sw || !mid || !l1cat || !y) return fail(SVDQ_ERR_ARG, "%s: null pointer", who);
   if (RTp <= 0 || RTp % 32) return fail(SVDQ_ERR_SHAPE, "%s: RTp=%d must be a positive multiple of 32", who, RTp);
-  if (splits < 1) return fail(SVDQ_ERR_ARG, "%s: splits=%d", who, splits);
   if (out_f32 != 0 && out_f32 != 1) return fail(SVDQ_ERR_ARG, "%s: out_f32=%d", who, out_f32);
   if (ldy < N) return fail(SVDQ_ERR_SHAPE, "%s: ldy=%lld < N=%d", who, (long long)ldy, N);
   if (!aligned16(qw) || !aligned16(mid) || !aligned16(l1cat) || (K / 2) % 8)
@@ -144,14 +146,12 @@ static int gemm_common_checks(const char* who, const void* qw, const void* sw, c
   return SVDQ_OK;
 }
 
-static svdq::GemmParams gemm_params(const void* qw, const void* sw, const float* mid, int splits,
-                                    const void* l1cat, int RTp, const void* bias, int M, int N, int K, void* y,
-                                    int64_t ldy) {
+static svdq::GemmParams gemm_params(const void* qw, const void* sw, const void* mid, const void* l1cat, int RTp,
+                                    const void* bias, int M, int N, int K, void* y, int64_t ldy) {
   svdq::GemmParams p{};
   p.qw = static_cast<const uint8_t*>(qw);
   p.sw = static_cast<const uint16_t*>(sw);
-  p.mid = mid;
-  p.splits = splits;
+  p.midp = static_cast<const uint16_t*>(mid);
   p.l1cat = static_cast<const uint16_t*>(l1cat);
   p.RTp = RTp;
   p.bias = static_cast<const uint16_t*>(bias);
@@ -185,10 +185,10 @@ int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int ope
 }
 
 int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
-                   const float* mid, int splits, const void* l1cat, int RTp, const void* bias, int M, int N,
-                   int K, int group, void* y, int64_t ldy, int out_f32, hipStream_t stream) {
+                   const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                   void* y, int64_t ldy, int out_f32, hipStream_t stream) {
   const void* sw = swp;
-  if (int e = gemm_common_checks("w4a4_gemm", qwe, sw, mid, splits, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
+  if (int e = gemm_common_checks("w4a4_gemm", qwe, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
     return e;
   if (!qa || !sxp) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
   if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
@@ -200,7 +200,7 @@ int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe
       (int64_t)N * (K / group) * 4 > INT32_MAX)
     return fail(SVDQ_ERR_SHAPE, "w4a4_gemm: M*K=%lld or N*K=%lld exceeds 2^31-1 bytes; split the call",
                 (long long)M * K, (long long)N * K);
-  svdq::GemmParams p = gemm_params(nullptr, sw, mid, splits, l1cat, RTp, bias, M, N, K, y, ldy);
+  svdq::GemmParams p = gemm_params(nullptr, sw, mid, l1cat, RTp, bias, M, N, K, y, ldy);
   p.qwe = static_cast<const uint8_t*>(qwe);
   p.qa = static_cast<const uint8_t*>(qa);
   p.sxp = static_cast<const uint32_t*>(sxp);
@@ -208,15 +208,15 @@ int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe
   return launched(svdq::launch_w4a4(p, group, operand, out_f32 == 1, stream), "w4a4_gemm");
 }
 
-int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const float* mid,
-                    int splits, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
-                    void* y, int64_t ldy, int out_f32, hipStream_t stream) {
-  if (int e = gemm_common_checks("w4a16_gemm", qw, sw, mid, splits, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
+int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const void* mid,
+                    const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group, void* y,
+                    int64_t ldy, int out_f32, hipStream_t stream) {
+  if (int e = gemm_common_checks("w4a16_gemm", qw, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
     return e;
   if (!xhat) return fail(SVDQ_ERR_ARG, "w4a16_gemm: null pointer");
   if (ldxh < K || ldxh % 8 || !aligned16(xhat))
     return fail(SVDQ_ERR_ALIGN, "w4a16_gemm: xhat must be 16-byte aligned with ldxh >= K, ldxh %% 8 == 0");
-  svdq::GemmParams p = gemm_params(qw, sw, mid, splits, l1cat, RTp, bias, M, N, K, y, ldy);
+  svdq::GemmParams p = gemm_params(qw, sw, mid, l1cat, RTp, bias, M, N, K, y, ldy);
   p.xhat = static_cast<const uint16_t*>(xhat);
   p.ldxh = ldxh;
   return launched(svdq::launch_w4a16(p, group, out_f32 == 1, stream), "w4a16_gemm");

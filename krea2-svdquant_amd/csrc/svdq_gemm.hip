@@ -28,39 +28,41 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4
 
 
 
-// acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store.  mid holds one
-// partial per K split of the activation pass; they are added here in split order.
+// acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store.  mid is the activation
+// pass's finalized operand, bf16 hi and lo planes per row ([M, 2, RTp]); both planes go through
+// the bf16 MFMA, so the low-rank term carries the f32 mid to 2^-18.  Two 16-column steps per
+// iteration, their twelve loads issued together (one memory latency per 32 columns of RTp).
 template <bool OUT_F32>
 __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2], int m0, int n0,
                                          int lr, int h) {
-  const long split_stride = (long)p.M * p.RTp;
-  for (int s = 0; s < p.RTp / 16; ++s) {
-    u32x4 ahi[2], alo[2], b[2];
+  const int RTp = p.RTp;
+  const uint16_t* arow[2];
+  const uint16_t* brow[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int m = min(m0 + 32 * i + lr, p.M - 1);
-      const float* src = p.mid + (long)m * p.RTp + 16 * s + 8 * h;
-      f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
-      f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
-      for (int sp = 1; sp < p.splits; ++sp) {
-        v0 += *reinterpret_cast<const f32x4*>(src + sp * split_stride);
-        v1 += *reinterpret_cast<const f32x4*>(src + sp * split_stride + 4);
+  for (int i = 0; i < 2; ++i) arow[i] = p.midp + (long)min(m0 + 32 * i + lr, p.M - 1) * (2 * RTp) + 8 * h;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) brow[j] = p.l1cat + (long)min(n0 + 32 * j + lr, p.N - 1) * RTp + 8 * h;
+  for (int s = 0; s < RTp / 16; s += 2) {
+    u32x4 ahi[2][2], alo[2][2], b[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        ahi[u][i] = ld16(arow[i] + 16 * (s + u));
+        alo[u][i] = ld16(arow[i] + RTp + 16 * (s + u));
       }
-      const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-      split_hi_lo(v, ahi[i], alo[i]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[u][j] = ld16(brow[j] + 16 * (s + u));
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = min(n0 + 32 * j + lr, p.N - 1);
-      b[j] = ld16(p.l1cat + (long)n * p.RTp + 16 * s + 8 * h);
-    }
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        acc[i][j] = mfma_bf16_32x32x16(ahi[i], b[j], acc[i][j]);
-        acc[i][j] = mfma_bf16_32x32x16(alo[i], b[j], acc[i][j]);
-      }
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = mfma_bf16_32x32x16(ahi[u][i], b[u][j], acc[i][j]);
+          acc[i][j] = mfma_bf16_32x32x16(alo[u][i], b[u][j], acc[i][j]);
+        }
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -83,16 +85,6 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
 }
 
 // --------------------------------------------------------------------------- W4A4
-// Block tile 256x128, 8 waves in a 4x2 grid (64x64 per wave = 2x2 MFMA 32x32 tiles), one
-// K-group per stage.  Per group and output element the accumulator update is one FMA,
-// acc += P * S, where P is the exact group dot product from the 8-bit MFMA and S = sx * sw
-// comes from a bf16 MFMA whose K=2 operand pairs are (sx, sx) and (bf16 hi, bf16 lo) of the
-// fp16 weight scale, i.e. the scale product is exact too.
-//   MODE 0: operands e4m3, v_mfma_f32_32x32x64_f8f6f4 (P already float32);
-//   MODE 1: operands int8 16*q, 2x v_mfma_i32_32x32x32_i8 (P int32, converted; 1/256 in S).
-// Operand A (activation codes, 8-bit) comes from the activation pass; operand B is the
-// packed INT4 weight, converted while staging into LDS.  Global loads run two groups ahead
-// in two register sets; LDS is double buffered.
 // Global -> LDS DMA (global_load_lds_dword / _dwordx4): lane L of the wave writes its 4 (16)
 // bytes from base + off at LDS address lds + 4 L (16 L); `lds` (wave-uniform) goes in M0, as
 // an operand, so the compiler owns that register.  Issued as inline asm so that the compiler
@@ -113,10 +105,12 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 // Block tile 256 x 128, 8 waves in a 4 x 2 grid, wave tile 64 x 64 = 2 x 2 sub-tiles of
 // 32 x 32.  K advances 128 columns per pipeline stage (two groups of 64 or one of 128).  A
 // stage is moved global -> LDS entirely by DMA (activation codes, expanded weight codes, both
-// scale operands) into a ring of three LDS buffers, two stages ahead of the MFMAs; each wave
-// issues the same number of DMA instructions per stage, so `s_waitcnt vmcnt(DMA)` retires
-// all but the newest stage.  Global bases are scalars advanced per stage; per-lane offsets
-// are constants.
+// scale operands) into a ring of three LDS buffers; the DMA of stage s + 2 is issued during
+// stage s, in four parts spread over its four half-group steps (issuing a stage's 64 DMA
+// instructions per CU in one burst stalls the address unit and every wave behind it).  Each
+// wave issues the same number of DMA instructions per stage, so `s_waitcnt vmcnt` with the
+// count of the stage still in flight retires the one needed next.  Global bases are scalars
+// advanced per stage; per-lane offsets are constants.
 //
 // LDS operand tiles: rows of 128 bytes = 8 chunks of 16; chunk c of row r sits at chunk
 // position c ^ ((r >> 1) & 7).  The 16 lanes of a ds_read_b128 phase read one logical chunk
@@ -126,34 +120,29 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 // INT8 MFMA, int32 converted to fp32), S = sx (x) sw on a bf16 MFMA with K = 2: A = (sx, sx)
 // then zeros, B = (hi(sw), lo(sw)) then zeros (zero for lanes 32-63), so S = sx hi + sx lo
 // exactly; acc += P * S (one VALU FMA per output and group).
+//   MODE 0: operands e4m3, v_mfma_f32_32x32x64_f8f6f4 (P already float32);
+//   MODE 1: operands int8 16*q, 2x v_mfma_i32_32x32x32_i8 (P int32, converted; 1/256 in S).
 //
-// Ping-pong schedule: the two waves of each SIMD (waves w and w + 4) run offset by one slot.
-// In every slot between workgroup barriers one of them issues MFMAs (products and scales of
-// two sub-tiles, at raised priority) while the other rescales its previous two sub-tiles into
-// its accumulators.  A single wave barely overlaps its own VALU work with its own MFMAs on
-// this part (measured), so the overlap has to come from the pair.  With G == 64 the next
-// half-group's fragments are read from LDS at the top of the M slot, under the MFMAs, into a
-// second register set; with G == 128 (twice the fragment registers) they are read in the V
-// slot.
-//
-// Slots: the leading waves (0-3) run M(h) in slot 2h and V(h) in slot 2h + 1; the trailing
-// waves (4-7) run M(h) in slot 2h + 1 and V(h) in slot 2h + 2, where h counts half-groups.
-// Every wave passes the same 2H barriers.  Stage s + 2 is issued at the first V of stage s;
-// stage s + 1 is waited for before the barrier that ends the last slot before any wave reads
-// it (slot 2 HPS (s + 1) - 3 when reads happen in M slots, - 2 when in V slots).  The
-// placement of reads, waits and DMA issues was checked against a slot-by-slot simulation for
-// every group count up to 60 (no read before its stage landed, no buffer re-filled while a
-// slower wave still reads it, equal barrier counts).
+// Schedule: every wave runs the same free sequence of half-group steps (one row sub-tile i
+// against both column sub-tiles): products and scales on the MFMA, then the rescale FMAs.  The
+// two waves of a SIMD drift apart and one's FMAs run under the other's MFMAs; a workgroup
+// barrier once per stage (re-aligning all waves costs a few percent, measured) is the only
+// synchronisation.  With G == 64 the next half-group's fragments are read from LDS at the top
+// of each step into the second register set, a full step ahead of their use; the barrier sits
+// before the last step of a stage, after which the first fragments of the next stage are read.
+// With G == 128 (twice the fragment registers, one set) the next fragments are read after the
+// step's MFMAs, and the barrier follows the last step's MFMAs.
 template <int G, int MODE, bool OUT_F32>
 __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   constexpr int TBM = 256, TBN = 128, NT = 512, NBUF = 3;
   constexpr int KB = 128;                     // K columns per pipeline stage
   constexpr int GPS = KB / G;                 // groups per stage
-  constexpr int HPS = 2 * GPS;                // half-groups per stage
+  constexpr int HPS = 2 * GPS;                // half-group steps per stage
   constexpr int KS = G / 64;                  // 64-column MFMA steps per group
   constexpr int ADMA = TBM * KB / (16 * NT);  // A: 16-byte DMA chunks per thread per stage (4)
   constexpr int BDMA = TBN * KB / (16 * NT);  // B: 16-byte DMA chunks per thread per stage (2)
   constexpr int DMA = ADMA + BDMA + 2;        // DMA instructions per thread per stage
+  static_assert(ADMA == 4 && BDMA == 2, "the DMA parts below assume 4 A and 2 B chunks per thread");
   constexpr int XS = TBM + 4, WS = TBN + 4;   // scale words per group; the last 4 are zero
   constexpr int ABUF = TBM * KB, BBUF = TBN * KB;
   __shared__ __attribute__((aligned(1024))) uint8_t sA[NBUF * ABUF];
@@ -163,7 +152,6 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int trail = wave >> 2;                // 0: leading waves, 1: trailing waves
   const int wm = wave >> 1, wn = wave & 1;
   const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
   int bm, bn;
@@ -171,7 +159,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   const int m0 = bm * TBM, n0 = bn * TBN;
   const int K = p.K, ngroups = K / G, nstages = (K + KB - 1) / KB, H = 2 * ngroups;
 
-  // Operand DMA (as in w4a4_kernel): wave w, chunk i -> 8 rows of a stage tile.
+  // Operand DMA: wave w, chunk i -> 8 rows of a stage tile (lane / 8 = row, lane % 8 = chunk).
   uint32_t arow_o[ADMA], brow_o[BDMA];
   int ac16[ADMA], bc16[BDMA];
 #pragma unroll
@@ -186,6 +174,8 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
     bc16[i] = 16 * ((lane % 8) ^ ((row >> 1) & 7));
     brow_o[i] = (uint32_t)min(n0 + row, p.N - 1) * (uint32_t)K;
   }
+  // Scale DMA: one dword per lane; wave w covers words 64 w .. 64 w + 63 of the stage's
+  // GPS x TBM (GPS x TBN) scale tile, wrapping (the duplicate words hold the same values).
   const int xs = (64 * wave + lane) % (GPS * TBM), ws = (64 * wave + lane) % (GPS * TBN);
   const int xj = xs / TBM, wj = ws / TBN;
   const uint32_t xrowc = (uint32_t)min(m0 + xs % TBM, p.M - 1), wrowc = (uint32_t)min(n0 + ws % TBN, p.N - 1);
@@ -198,24 +188,28 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   const uint32_t ldsA = lds_offset(sA), ldsB = lds_offset(sB), ldsX = lds_offset(&sX[0][0][0]),
                  ldsW = lds_offset(&sW[0][0][0]);
 
-  auto gload = [&](int s, int buf) {
+  // Part q of stage s's DMA into ring buffer `buf`: q0 = both scale tiles + A chunk 0 (3
+  // instructions), q1 = A chunks 1-2, q2 = A chunk 3 + B chunk 0, q3 = B chunk 1.  Columns past
+  // K (a last stage of one group of 64) re-read the stage's last 16 bytes; never consumed.
+  auto gload_part = [&](int s, int buf, int q) {
     const int col0 = s * KB;
-    const bool tail = col0 + KB > K;
+    const int lim = col0 + KB > K ? K - col0 - 16 : KB;
     const uint8_t* qa_s = p.qa + col0;
     const uint8_t* qw_s = p.qwe + col0;
-    const int g0 = s * GPS;
-    const int jmax = ngroups - 1 - g0;
-    const uint32_t* sx_s = p.sxp + (long)g0 * p.M;
-    const uint32_t* sw_s = p.swp + (long)g0 * p.N;
-    dma4(sx_s, 4 * ((uint32_t)min(xj, jmax) * (uint32_t)p.M + xrowc), ldsX + 4 * ((buf * GPS + xjs) * XS + xbase));
-    dma4(sw_s, 4 * ((uint32_t)min(wj, jmax) * (uint32_t)p.N + wrowc), ldsW + 4 * ((buf * GPS + wjs) * WS + wbase));
-    const int lim = tail ? K - col0 - 16 : KB;
+    if (q == 0) {
+      const int g0 = s * GPS;
+      const int jmax = ngroups - 1 - g0;
+      const uint32_t* sx_s = p.sxp + (long)g0 * p.M;
+      const uint32_t* sw_s = p.swp + (long)g0 * p.N;
+      dma4(sx_s, 4 * ((uint32_t)min(xj, jmax) * (uint32_t)p.M + xrowc), ldsX + 4 * ((buf * GPS + xjs) * XS + xbase));
+      dma4(sw_s, 4 * ((uint32_t)min(wj, jmax) * (uint32_t)p.N + wrowc), ldsW + 4 * ((buf * GPS + wjs) * WS + wbase));
+    }
 #pragma unroll
     for (int i = 0; i < ADMA; ++i)
-      dma16(qa_s, arow_o[i] + min(ac16[i], lim), ldsA + buf * ABUF + (ADMA * wave + i) * 1024);
+      if ((i + 1) / 2 == q) dma16(qa_s, arow_o[i] + min(ac16[i], lim), ldsA + buf * ABUF + (ADMA * wave + i) * 1024);
 #pragma unroll
     for (int i = 0; i < BDMA; ++i)
-      dma16(qw_s, brow_o[i] + min(bc16[i], lim), ldsB + buf * BBUF + (BDMA * wave + i) * 1024);
+      if (q == 2 + i) dma16(qw_s, brow_o[i] + min(bc16[i], lim), ldsB + buf * BBUF + (BDMA * wave + i) * 1024);
   };
 
   f32x16 acc[2][2];
@@ -239,9 +233,9 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   const int wo0 = 4 * (h ? TBN : 64 * wn + lr), wo1 = 4 * (h ? TBN : 64 * wn + 32 + lr);
   u32x4 xop[2] = {u32x4{}, u32x4{}};
 
-  // Fragments.  G == 64 (RM): the next half-group's fragments are read at the start of the M
-  // slot, under the MFMAs, into the other set: A by half-group parity, B and the weight scales
-  // by group parity.  G == 128: one set, read in the V slot (the registers do not fit twice).
+  // Fragments.  G == 64 (RM): the next half-group's fragments are read a step ahead into the
+  // other set: A by half-group parity, B and the weight scales by group parity.  G == 128: one
+  // set (the registers do not fit twice).
   constexpr bool RM = G == 64;
   constexpr int NS = RM ? 2 : 1;
   u32x4 fa_[NS][KS][2], fb_[NS][2][KS][2], wop_[NS][2];
@@ -271,7 +265,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
       wop_[bi][1][0] = *reinterpret_cast<const uint32_t*>(w0 + wo1);
     }
   };
-  // Product of sub-tile (i, j): FP8 -> fp32 sums directly; INT8 -> int32 sums (converted in V).
+  // Product of sub-tile (i, j): FP8 -> fp32 sums directly; INT8 -> int32 sums (converted later).
   auto mfma_p8 = [&](int ai, int bi, int j) {
     f32x16 pf = mfma_fp8_32x32x64(fa_[ai][0], fb_[bi][j][0], f32x16{});
 #pragma unroll
@@ -287,57 +281,57 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
         pi = mfma_i8_32x32x32(__builtin_bit_cast(i32x4, fa_[ai][ks][t]), __builtin_bit_cast(i32x4, fb_[bi][j][ks][t]), pi);
     return pi;
   };
-  // Fence operands: every fragment register (both sets), so that reads issued before a fence
-  // have landed at it and nothing that reads them moves across it.
+  // Fence on every fragment register (both sets): reads issued before it have landed at it.
 #define SVDQ_FRAGS_1 "+v"(fa_[0][0][0]), "+v"(fa_[0][0][1]), "+v"(fb_[0][0][0][0]), "+v"(fb_[0][0][0][1]), \
     "+v"(fb_[0][1][0][0]), "+v"(fb_[0][1][0][1]), "+v"(xop[0]), "+v"(xop[1]), "+v"(wop_[0][0]), "+v"(wop_[0][1])
 #define SVDQ_FRAGS_2 "+v"(fa_[NS - 1][0][0]), "+v"(fa_[NS - 1][0][1]), "+v"(fb_[NS - 1][0][0][0]), \
     "+v"(fb_[NS - 1][0][0][1]), "+v"(fb_[NS - 1][1][0][0]), "+v"(fb_[NS - 1][1][0][1]), "+v"(wop_[NS - 1][0]), \
     "+v"(wop_[NS - 1][1])
-#define SVDQ_FRAGS_K2 "+v"(fa_[0][KS - 1][0]), "+v"(fa_[0][KS - 1][1]), "+v"(fb_[0][0][KS - 1][0]), \
-    "+v"(fb_[0][0][KS - 1][1]), "+v"(fb_[0][1][KS - 1][0]), "+v"(fb_[0][1][KS - 1][1])
   auto frag_fence = [&]() {
     if (RM) asm volatile("" : SVDQ_FRAGS_1, SVDQ_FRAGS_2::"memory");
-    else if (KS == 2) asm volatile("" : SVDQ_FRAGS_1, SVDQ_FRAGS_K2::"memory");
     else asm volatile("" : SVDQ_FRAGS_1::"memory");
   };
-  // End of an M slot: products complete (their registers are operands), priority back down.
-  auto end_m = [&](f32x16 (&P)[2], i32x16 (&PI)[2], f32x16 (&S)[2]) {
-    if (RM) frag_fence();   // next fragments, read at the top of this slot, have landed
-    if (MODE == 0)
-      asm volatile("s_setprio 0\n\ts_barrier" : "+v"(P[0]), "+v"(P[1]), "+v"(S[0]), "+v"(S[1])::"memory");
-    else
-      asm volatile("s_setprio 0\n\ts_barrier" : "+v"(PI[0]), "+v"(PI[1]), "+v"(S[0]), "+v"(S[1])::"memory");
-  };
-  // End of a V slot: accumulators written, fragments in place; priority up for the M slot.
-  auto end_v = [&]() {
-    frag_fence();
-    asm volatile("s_barrier\n\ts_setprio 1" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]),
-                 "+v"(acc[1][1])::"memory");
-  };
+#undef SVDQ_FRAGS_1
+#undef SVDQ_FRAGS_2
 
-  gload(0, 0);
-  gload(min(1, nstages - 1), 1);
+  // Stages 0 and 1 in flight, stage 0 landed everywhere; stage 2 goes out during stage 0.
+#pragma unroll
+  for (int q = 0; q < 4; ++q) gload_part(0, 0, q);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) gload_part(min(1, nstages - 1), 1, q);
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
   __syncthreads();
   read_half(0, 0, 0, 0, 0);
-  if (trail) {
-    end_v();      // the trailing waves sit out slot 0
-  } else {
-    frag_fence();
-    asm volatile("s_setprio 1" ::: "memory");
-  }
   for (int s = 0; s < nstages; ++s) {
+    const bool more = s + 1 < nstages;
+    const int sd = min(s + 2, nstages - 1);   // stage whose DMA goes out now (a re-read past the end)
 #pragma unroll
     for (int hh = 0; hh < HPS; ++hh) {
       const int hg = s * HPS + hh;            // half-group index
       if (hh > 0 && hg >= H) break;           // K has an odd number of groups of 64
       const int i = hh & 1, gi = hh >> 1;
       const int ai = RM ? i : 0, bi = RM ? gi : 0;
-      const int hn = hh + 1 == HPS ? 0 : hh + 1;   // next half-group's position in its stage
-      const int sn = hh + 1 == HPS ? s + 1 : s;
-      // ---- M slot: (RM) next fragments, then products and scales of sub-tiles (i, 0), (i, 1)
-      if (RM && hg + 1 < H) read_half(sn, hn >> 1, hn & 1, hn & 1, hn >> 1);
+      const bool last = hh == HPS - 1;
+      // This step's fragments in place and the previous step's rescale issued before the next
+      // reads go out (keeps one register set live per step).
+      asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(fa_[ai][0][0]),
+                   "+v"(fa_[ai][KS - 1][1]), "+v"(fb_[bi][0][0][0]), "+v"(fb_[bi][0][KS - 1][1]), "+v"(fb_[bi][1][0][0]),
+                   "+v"(fb_[bi][1][KS - 1][1]), "+v"(xop[i]), "+v"(wop_[bi][0]), "+v"(wop_[bi][1])::"memory");
+      if (RM) {
+        if (last) {
+          if (more) {
+            // Stage s + 1 landed here (only part 3 of stage s + 2, issued below, may be in
+            // flight besides the other parts of s + 2) and every wave's reads of stage s are
+            // complete before the barrier; then stage s + 1's first fragments.
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA - 1) : "memory");
+            frag_fence();
+            asm volatile("s_barrier" ::: "memory");
+            read_half(s + 1, 0, 0, 0, 0);
+          }
+        } else if (hg + 1 < H) {
+          read_half(s, (hh + 1) >> 1, (hh + 1) & 1, (hh + 1) & 1, (hh + 1) >> 1);
+        }
+      }
       f32x16 P[2], S[2];
       i32x16 PI[2];
 #pragma unroll
@@ -346,28 +340,32 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
         else PI[j] = mfma_pi(ai, bi, j);
         S[j] = mfma_bf16_32x32x16(xop[i], wop_[bi][j], f32x16{});
       }
-      // stage s + 1 must have landed before the barrier ending slot 2 HPS (s + 1) - (RM ? 3 : 2)
-      if (RM ? (trail && hh == HPS - 2) : (!trail && hh == HPS - 1))
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
-      end_m(P, PI, S);
-      // ---- V slot: issue stage s + 2, rescale, (not RM) read the next fragments
-      if (hh == 0) gload(min(s + 2, nstages - 1), (s + 2) % NBUF);
+      // Stage s + 2 -> buffer (s + 2) % 3, last read in stage s - 1 (before this stage's
+      // opening barrier).
+      if (RM) {
+        gload_part(sd, (s + 2) % NBUF, hh);
+      } else {
+        gload_part(sd, (s + 2) % NBUF, 2 * hh);
+        gload_part(sd, (s + 2) % NBUF, 2 * hh + 1);
+        if (!last) {
+          read_half(s, 0, 1, 0, 0);
+        } else if (more) {
+          // the step's MFMAs issued (their operands are overwritten next), stage s + 1 landed
+          if (MODE == 0) asm volatile("" : "+v"(P[0]), "+v"(P[1]), "+v"(S[0]), "+v"(S[1])::"memory");
+          else asm volatile("" : "+v"(PI[0]), "+v"(PI[1]), "+v"(S[0]), "+v"(S[1])::"memory");
+          asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DMA) : "memory");
+          read_half(s + 1, 0, 0, 0, 0);
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const f32x16 pf = MODE == 0 ? P[j] : __builtin_convertvector(PI[j], f32x16);
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(pf[r], S[j][r], acc[i][j][r]);
       }
-      if (!RM && hg + 1 < H) read_half(sn, hn >> 1, hn & 1, 0, 0);
-      if (RM ? (!trail && hh == HPS - 2) : (trail && hh == HPS - 2))
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
-      if (!(trail && hg == H - 1)) end_v();
     }
   }
-#undef SVDQ_FRAGS_1
-#undef SVDQ_FRAGS_2
-#undef SVDQ_FRAGS_K2
-  asm volatile("s_setprio 0\n\ts_waitcnt vmcnt(0)" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h);
 }

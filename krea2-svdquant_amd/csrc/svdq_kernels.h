@@ -19,7 +19,7 @@ struct ActParams {
   uint16_t* sx;             // [M, K/G] bf16, or [K/G, M] u32 (sx, sx) pairs when sx_pairs
   uint16_t* xhat;           // [M, ldxh] bf16 (null unless requested)
   long ldxh;
-  float* mid;               // [S, M, RTp]: one partial per K split (summed by the GEMM)
+  float* mid;               // [S, M, RTp]: one partial per K split (summed by launch_mid_finalize)
   int gps;                  // K-groups per split
   int exact;                // 1: IEEE division for x / s everywhere
   int sx_pairs;             // 1: sx as u32 bf16 pairs
@@ -34,8 +34,7 @@ struct GemmParams {
   const uint8_t* qwe;       // [N, K] 8-bit weight operand codes (W4A4)
   const uint16_t* sw;       // [N, K/G] fp16 weight scales (W4A16)
   const uint32_t* swp;      // [K/G, N] (bf16 hi, bf16 lo) pairs of the weight scales (W4A4)
-  const float* mid;         // [S, M, RTp] f32 low-rank/LoRA down projections, per K split
-  int splits;               // S
+  const uint16_t* midp;     // [M, 2, RTp] bf16 low-rank/LoRA down projections: hi plane, lo plane
   const uint16_t* l1cat;    // [N, RTp] bf16 up projections (zero padded)
   int RTp;
   const uint16_t* bias;     // [N] bf16 or null
@@ -47,6 +46,9 @@ struct GemmParams {
 int act_splits(int M, int K, int G);
 // oper: 0 = no codes (x_hat only), 1 = e4m3 operand codes, 2 = int8 16*q operand codes
 hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, int splits, hipStream_t st);
+// Sums the S split partials `part` [S, M, RTp] in split order and writes the GEMM epilogue's
+// operand midp [M, 2, RTp] (bf16 hi plane, then bf16 lo plane, hi + lo within 2^-18 of the f32 sum, relative).
+hipError_t launch_mid_finalize(const float* part, int S, int M, int RTp, uint16_t* midp, hipStream_t st);
 hipError_t launch_prepare_smooth(const uint16_t* s, float* srs, int K, hipStream_t st);
 // mode: 0 = e4m3 operands on the FP8 MFMA, 1 = int8 operands on the INT8 MFMA
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st);

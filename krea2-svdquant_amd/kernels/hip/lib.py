@@ -42,8 +42,8 @@ SIGNATURES = {
                             _P, _I, _P]),
     "svdq_prepare_weight_scales": (_I, [_P, _P, _I, _I, _I, _P]),
     "svdq_prepare_weight_operand": (_I, [_P, _P, _I, _I, _I, _P]),
-    "svdq_w4a4_gemm": (_I, [_P, _I, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
-    "svdq_w4a16_gemm": (_I, [_P, _L, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
+    "svdq_w4a4_gemm": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
+    "svdq_w4a16_gemm": (_I, [_P, _L, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
 }
 
 _lock = threading.Lock()

@@ -104,9 +104,10 @@ def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
 
     ``operand`` selects the W4A4 GEMM operand codes written (``OPERAND_E4M3`` / ``OPERAND_I8``)
     or none (``OPERAND_NONE``: x_hat only, the W4A16 path).  Returns
-    ``(qa uint8 [M, K], sx bf16 [M, K/G], qx uint8 [M, K/2], xhat bf16 [M, K], mid f32 [S, M, rtp])``
-    where ``mid`` holds one partial per K split (the GEMM adds them); outputs not requested are
-    empty tensors (``qx`` needs ``packed``, ``xhat`` ``want_xhat``).  With ``sx_pairs`` the
+    ``(qa uint8 [M, K], sx bf16 [M, K/G], qx uint8 [M, K/2], xhat bf16 [M, K], mid f32 [S + 1, M, rtp])``
+    where ``mid`` is the pass's workspace: ``mid[0]`` holds the GEMM epilogue operand (bf16 hi and
+    lo planes per row, see ``mid_values``), ``mid[1:]`` one partial per K split; outputs not
+    requested are empty tensors (``qx`` needs ``packed``, ``xhat`` ``want_xhat``).  With ``sx_pairs`` the
     scales come as int32 [K/G, M] (group-major) bf16 pairs (bits | bits << 16), the form
     ``w4a4_gemm`` takes.
     """
@@ -139,7 +140,7 @@ def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
     sx = torch.empty(sx_shape, dtype=torch.int32 if sx_pairs else torch.bfloat16, device=dev)
     qx = torch.empty((m, k // 2) if packed else (0,), dtype=torch.uint8, device=dev)
     xhat = torch.empty((m, k) if want_xhat else (0,), dtype=torch.bfloat16, device=dev)
-    mid = torch.empty((splits, m, rtp), dtype=torch.float32, device=dev)
+    mid = torch.empty((splits + 1, m, rtp), dtype=torch.float32, device=dev)
     flags = ((lib.SVDQ_ACT_OPERAND_E4M3 if operand == OPERAND_E4M3 else 0)
              | (lib.SVDQ_ACT_OPERAND_I8 if operand == OPERAND_I8 else 0)
              | (lib.SVDQ_ACT_PACKED if packed else 0) | (lib.SVDQ_ACT_XHAT if want_xhat else 0)
@@ -160,7 +161,7 @@ def _(x, srs, l2, lora_down, lora_mult, group_size, rtp, operand, packed, want_x
     sx = x.new_empty(sx_shape, dtype=torch.int32 if sx_pairs else torch.bfloat16)
     qx = x.new_empty((m, k // 2) if packed else (0,), dtype=torch.uint8)
     xhat = x.new_empty((m, k) if want_xhat else (0,), dtype=torch.bfloat16)
-    return qa, sx, qx, xhat, x.new_empty((_splits(m, k, group_size, rtp), m, rtp), dtype=torch.float32)
+    return qa, sx, qx, xhat, x.new_empty((_splits(m, k, group_size, rtp) + 1, m, rtp), dtype=torch.float32)
 
 
 _split_cache: dict[tuple[int, int, int, int], int] = {}
@@ -177,9 +178,27 @@ def _splits(m: int, k: int, group_size: int, rtp: int) -> int:
     return hit
 
 
+def mid_values(mid: Tensor) -> Tensor:
+    """The low-rank activations ``act_quant`` left at the head of its ``mid`` workspace, as float32
+    [M, rtp]: the bf16 hi plane plus the bf16 lo plane of each row."""
+    m, rtp = mid.shape[1], mid.shape[2]
+    planes = mid[0].contiguous().view(torch.bfloat16).view(m, 2, rtp).float()
+    return planes[:, 0] + planes[:, 1]
+
+
+def pack_mid(values: Tensor) -> Tensor:
+    """Inverse of ``mid_values`` for a float32 [M, rtp] tensor: a [1, M, rtp] workspace whose head
+    holds the hi / lo planes the GEMMs read (hi = bf16(v), lo = bf16(v - hi))."""
+    v = values.float().contiguous()
+    hi = v.to(torch.bfloat16)
+    lo = (v - hi.float()).to(torch.bfloat16)
+    return torch.stack((hi, lo), dim=1).contiguous().view(torch.float32).view(1, v.shape[0], v.shape[1])
+
+
 def _check_epilogue(mid: Tensor, l1cat: Tensor, bias: Optional[Tensor], m: int, n: int, dev: torch.device) -> None:
     _check_dev("mid", mid, dev, torch.float32)
-    _need(mid.dim() == 3 and mid.shape[1] == m, ValueError, f"mid must be [splits, {m}, RTp]")
+    _need(mid.dim() == 3 and mid.shape[0] >= 1 and mid.shape[1] == m, ValueError,
+          f"mid must be act_quant's workspace [S + 1, {m}, RTp]")
     _check_dev("l1cat", l1cat, dev, torch.bfloat16)
     _need(tuple(l1cat.shape) == (n, mid.shape[2]), ValueError,
           f"l1cat must be [{n}, {mid.shape[2]}], got {tuple(l1cat.shape)}")
@@ -227,8 +246,7 @@ def w4a4_gemm(qa: Tensor, sx_pairs: Tensor, weight_operand: Tensor, weight_scale
     _check_epilogue(mid, l1cat, bias, m, n, dev)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
     lib.call("svdq_w4a4_gemm", _vp(qa), operand, _vp(sx_pairs), _vp(weight_operand), _vp(weight_scale_pairs), _vp(mid),
-             mid.shape[0], _vp(l1cat), mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32),
-             _stream(dev))
+             _vp(l1cat), mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32), _stream(dev))
     return y
 
 
@@ -247,8 +265,8 @@ def w4a16_gemm(xhat: Tensor, qweight: Tensor, weight_scales: Tensor, mid: Tensor
     m, k = xhat.shape
     n = _check_gemm(qweight, weight_scales, mid, l1cat, bias, m, k, group_size, dev)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
-    lib.call("svdq_w4a16_gemm", _vp(xhat), k, _vp(qweight), _vp(weight_scales), _vp(mid), mid.shape[0],
-             _vp(l1cat), mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32), _stream(dev))
+    lib.call("svdq_w4a16_gemm", _vp(xhat), k, _vp(qweight), _vp(weight_scales), _vp(mid), _vp(l1cat),
+             mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32), _stream(dev))
     return y
 
 

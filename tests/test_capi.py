@@ -31,7 +31,7 @@ def test_group_support_and_workspace_sizing():
     assert h.svdq_group_supported(32) == 0
     s, mp = ctypes.c_int(), ctypes.c_int64()
     lib.call("svdq_act_quant_workspace", 4096, 6144, 64, 32, ctypes.byref(s), ctypes.byref(mp))
-    assert s.value >= 1 and mp.value == s.value * 4096 * 32
+    assert s.value >= 1 and mp.value == (s.value + 1) * 4096 * 32   # finalized head + one partial per split
     lib.call("svdq_act_quant_workspace", 256, 6144, 64, 32, ctypes.byref(s), ctypes.byref(mp))
     assert 1 < s.value <= 6144 // 64 // 4
 
@@ -52,16 +52,15 @@ def test_workspace_rejects_bad_arguments(args, status, needle):
 def test_gemm_rejects_null_and_misaligned_pointers_before_any_launch():
     nul = None
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_w4a4_gemm", nul, 0, nul, nul, nul, nul, 1, nul, 32, nul, 128, 128, 128, 64, nul, 128, 0, nul)
+        lib.call("svdq_w4a4_gemm", nul, 0, nul, nul, nul, nul, nul, 32, nul, 128, 128, 128, 64, nul, 128, 0, nul)
     assert ei.value.status == -1
     fake = ctypes.c_void_p(0x1000)
     odd = ctypes.c_void_p(0x1008)
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_w4a4_gemm", fake, 0, fake, odd, fake, fake, 1, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0,
-                 nul)
+        lib.call("svdq_w4a4_gemm", fake, 0, fake, odd, fake, fake, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0, nul)
     assert ei.value.status == -3
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_w4a16_gemm", fake, 100, fake, fake, fake, 1, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0, nul)
+        lib.call("svdq_w4a16_gemm", fake, 100, fake, fake, fake, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0, nul)
     assert ei.value.status == -3
     with pytest.raises(lib.SVDQError) as ei:
         lib.call("svdq_act_quant", fake, 128, fake, fake, 200, nul, 0, nul, 64, 128, 64, 224, lib.SVDQ_ACT_OPERAND_E4M3,
@@ -95,6 +94,6 @@ def test_prepare_entry_points_reject_bad_arguments_before_any_launch():
 def test_w4a4_gemm_rejects_operands_beyond_32bit_offsets():
     fake = ctypes.c_void_p(0x1000)
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_w4a4_gemm", fake, 0, fake, fake, fake, fake, 1, fake, 32, None, 65536, 128, 65536, 64, fake,
-                 128, 0, None)
+        lib.call("svdq_w4a4_gemm", fake, 0, fake, fake, fake, fake, fake, 32, None, 65536, 128, 65536, 64, fake, 128,
+                 0, None)
     assert ei.value.status == -2 and "2^31" in str(ei.value)

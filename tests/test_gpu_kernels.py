@@ -95,7 +95,8 @@ def test_act_quant_golden_bit_exact(dev, name):
     r = st.l2.shape[0]
     ad = st.adapters[0]
     lmid = ad.multiplier * (x.astype(np.float64) @ ad.down.astype(np.float64).T)
-    got = mid.double().sum(0).cpu().numpy()
+    _, ops = _ops()
+    got = ops.mid_values(mid).double().cpu().numpy()
     assert rel_l2(got[:, :r], fx["mid"]) < 1e-5
     assert rel_l2(got[:, r:r + ad.rank], lmid) < 1e-5
     assert (got[:, r + ad.rank:] == 0).all()
@@ -131,7 +132,24 @@ def test_act_quant_random_shapes_bit_exact(dev, m, k, g):
     assert np.array_equal(qa.cpu().numpy(), operand_bytes(codes, "e4m3"))
     assert np.array_equal(bf16_bits_of(sx), nm.bf16_bits(sxo))
     ref_mid = xh.astype(np.float64) @ st.l2.astype(np.float64).T
-    assert rel_l2(mid.double().sum(0).cpu().numpy()[:, :32], ref_mid) < 1e-5
+    _, ops = _ops()
+    assert rel_l2(ops.mid_values(mid).double().cpu().numpy()[:, :32], ref_mid) < 1e-5
+    _check_mid_head(mid)
+
+
+def _check_mid_head(mid):
+    """The workspace head is the split partials summed in split order (float32), then split into
+    bf16 hi = bf16(v) and lo = bf16(v - hi): bit for bit."""
+    part = mid[1:].float()
+    v = part[0].clone()
+    for s in range(1, part.shape[0]):
+        v = v + part[s]
+    hi = v.to(torch.bfloat16)
+    lo = (v - hi.float()).to(torch.bfloat16)
+    m, rtp = v.shape
+    planes = mid[0].contiguous().view(torch.bfloat16).view(m, 2, rtp)
+    assert torch.equal(planes[:, 0].view(torch.int16), hi.view(torch.int16))
+    assert torch.equal(planes[:, 1].view(torch.int16), lo.view(torch.int16))
 
 
 def _layer_outputs(x_np, st, dev, mode, out_f32, operand="e4m3"):
