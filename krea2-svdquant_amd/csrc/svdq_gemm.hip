@@ -28,13 +28,14 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4
 
 
 
-// acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store.  mid is the activation
+// acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store (directly, or through the
+// wave's 8 KB LDS region `stage` when it is given).  mid is the activation
 // pass's finalized operand, bf16 hi and lo planes per row ([M, 2, RTp]); both planes go through
 // the bf16 MFMA, so the low-rank term carries the f32 mid to 2^-18.  Two 16-column steps per
 // iteration, their twelve loads issued together (one memory latency per 32 columns of RTp).
 template <bool OUT_F32>
 __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2], int m0, int n0,
-                                         int lr, int h) {
+                                         int lr, int h, uint8_t* stage) {
   const int RTp = p.RTp;
   const uint16_t* arow[2];
   const uint16_t* brow[2];
@@ -54,6 +55,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
 #pragma unroll
       for (int j = 0; j < 2; ++j) b[u][j] = ld16(brow[j] + 16 * (s + u));
     }
+    // all twelve loads in flight before the first MFMA waits on one of them
+    asm volatile("" : "+v"(ahi[0][0]), "+v"(ahi[0][1]), "+v"(ahi[1][0]), "+v"(ahi[1][1]), "+v"(alo[0][0]),
+                 "+v"(alo[0][1]), "+v"(alo[1][0]), "+v"(alo[1][1]), "+v"(b[0][0]), "+v"(b[0][1]), "+v"(b[1][0]),
+                 "+v"(b[1][1]));
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -64,23 +69,72 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
           acc[i][j] = mfma_bf16_32x32x16(alo[u][i], b[u][j], acc[i][j]);
         }
   }
+  float bv[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = n0 + 32 * j + lr;
-    if (n >= p.N) continue;
-    const float bv = p.bias ? bf16f(p.bias[n]) : 0.0f;
+    bv[j] = p.bias && n < p.N ? bf16f(p.bias[n]) : 0.0f;
+  }
+  if (stage == nullptr) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 32 * j + lr;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (m >= p.M) continue;
+          const float v = acc[i][j][r] + bv[j];
+          if (OUT_F32)
+            reinterpret_cast<float*>(p.y)[(long)m * p.ldy + n] = v;
+          else
+            reinterpret_cast<uint16_t*>(p.y)[(long)m * p.ldy + n] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+        }
+    }
+    return;
+  }
+  // Staged: per 32-row half of the wave tile, the values go to the wave's LDS region (rows of
+  // 64 values, 16-byte chunk c of row r at c ^ (CPR / 2) when (r >> 2) is odd, so the two
+  // half-waves, 4 rows apart, write disjoint banks) and come back as 16-byte row chunks for
+  // coalesced stores.
+  constexpr int ES = OUT_F32 ? 4 : 2;         // bytes per value
+  constexpr int CPR = 64 * ES / 16;           // 16-byte chunks per row
+  constexpr int VPC = 16 / ES;                // values per chunk
+  const bool vec = (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.ldy % VPC == 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (m >= p.M) continue;
-        const float v = acc[i][j][r] + bv;
-        if (OUT_F32)
-          reinterpret_cast<float*>(p.y)[(long)m * p.ldy + n] = v;
-        else
-          reinterpret_cast<uint16_t*>(p.y)[(long)m * p.ldy + n] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+        const int row = 8 * (r >> 2) + 4 * h + (r & 3), col = 32 * j + lr;
+        const int pos = (col / VPC) ^ ((row >> 2) & 1 ? CPR / 2 : 0);
+        uint8_t* dst = stage + row * (64 * ES) + pos * 16 + (col % VPC) * ES;
+        const float v = acc[i][j][r] + bv[j];
+        if (OUT_F32) *reinterpret_cast<float*>(dst) = v;
+        else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
       }
+#pragma unroll
+    for (int it = 0; it < CPR / 2; ++it) {
+      const int idx = 64 * it + (h << 5 | lr), row = idx / CPR, c = idx % CPR;
+      const int pos = c ^ ((row >> 2) & 1 ? CPR / 2 : 0);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * (64 * ES) + pos * 16);
+      const int m = m0 + 32 * i + row, n = n0 + c * VPC;
+      if (m >= p.M) continue;
+      uint8_t* out = reinterpret_cast<uint8_t*>(p.y) + ((long)m * p.ldy + n) * ES;
+      if (vec && n + VPC <= p.N) {
+        st16(out, v);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VPC; ++e) {
+          if (n + e >= p.N) break;
+          if (OUT_F32) reinterpret_cast<uint32_t*>(out)[e] = v[e];
+          else reinterpret_cast<uint16_t*>(out)[e] = (uint16_t)(v[e / 2] >> (16 * (e % 2)));
+        }
+      }
+    }
   }
 }
 
@@ -297,14 +351,18 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   // Stages 0 and 1 in flight, stage 0 landed everywhere; stage 2 goes out during stage 0.
 #pragma unroll
   for (int q = 0; q < 4; ++q) gload_part(0, 0, q);
+  if (nstages > 1) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) gload_part(min(1, nstages - 1), 1, q);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
+    for (int q = 0; q < 4; ++q) gload_part(1, 1, q);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
   __syncthreads();
   read_half(0, 0, 0, 0, 0);
   for (int s = 0; s < nstages; ++s) {
     const bool more = s + 1 < nstages;
-    const int sd = min(s + 2, nstages - 1);   // stage whose DMA goes out now (a re-read past the end)
+    const bool ahead = s + 2 < nstages;       // stage s + 2 exists: its DMA goes out in this stage
 #pragma unroll
     for (int hh = 0; hh < HPS; ++hh) {
       const int hg = s * HPS + hh;            // half-group index
@@ -320,10 +378,11 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
       if (RM) {
         if (last) {
           if (more) {
-            // Stage s + 1 landed here (only part 3 of stage s + 2, issued below, may be in
-            // flight besides the other parts of s + 2) and every wave's reads of stage s are
-            // complete before the barrier; then stage s + 1's first fragments.
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA - 1) : "memory");
+            // Stage s + 1 landed here (parts 0-2 of stage s + 2 may be in flight; part 3 goes
+            // out below) and every wave's reads of stage s are complete before the barrier;
+            // then stage s + 1's first fragments.
+            if (ahead) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA - 1) : "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             frag_fence();
             asm volatile("s_barrier" ::: "memory");
             read_half(s + 1, 0, 0, 0, 0);
@@ -343,17 +402,20 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
       // Stage s + 2 -> buffer (s + 2) % 3, last read in stage s - 1 (before this stage's
       // opening barrier).
       if (RM) {
-        gload_part(sd, (s + 2) % NBUF, hh);
+        if (ahead) gload_part(s + 2, (s + 2) % NBUF, hh);
       } else {
-        gload_part(sd, (s + 2) % NBUF, 2 * hh);
-        gload_part(sd, (s + 2) % NBUF, 2 * hh + 1);
+        if (ahead) {
+          gload_part(s + 2, (s + 2) % NBUF, 2 * hh);
+          gload_part(s + 2, (s + 2) % NBUF, 2 * hh + 1);
+        }
         if (!last) {
           read_half(s, 0, 1, 0, 0);
         } else if (more) {
           // the step's MFMAs issued (their operands are overwritten next), stage s + 1 landed
           if (MODE == 0) asm volatile("" : "+v"(P[0]), "+v"(P[1]), "+v"(S[0]), "+v"(S[1])::"memory");
           else asm volatile("" : "+v"(PI[0]), "+v"(PI[1]), "+v"(S[0]), "+v"(S[1])::"memory");
-          asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DMA) : "memory");
+          if (ahead) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DMA) : "memory");
+          else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
           read_half(s + 1, 0, 0, 0, 0);
         }
       }
@@ -365,9 +427,10 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
       }
     }
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h);
+  // No DMA is in flight (none goes out in the last stage); once every wave is past its last
+  // reads, the operand buffers hold the output staging regions.
+  __syncthreads();
+  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, sA + wave * 8192);
 }
 
 // Weight operand of the W4A4 GEMM, once per layer: each packed dword (8 nibbles, k0 in the
@@ -491,7 +554,7 @@ __global__ void __launch_bounds__(NTHR) w4a16_kernel(GemmParams p) {
     __syncthreads();
   }
 
-  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h);
+  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, nullptr);
 }
 
 }  // namespace

@@ -185,6 +185,8 @@ def test_layer_golden(dev, name, mode):
     (64, 256, 1152, 64, 32, 32, False),   # 18 groups: 9 stages
     (96, 320, 384, 128, 32, 0, True),     # group 128: 3 stages
     (33, 128, 896, 128, 64, 64, False),   # group 128: 7 stages
+    (70, 100, 256, 64, 32, 0, True),      # two stages; N % 8 != 0 (element stores at the tile edge)
+    (50, 136, 128, 128, 32, 32, False),   # group 128: a single stage
 ])
 @pytest.mark.parametrize("mode", ["w4a4", "w4a16"])
 def test_layer_random_shapes(dev, m, n, k, g, r, rl, bias, mode):
