@@ -45,10 +45,14 @@ typedef enum svdq_status {
 #define SVDQ_ACT_OPERAND_I8 16u   /* quantize: write scales sx and int8 (16*q) operand codes qa */
 #define SVDQ_ACT_SX_PAIRS 32u     /* quantize: write sx as u32 bf16 pairs (sx | sx << 16), the
                                      form svdq_w4a4_gemm takes (its scale-MFMA operand)        */
+#define SVDQ_ACT_OPERAND_E3M2 64u /* quantize: write scales sx and e3m2 (FP6) operand codes qa in
+                                     the planar layout (see svdq_act_quant)                       */
 
 /* Operand formats of svdq_w4a4_gemm (must match the SVDQ_ACT_OPERAND_* flag used). */
 #define SVDQ_OPERAND_E4M3 0    /* FP8 MFMA (v_mfma_f32_32x32x64_f8f6f4): every INT4 code is exact */
 #define SVDQ_OPERAND_I8 1      /* INT8 MFMA (v_mfma_i32_32x32x32_i8) on 16*q                     */
+#define SVDQ_OPERAND_E3M2 2    /* FP6 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4, e3m2 x e3m2), twice the
+                                  FP8 rate: every INT4 code is an exact e3m2 value; planar layout */
 
 /* Library version string. */
 const char* svdq_version(void);
@@ -82,9 +86,14 @@ int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int6
  *          SVDQ_ACT_SX_PAIRS u32 [K/group, M] (group-major) holding (bits | bits << 16)
  *     qa : u8 [M, K] operand codes of the W4A4 GEMM: the code of k sits at byte
  *          8*(k/8) + perm(k%8), perm = {0,4,1,5,2,6,3,7} (even k of a chunk of 8, then odd k);
- *          e4m3(q) or int8 16*q
+ *          e4m3(q) or int8 16*q.  SVDQ_ACT_OPERAND_E3M2: u8 [Mp * K * 3/4], Mp = M rounded up to
+ *          even, planar: for k-step t = k / 64 and half h = (k / 32) % 2 the row's 32 e3m2
+ *          codes are contiguous 6-bit fields (field f = code of k = 64 t + 32 h + f) in 24 bytes,
+ *          bytes 0-15 at Q[t][h][Mp][16] (offset 0), bytes 16-23 at P[t][h][Mp][8] (offset
+ *          Mp * K / 2); rows of the padding are not written
  *     qx : u8 [M, K/2] canonical packed codes (pack.py:47-56), if SVDQ_ACT_PACKED
  *   xhat     : bf16 [M, ldxh] (SVDQ_ACT_XHAT; with a quantizing flag only for e4m3)
+ *   E3M2 needs K % 64 == 0 (always true: group 64 or 128) and a 16-byte aligned qa.
  *   mid      : workspace of svdq_act_quant_workspace's mid_floats floats.  Output at its head:
  *              bf16 [M, 2, RTp], per row the hi plane then the lo plane of the f32 low-rank
  *              activations (hi + lo within 2^-18 relative), whose columns are [0, r) = x_hat @ l2^T,
@@ -108,7 +117,9 @@ int svdq_prepare_weight_scales(const void* sw, void* swp, int N, int ngroups, in
  * in the byte order and `operand` format of svdq_act_quant's qa.  No reference counterpart:
  * the GEMM streams both operands into LDS without unpacking, trading N*K bytes of HBM for
  * the per-tile conversion work.
- *   qw : u8 [N, K/2]      qwe : u8 [N, K] (output);  K % 16 == 0 */
+ *   qw : u8 [N, K/2]      qwe : u8 [N, K] (output);  K % 16 == 0
+ *   SVDQ_OPERAND_E3M2: qwe u8 [Np * K * 3/4], Np = N rounded up to even, in the planar layout
+ *   of svdq_act_quant's e3m2 qa (rows n); K % 64 == 0 */
 int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int operand, hipStream_t stream);
 
 /* W4A4 GEMM with fused epilogue.  Replaces the residual product of reference
@@ -116,11 +127,12 @@ int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int ope
  * low-rank add + bias of generic_int4.py:84-133 / svd.py:159-163 and the LoRA add of
  * runtime/linear.py:158-160:
  *   y = sum_g sx sw (qa . qw)_g + mid @ l1cat^T + bias
- *   qa : u8 [M, K] operand codes (svdq_act_quant) in `operand` format (SVDQ_OPERAND_*)
+ *   qa : u8 [M, K] operand codes (svdq_act_quant) in `operand` format (SVDQ_OPERAND_*); the
+ *        planar [Mp * K * 3/4] bytes for SVDQ_OPERAND_E3M2
  *   sxp: u32 [K/group, M] bf16 pairs (svdq_act_quant with SVDQ_ACT_SX_PAIRS)
- *   qwe: u8 [N, K] from svdq_prepare_weight_operand (same format)
+ *   qwe: u8 [N, K] from svdq_prepare_weight_operand (same format; planar for E3M2)
  *   swp: u32 [K/group, N] from svdq_prepare_weight_scales (same operand format)
- *   M*K and N*K below 2^31 (larger problems are split over rows by the caller)
+ *   E4M3 / I8: M*K and N*K below 2^31 (larger problems are split over rows by the caller)
  *   mid: bf16 [M, 2, RTp] (hi, lo planes) = the head of svdq_act_quant's mid workspace
  *   l1cat : bf16 [N, RTp] = [l1 | up_1 | ... | 0]
  *   bias: bf16 [N] or NULL     y : [M, ldy], bf16 (out_f32 = 0) or f32 (out_f32 = 1) */

@@ -75,7 +75,12 @@ __device__ __forceinline__ void smooth64(const u32x4 (&xr)[8], cfloat_ptr sv, cf
   range_bad = bad;
 }
 
-// OPER: GEMM operand codes written (0 none, 1 e4m3, 2 int8 16*q).
+// OPER: GEMM operand codes written (0 none, 1 e4m3, 2 int8 16*q, 3 e3m2 planar).  The e3m2 layout
+// of an [R, K] operand, Rp = R rounded up to even: for k-step t (64 columns) and half h (columns
+// 64 t + 32 h ..), the first 16 bytes of each row's 24-byte field vector in plane Q[t][h][Rp][16]
+// (at byte 0), the last 8 in plane P[t][h][Rp][8] (at byte Rp K / 2) -- rows contiguous, so the
+// lanes (rows) of a wave store whole 1 KB / 512 B runs and the GEMM's DMA and LDS reads stream
+// whole planes.
 template <int G, int NT, int OPER, bool XHAT>
 __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
   constexpr int HB = G / 64;             // 64-column blocks per group
@@ -138,6 +143,7 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
       for (int b = 0; b < HB; ++b) {
         u32x4 op[4];
         uint32_t nib[8];
+        f32x16 ex, ey;                      // OPER 3: the half's even-k and odd-k codes
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
           float t[8];
@@ -155,6 +161,21 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
             op[c >> 1][2 * (c & 1)] = lo;
             op[c >> 1][2 * (c & 1) + 1] = hi;
           }
+          if (OPER == 3) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              ex[4 * (c & 3) + e] = t[2 * e];
+              ey[4 * (c & 3) + e] = t[2 * e + 1];
+            }
+            if ((c & 3) == 3 && rok) {
+              // k-step kt, half c / 4: 16 bytes to plane Q, 8 bytes to plane P
+              const u32x6 f = codes_to_e3m2(ex, ey);
+              const long mp = (p.M + 1) & ~1;      // plane rows, padded to even
+              const long plane = (long)((g * HB + b) * 2 + (c >> 2)) * mp + rowc;
+              *reinterpret_cast<u32x4*>(p.qa + plane * 16) = u32x4{f[0], f[1], f[2], f[3]};
+              *reinterpret_cast<u32x2*>(p.qa + mp * (K / 2) + plane * 8) = u32x2{f[4], f[5]};
+            }
+          }
           if (OPER == 2 || p.qx) {
             uint32_t w = 0;
 #pragma unroll
@@ -169,9 +190,11 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
           }
         }
         if (rok) {
-          uint8_t* od = p.qa + rowc * K + g * G + 64 * b;
+          if (OPER != 3) {
+            uint8_t* od = p.qa + rowc * K + g * G + 64 * b;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(od + 16 * q) = op[q];
+            for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(od + 16 * q) = op[q];
+          }
           if (p.qx) {
             uint8_t* dst = p.qx + rowc * (K / 2) + (g * G + 64 * b) / 2;
             *reinterpret_cast<u32x4*>(dst) = u32x4{nib[0], nib[1], nib[2], nib[3]};
@@ -319,6 +342,7 @@ hipError_t launch_act_nt(const ActParams& p, int nt, dim3 grid, hipStream_t st) 
 
 template <int G>
 hipError_t launch_act_g(const ActParams& p, int nt, int oper, bool xhat, dim3 grid, hipStream_t st) {
+  if (oper == 3 && !xhat) return launch_act_nt<G, 3, false>(p, nt, grid, st);
   if (oper == 1 && !xhat) return launch_act_nt<G, 1, false>(p, nt, grid, st);
   if (oper == 1 && xhat) return launch_act_nt<G, 1, true>(p, nt, grid, st);
   if (oper == 2 && !xhat) return launch_act_nt<G, 2, false>(p, nt, grid, st);

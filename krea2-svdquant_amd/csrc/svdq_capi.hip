@@ -73,16 +73,18 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
                    int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
                    float* mid, int splits, hipStream_t stream) {
   const unsigned known = SVDQ_ACT_PACKED | SVDQ_ACT_XHAT | SVDQ_ACT_EXACT_DIV | SVDQ_ACT_OPERAND_E4M3 |
-                         SVDQ_ACT_OPERAND_I8 | SVDQ_ACT_SX_PAIRS;
+                         SVDQ_ACT_OPERAND_I8 | SVDQ_ACT_SX_PAIRS | SVDQ_ACT_OPERAND_E3M2;
   if (flags & ~known) return fail(SVDQ_ERR_ARG, "act_quant: unknown flags 0x%x", flags);
   const bool e4m3 = flags & SVDQ_ACT_OPERAND_E4M3, i8 = flags & SVDQ_ACT_OPERAND_I8;
-  const bool quant = e4m3 || i8, want_xhat = flags & SVDQ_ACT_XHAT, packed = flags & SVDQ_ACT_PACKED;
-  if (e4m3 && i8) return fail(SVDQ_ERR_ARG, "act_quant: two operand formats requested");
+  const bool e3m2 = flags & SVDQ_ACT_OPERAND_E3M2;
+  const bool quant = e4m3 || i8 || e3m2, want_xhat = flags & SVDQ_ACT_XHAT, packed = flags & SVDQ_ACT_PACKED;
+  if ((int)e4m3 + (int)i8 + (int)e3m2 > 1) return fail(SVDQ_ERR_ARG, "act_quant: two operand formats requested");
   if (!quant && !want_xhat) return fail(SVDQ_ERR_ARG, "act_quant: neither an operand format nor XHAT requested");
   if (packed && !quant) return fail(SVDQ_ERR_ARG, "act_quant: PACKED needs an operand format");
   const bool pairs = flags & SVDQ_ACT_SX_PAIRS;
   if (pairs && !quant) return fail(SVDQ_ERR_ARG, "act_quant: SX_PAIRS needs an operand format");
-  if (i8 && want_xhat) return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: XHAT with int8 operands has no kernel");
+  if ((i8 || e3m2) && want_xhat)
+    return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: XHAT with int8 or e3m2 operands has no kernel");
   if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant: M=%d", M);
   if (int e = check_group(group, K)) return e;
   if (r < 1 || rl < 0) return fail(SVDQ_ERR_SHAPE, "act_quant: rank r=%d rl=%d", r, rl);
@@ -125,7 +127,7 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
   p.gps = (ngroups + splits - 1) / splits;
   p.exact = (flags & SVDQ_ACT_EXACT_DIV) ? 1 : 0;
   p.sx_pairs = pairs ? 1 : 0;
-  if (int e = launched(svdq::launch_act(p, group, nt, e4m3 ? 1 : (i8 ? 2 : 0), want_xhat, splits, stream),
+  if (int e = launched(svdq::launch_act(p, group, nt, e4m3 ? 1 : (i8 ? 2 : (e3m2 ? 3 : 0)), want_xhat, splits, stream),
                        "act_quant"))
     return e;
   return launched(svdq::launch_mid_finalize(p.mid, splits, M, RTp, reinterpret_cast<uint16_t*>(mid), stream),
@@ -166,7 +168,7 @@ static svdq::GemmParams gemm_params(const void* qw, const void* sw, const void* 
 int svdq_prepare_weight_scales(const void* sw, void* swp, int N, int ngroups, int operand, hipStream_t stream) {
   if (!sw || !swp) return fail(SVDQ_ERR_ARG, "prepare_weight_scales: null pointer");
   if (N <= 0 || ngroups <= 0) return fail(SVDQ_ERR_ARG, "prepare_weight_scales: N=%d ngroups=%d", N, ngroups);
-  if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
+  if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8 && operand != SVDQ_OPERAND_E3M2)
     return fail(SVDQ_ERR_ARG, "prepare_weight_scales: operand format %d", operand);
   return launched(svdq::launch_weight_scale_pairs(static_cast<const uint16_t*>(sw), static_cast<uint32_t*>(swp), N,
                                                   ngroups, operand, stream),
@@ -176,11 +178,13 @@ int svdq_prepare_weight_scales(const void* sw, void* swp, int N, int ngroups, in
 int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int operand, hipStream_t stream) {
   if (!qw || !qwe) return fail(SVDQ_ERR_ARG, "prepare_weight_operand: null pointer");
   if (N <= 0 || K <= 0 || K % 16) return fail(SVDQ_ERR_SHAPE, "prepare_weight_operand: N=%d K=%d (K %% 16 == 0)", N, K);
-  if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
+  if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8 && operand != SVDQ_OPERAND_E3M2)
     return fail(SVDQ_ERR_ARG, "prepare_weight_operand: operand format %d", operand);
+  if (operand == SVDQ_OPERAND_E3M2 && K % 64)
+    return fail(SVDQ_ERR_SHAPE, "prepare_weight_operand: K=%d (e3m2 needs K %% 64 == 0)", K);
   if (!aligned16(qw) || !aligned16(qwe)) return fail(SVDQ_ERR_ALIGN, "prepare_weight_operand: pointers must be 16-byte aligned");
-  return launched(svdq::launch_weight_operand(static_cast<const uint8_t*>(qw), static_cast<uint8_t*>(qwe),
-                                              (long)N * (K / 8), operand, stream),
+  return launched(svdq::launch_weight_operand(static_cast<const uint8_t*>(qw), static_cast<uint8_t*>(qwe), N, K,
+                                              operand, stream),
                   "prepare_weight_operand");
 }
 
@@ -191,13 +195,15 @@ int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe
   if (int e = gemm_common_checks("w4a4_gemm", qwe, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
     return e;
   if (!qa || !sxp) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
-  if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8)
+  if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8 && operand != SVDQ_OPERAND_E3M2)
     return fail(SVDQ_ERR_ARG, "w4a4_gemm: operand format %d", operand);
   if (!aligned16(qa) || !aligned16(qwe) || reinterpret_cast<uintptr_t>(sxp) % 4 || reinterpret_cast<uintptr_t>(swp) % 4)
     return fail(SVDQ_ERR_ALIGN, "w4a4_gemm: qa, qwe must be 16-byte aligned, sxp, swp 4-byte aligned");
-  // The kernel addresses qa and qwe with 32-bit byte offsets.
-  if ((int64_t)M * K > INT32_MAX || (int64_t)N * K > INT32_MAX || (int64_t)M * (K / group) * 4 > INT32_MAX ||
-      (int64_t)N * (K / group) * 4 > INT32_MAX)
+  // The 8-bit kernels address qa and qwe with 32-bit byte offsets (the e3m2 kernel with 64-bit
+  // plane bases and 32-bit row offsets).
+  if (operand != SVDQ_OPERAND_E3M2 &&
+      ((int64_t)M * K > INT32_MAX || (int64_t)N * K > INT32_MAX || (int64_t)M * (K / group) * 4 > INT32_MAX ||
+       (int64_t)N * (K / group) * 4 > INT32_MAX))
     return fail(SVDQ_ERR_SHAPE, "w4a4_gemm: M*K=%lld or N*K=%lld exceeds 2^31-1 bytes; split the call",
                 (long long)M * K, (long long)N * K);
   svdq::GemmParams p = gemm_params(nullptr, sw, mid, l1cat, RTp, bias, M, N, K, y, ldy);

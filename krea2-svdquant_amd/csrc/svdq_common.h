@@ -28,6 +28,8 @@ typedef __bf16   bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16   bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x2  __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4  __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x6  __attribute__((ext_vector_type(6)));
+typedef uint32_t u32x8  __attribute__((ext_vector_type(8)));
 
 // ---- bf16 / fp16 bit helpers ------------------------------------------------
 __device__ __forceinline__ float bf16lo(uint32_t d) { return __uint_as_float(d << 16); }
@@ -76,6 +78,26 @@ __device__ __forceinline__ f32x16 mfma_fp8_32x32x64(const u32x4 (&a)[2], const u
                     (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]};
   // format 0/0 = e4m3 x e4m3; E8M0 scale 127 = 2^0 on both sides
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
+}
+
+// e3m2 x e3m2 (FP6, format 3 on both sides): a lane's 32 codes are 6 dwords, given as the
+// 16-byte and 8-byte parts the GEMM reads from its two LDS planes; the instruction reads 6
+// registers, the two upper lanes of the 8-lane operand are left undefined.
+__device__ __forceinline__ f32x16 mfma_fp6_32x32x64(u32x4 aq, u32x2 ar, u32x4 bq, u32x2 br, f32x16 c) {
+  typedef int i32x8 __attribute__((ext_vector_type(8)));
+  const u32x4 ar4 = __builtin_shufflevector(ar, ar, 0, 1, -1, -1);
+  const u32x4 br4 = __builtin_shufflevector(br, br, 0, 1, -1, -1);
+  const i32x8 av = __builtin_bit_cast(i32x8, __builtin_shufflevector(aq, ar4, 0, 1, 2, 3, 4, 5, -1, -1));
+  const i32x8 bv = __builtin_bit_cast(i32x8, __builtin_shufflevector(bq, br4, 0, 1, 2, 3, 4, 5, -1, -1));
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 3, 3, 0, 127, 0, 127);
+}
+
+// e3m2 operand of 32 codes given as floats (k = 2i in x[i], k = 2i + 1 in y[i]):
+// v_cvt_scalef32_2xpk16_bf6 writes field 2i from x[i] and field 2i + 1 from y[i] (contiguous
+// 6-bit fields over 6 dwords), so field f holds k = f, the operand layout of the FP6 MFMA.
+// Exact: every INT4 code is an e3m2 value (8 = 1.0 x 2^3, 7 = 1.11b x 2^2, ...).
+__device__ __forceinline__ u32x6 codes_to_e3m2(f32x16 x, f32x16 y) {
+  return __builtin_bit_cast(u32x6, __builtin_amdgcn_cvt_scalef32_2xpk16_bf6_f32(x, y, 1.0f));
 }
 
 // ---- INT4 code conversion (8-bit MFMA operands) ---------------------------------

@@ -433,6 +433,227 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, sA + wave * 8192);
 }
 
+// W4A4 GEMM on the FP6 MFMA (e3m2 operands, v_mfma_scale_f32_32x32x64_f8f6f4 with format 3 on
+// both sides): the INT4 codes are exact e3m2 values and the FP6 MFMA runs at twice the FP8 rate.
+// The arithmetic (exact group sums P, scale products S on the bf16 MFMA, acc += P * S), the wave
+// grid, the free-running schedule and the epilogue are those of w4a4_kernel; the operands come in
+// the planar e3m2 layout of the activation pass, so the stage tiles are rows-contiguous planes:
+//   A: for each of the stage's 4 k-steps t and halves h, a plane of 256 rows x 16 bytes (Q) and
+//      one of 256 rows x 8 bytes (P) -- a lane's 6-register operand is its row's Q and P parts;
+//   B: the same with 128 rows.
+// A ds_read_b128 phase (16 lanes, 16 consecutive rows) and a ds_read_b64 phase (32 lanes, 32
+// rows) read contiguous bytes: no bank conflicts and no swizzle.  A stage is 256 columns of K
+// in a ring of two LDS buffers (80000 bytes each); stage s + 1 is moved in by DMA in parts
+// during the first half-group steps of stage s (wave w streams plane w of every operand and a
+// share of the scale tiles: 12 DMA instructions per wave per stage for G = 64) and waited for
+// before the barrier that ends stage s.  Rows of the planes are padded to an even count so that a
+// 16-byte DMA lane carries two 8-byte P rows.
+template <int G, bool OUT_F32>
+__global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
+  constexpr int TBM = 256, TBN = 128, NBUF = 2;
+  constexpr int KB = 256;                     // K columns per pipeline stage
+  constexpr int KT = KB / 64;                 // k-steps per stage
+  constexpr int GPS = KB / G;                 // groups per stage
+  constexpr int HPS = 2 * GPS;                // half-group steps per stage
+  constexpr int KS = G / 64;                  // k-steps per group
+  constexpr int AQ = KT * 2 * TBM * 16, AP = KT * 2 * TBM * 8, BQ = KT * 2 * TBN * 16, BP = KT * 2 * TBN * 8;
+  constexpr int XS = TBM + 4, WS = TBN + 4;   // scale words per group; the last 4 are zero
+  constexpr int SXD = (GPS * TBM + 511) / 512, SWD = (GPS * TBN + 511) / 512;   // scale DMAs per wave
+  constexpr int NDMA = 4 + 2 + 2 + 1 + SXD + SWD;                               // DMAs per wave per stage
+  constexpr int NPART = HPS > 2 ? HPS - 2 : 1;                                  // steps that issue DMA
+  constexpr int PER = (NDMA + NPART - 1) / NPART;
+  static_assert(KT * 2 == 8, "one plane per wave");
+  __shared__ __attribute__((aligned(1024))) uint8_t sAQ[NBUF][AQ];
+  __shared__ __attribute__((aligned(1024))) uint8_t sAP[NBUF][AP];
+  __shared__ __attribute__((aligned(1024))) uint8_t sBQ[NBUF][BQ];
+  __shared__ __attribute__((aligned(1024))) uint8_t sBP[NBUF][BP];
+  __shared__ __attribute__((aligned(16))) uint32_t sX[NBUF][GPS][XS];   // (sx, sx) bf16 pairs
+  __shared__ __attribute__((aligned(16))) uint32_t sW[NBUF][GPS][WS];   // (hi, lo) of sw
+
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
+  int bm, bn;
+  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
+  const int m0 = bm * TBM, n0 = bn * TBN;
+  const int K = p.K, ngroups = K / G, nkt = K / 64, nstages = (K + KB - 1) / KB, H = 2 * ngroups;
+  const int Mp = (p.M + 1) & ~1, Np = (p.N + 1) & ~1;
+
+  // Operand DMA, wave w <-> plane w = (k-step w / 2, half w % 2) of each operand.  Per-lane byte
+  // offsets within a plane (rows clamped into the operand; clamped rows are never stored).
+  uint32_t aq_o[4], ap_o[2], bq_o[2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) aq_o[c] = (uint32_t)min(m0 + 64 * c + lane, p.M - 1) * 16u;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) ap_o[c] = (uint32_t)min(m0 + 128 * c + 2 * lane, Mp - 2) * 8u;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) bq_o[c] = (uint32_t)min(n0 + 64 * c + lane, p.N - 1) * 16u;
+  const uint32_t bp_o = (uint32_t)min(n0 + 2 * lane, Np - 2) * 8u;
+  const long aP0 = (long)nkt * 2 * Mp * 16, bP0 = (long)nkt * 2 * Np * 16;   // P region offsets
+  if (tid < NBUF * GPS * 4) {
+    sX[tid / (4 * GPS)][(tid / 4) % GPS][TBM + tid % 4] = 0u;
+    sW[tid / (4 * GPS)][(tid / 4) % GPS][TBN + tid % 4] = 0u;
+  }
+  const uint32_t ldsAQ = lds_offset(sAQ), ldsAP = lds_offset(sAP), ldsBQ = lds_offset(sBQ),
+                 ldsBP = lds_offset(sBP), ldsX = lds_offset(&sX[0][0][0]), ldsW = lds_offset(&sW[0][0][0]);
+
+  // DMA d (0 .. NDMA-1) of stage s into buffer buf: 0-3 A Q rows 64 d.., 4-5 A P rows 128 (d-4)..,
+  // 6-7 B Q rows 64 (d-6).., 8 B P, then the scale words (64 per instruction, wrapping).
+  auto dma = [&](int s, int buf, int d) {
+    const int kt = min(s * KT + (wave >> 1), nkt - 1);    // a k-step past K re-reads the last one
+    const long pl = (long)(kt * 2 + (wave & 1));
+    if (d < 4) {
+      dma16(p.qa + pl * Mp * 16, aq_o[d], ldsAQ + buf * AQ + (wave * TBM + 64 * d) * 16);
+    } else if (d < 6) {
+      dma16(p.qa + aP0 + pl * Mp * 8, ap_o[d - 4], ldsAP + buf * AP + (wave * TBM + 128 * (d - 4)) * 8);
+    } else if (d < 8) {
+      dma16(p.qwe + pl * Np * 16, bq_o[d - 6], ldsBQ + buf * BQ + (wave * TBN + 64 * (d - 6)) * 16);
+    } else if (d == 8) {
+      dma16(p.qwe + bP0 + pl * Np * 8, bp_o, ldsBP + buf * BP + wave * TBN * 8);
+    } else {
+      const int g0 = s * GPS, jmax = ngroups - 1 - g0;
+      if (d < 9 + SXD) {
+        const int w0 = (512 * (d - 9) + 64 * wave) % (GPS * TBM), j = w0 / TBM, r0 = w0 % TBM;
+        const uint32_t off = 4u * ((uint32_t)min(j, jmax) * (uint32_t)p.M + (uint32_t)min(m0 + r0 + lane, p.M - 1));
+        dma4(p.sxp + (long)g0 * p.M, off, ldsX + 4 * ((buf * GPS + j) * XS + r0));
+      } else {
+        const int w0 = (512 * (d - 9 - SXD) + 64 * wave) % (GPS * TBN), j = w0 / TBN, r0 = w0 % TBN;
+        const uint32_t off = 4u * ((uint32_t)min(j, jmax) * (uint32_t)p.N + (uint32_t)min(n0 + r0 + lane, p.N - 1));
+        dma4(p.swp + (long)g0 * p.N, off, ldsW + 4 * ((buf * GPS + j) * WS + r0));
+      }
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  const int xo0 = 4 * (64 * wm + lr), xo1 = xo0 + 128;
+  const int wo0 = 4 * (h ? TBN : 64 * wn + lr), wo1 = 4 * (h ? TBN : 64 * wn + 32 + lr);
+  u32x4 xop[2] = {u32x4{}, u32x4{}};
+
+  // Fragments: Q (16 bytes) and P (8 bytes) parts per k-step.  G == 64 (RM): the next
+  // half-group's fragments are read a step ahead into the other set (A by half-group parity, B
+  // and the weight scales by group parity); G == 128: one set.
+  constexpr bool RM = G == 64;
+  constexpr int NS = RM ? 2 : 1;
+  u32x4 faq[NS][KS], fbq[NS][2][KS], wop_[NS][2];
+  u32x2 fap[NS][KS], fbp[NS][2][KS];
+#pragma unroll
+  for (int q = 0; q < NS; ++q) wop_[q][0] = wop_[q][1] = u32x4{};
+  auto read_half = [&](int buf, int gi, int i, int ai, int bi) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int pl = (gi * KS + ks) * 2 + h;
+      const int ra = pl * TBM + 64 * wm + 32 * i + lr;
+      faq[ai][ks] = *reinterpret_cast<const u32x4*>(&sAQ[buf][ra * 16]);
+      fap[ai][ks] = *reinterpret_cast<const u32x2*>(&sAP[buf][ra * 8]);
+      if (i == 0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int rb = pl * TBN + 64 * wn + 32 * j + lr;
+          fbq[bi][j][ks] = *reinterpret_cast<const u32x4*>(&sBQ[buf][rb * 16]);
+          fbp[bi][j][ks] = *reinterpret_cast<const u32x2*>(&sBP[buf][rb * 8]);
+        }
+      }
+    }
+    const uint8_t* x0 = reinterpret_cast<const uint8_t*>(&sX[buf][gi][0]);
+    xop[i][0] = *reinterpret_cast<const uint32_t*>(x0 + (i ? xo1 : xo0));
+    if (i == 0) {
+      const uint8_t* w0 = reinterpret_cast<const uint8_t*>(&sW[buf][gi][0]);
+      wop_[bi][0][0] = *reinterpret_cast<const uint32_t*>(w0 + wo0);
+      wop_[bi][1][0] = *reinterpret_cast<const uint32_t*>(w0 + wo1);
+    }
+  };
+  auto mfma_p6 = [&](int ai, int bi, int j) {
+    f32x16 pf = mfma_fp6_32x32x64(faq[ai][0], fap[ai][0], fbq[bi][j][0], fbp[bi][j][0], f32x16{});
+#pragma unroll
+    for (int ks = 1; ks < KS; ++ks) pf = mfma_fp6_32x32x64(faq[ai][ks], fap[ai][ks], fbq[bi][j][ks], fbp[bi][j][ks], pf);
+    return pf;
+  };
+  // Fence on every fragment register (both sets): reads issued before it have landed at it.
+#define SVDQ_FRAGS6_1 "+v"(faq[0][0]), "+v"(fap[0][0]), "+v"(fbq[0][0][0]), "+v"(fbp[0][0][0]), "+v"(fbq[0][1][0]), \
+    "+v"(fbp[0][1][0]), "+v"(xop[0]), "+v"(xop[1]), "+v"(wop_[0][0]), "+v"(wop_[0][1])
+#define SVDQ_FRAGS6_2 "+v"(faq[NS - 1][0]), "+v"(fap[NS - 1][0]), "+v"(fbq[NS - 1][0][0]), "+v"(fbp[NS - 1][0][0]), \
+    "+v"(fbq[NS - 1][1][0]), "+v"(fbp[NS - 1][1][0]), "+v"(wop_[NS - 1][0]), "+v"(wop_[NS - 1][1])
+  auto frag_fence = [&]() {
+    if (RM) asm volatile("" : SVDQ_FRAGS6_1, SVDQ_FRAGS6_2::"memory");
+    else asm volatile("" : SVDQ_FRAGS6_1::"memory");
+  };
+#undef SVDQ_FRAGS6_1
+#undef SVDQ_FRAGS6_2
+
+  // Stage 0 landed everywhere; stage s + 1 goes out during stage s.
+#pragma unroll
+  for (int d = 0; d < NDMA; ++d) dma(0, 0, d);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  read_half(0, 0, 0, 0, 0);
+  for (int s = 0; s < nstages; ++s) {
+    const bool more = s + 1 < nstages;
+    const int buf = s & 1, nbuf = buf ^ 1;
+#pragma unroll
+    for (int hh = 0; hh < HPS; ++hh) {
+      const int hg = s * HPS + hh;            // half-group index
+      if (hh > 0 && hg >= H) break;           // the last stage holds fewer groups
+      const int i = hh & 1, gi = hh >> 1;
+      const int ai = RM ? i : 0, bi = RM ? (gi & 1) : 0;
+      const bool last = hh == HPS - 1;
+      // This step's fragments in place and the previous step's rescale issued before the next
+      // reads go out (keeps one register set live per step).
+      asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(faq[ai][0]),
+                   "+v"(fap[ai][KS - 1]), "+v"(fbq[bi][0][0]), "+v"(fbp[bi][0][KS - 1]), "+v"(fbq[bi][1][0]),
+                   "+v"(fbp[bi][1][KS - 1]), "+v"(xop[i]), "+v"(wop_[bi][0]), "+v"(wop_[bi][1])::"memory");
+      if (RM) {
+        if (last) {
+          if (more) {
+            // stage s + 1 landed everywhere and every wave's reads of stage s are complete
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            frag_fence();
+            asm volatile("s_barrier" ::: "memory");
+            read_half(nbuf, 0, 0, 0, 0);
+          }
+        } else if (hg + 1 < H) {
+          read_half(buf, (hh + 1) >> 1, (hh + 1) & 1, (hh + 1) & 1, ((hh + 1) >> 1) & 1);
+        }
+      }
+      f32x16 P[2], S[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        P[j] = mfma_p6(ai, bi, j);
+        S[j] = mfma_bf16_32x32x16(xop[i], wop_[bi][j], f32x16{});
+      }
+      // stage s + 1 -> buffer nbuf, last read in stage s - 1 (before the barrier that ended it)
+      if (more && hh < NPART) {
+#pragma unroll
+        for (int d = hh * PER; d < (hh + 1) * PER; ++d)
+          if (d < NDMA) dma(s + 1, nbuf, d);
+      }
+      if (!RM) {
+        if (!last) {
+          if (hg + 1 < H) read_half(buf, (hh + 1) >> 1, (hh + 1) & 1, 0, 0);
+        } else if (more) {
+          // the step's MFMAs issued (their operands are overwritten next), stage s + 1 landed
+          asm volatile("" : "+v"(P[0]), "+v"(P[1]), "+v"(S[0]), "+v"(S[1])::"memory");
+          asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+          read_half(nbuf, 0, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(P[j][r], S[j][r], acc[i][j][r]);
+    }
+  }
+  // No DMA is in flight (none goes out in the last stage); once every wave is past its last
+  // reads, the A planes hold the output staging regions.
+  __syncthreads();
+  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[0][0] + wave * 8192);
+}
+
 // Weight operand of the W4A4 GEMM, once per layer: each packed dword (8 nibbles, k0 in the
 // low nibble) becomes 8 operand bytes [k0 k2 k4 k6 k1 k3 k5 k7].
 __global__ void weight_operand_kernel(const uint32_t* __restrict__ qw, u32x2* __restrict__ out, long n, int mode) {
@@ -441,6 +662,33 @@ __global__ void weight_operand_kernel(const uint32_t* __restrict__ qw, u32x2* __
     if (mode == 0) nib8_to_e4m3(qw[i], lo, hi);
     else nib8_to_i8x16(qw[i], lo, hi);
     out[i] = u32x2{lo, hi};
+  }
+}
+
+// e3m2 (FP6) weight operand, once per layer: thread per (row n, k-step t, half h) turns 32 packed
+// codes into their 6-dword field vector (codes_to_e3m2: field f <- k = 64 t + 32 h + f) and writes
+// it to the planar layout of the activation pass's e3m2 operand, rows padded to Np (even).
+__global__ void weight_operand_e3m2_kernel(const uint8_t* __restrict__ qw, uint8_t* __restrict__ out, int N, int Np,
+                                           int K) {
+  const int kt_n = K / 64;
+  const long total = (long)N * kt_n * 2;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
+    const int n = (int)(idx % N);
+    const long plane = idx / N;                       // t * 2 + h
+    const u32x4 w = *reinterpret_cast<const u32x4*>(qw + (long)n * (K / 2) + plane * 16);
+    f32x16 x, y;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t byte = (w[d] >> (8 * e)) & 0xFFu;   // k = 2 (4 d + e) low nibble, + 1 high
+        x[4 * d + e] = (float)((int)(byte & 15u) - 8);
+        y[4 * d + e] = (float)((int)(byte >> 4) - 8);
+      }
+    const u32x6 f = codes_to_e3m2(x, y);
+    const long row = plane * Np + n;
+    *reinterpret_cast<u32x4*>(out + row * 16) = u32x4{f[0], f[1], f[2], f[3]};
+    *reinterpret_cast<u32x2*>(out + (long)kt_n * 2 * Np * 16 + row * 8) = u32x2{f[4], f[5]};
   }
 }
 
@@ -573,16 +821,36 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
   SVDQ_W4A4(64, 1)
   SVDQ_W4A4(128, 1)
 #undef SVDQ_W4A4
+  if (mode == 2) {
+    if (G == 64) {
+      if (out_f32) w4a4_e3m2_kernel<64, true><<<grid, 512, 0, st>>>(p);
+      else w4a4_e3m2_kernel<64, false><<<grid, 512, 0, st>>>(p);
+      return hipGetLastError();
+    }
+    if (G == 128) {
+      if (out_f32) w4a4_e3m2_kernel<128, true><<<grid, 512, 0, st>>>(p);
+      else w4a4_e3m2_kernel<128, false><<<grid, 512, 0, st>>>(p);
+      return hipGetLastError();
+    }
+  }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, int n, int ngroups, int mode, hipStream_t st) {
   const long blocks = std::min<long>(((long)n * ngroups + 255) / 256, 8192);
-  weight_scale_pairs_kernel<<<(unsigned)blocks, 256, 0, st>>>(sw, out, n, ngroups, mode == 0 ? 1.0f : 1.0f / 256.0f);
+  // int8 operands are 16 q on both sides: 1/256 folded into the weight scale
+  weight_scale_pairs_kernel<<<(unsigned)blocks, 256, 0, st>>>(sw, out, n, ngroups, mode == 1 ? 1.0f / 256.0f : 1.0f);
   return hipGetLastError();
 }
 
-hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, long ndwords, int mode, hipStream_t st) {
+hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, int mode, hipStream_t st) {
+  if (mode == 2) {
+    const long total = (long)N * (K / 64) * 2;
+    const long blocks = std::min<long>((total + 255) / 256, 8192);
+    weight_operand_e3m2_kernel<<<(unsigned)blocks, 256, 0, st>>>(qw, qwe, N, (N + 1) & ~1, K);
+    return hipGetLastError();
+  }
+  const long ndwords = (long)N * (K / 8);
   const long blocks = std::min<long>((ndwords + 255) / 256, 8192);
   weight_operand_kernel<<<(unsigned)blocks, 256, 0, st>>>(reinterpret_cast<const uint32_t*>(qw),
                                                           reinterpret_cast<u32x2*>(qwe), ndwords, mode);

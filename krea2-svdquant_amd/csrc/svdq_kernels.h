@@ -50,10 +50,13 @@ hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, in
 // operand midp [M, 2, RTp] (bf16 hi plane, then bf16 lo plane, hi + lo within 2^-18 of the f32 sum, relative).
 hipError_t launch_mid_finalize(const float* part, int S, int M, int RTp, uint16_t* midp, hipStream_t st);
 hipError_t launch_prepare_smooth(const uint16_t* s, float* srs, int K, hipStream_t st);
-// mode: 0 = e4m3 operands on the FP8 MFMA, 1 = int8 operands on the INT8 MFMA
+// mode: 0 = e4m3 operands on the FP8 MFMA, 1 = int8 operands on the INT8 MFMA, 2 = e3m2 planar
+// operands on the FP6 MFMA
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st);
 hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, int n, int ngroups, int mode, hipStream_t st);
-hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, long ndwords, int mode, hipStream_t st);
+// mode: 0 = e4m3, 1 = int8 16*q (both [N, K] bytes), 2 = e3m2 planar ((N + 1) & ~1 rows, K * 3 / 4
+// bytes per row)
+hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, int mode, hipStream_t st);
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st);
 
 }  // namespace svdq

@@ -39,7 +39,7 @@ class PreparedLayer:
     qweight: Tensor              # uint8 [N, Kp/2]
     weight_scales: Tensor        # fp16 [N, Kp/G]
     scale_pairs: dict            # operand code -> int32 [Kp/G, N] W4A4 scale-MFMA operand (lazy)
-    operands: dict               # operand code -> uint8 [N, Kp] W4A4 weight operand codes (lazy)
+    operands: dict               # operand code -> W4A4 weight operand (uint8 [N, Kp], e3m2 planar) (lazy)
     bias: Optional[Tensor]       # bf16 [N]
     group_size: int
     n: int
@@ -144,8 +144,8 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
                      exact_div: bool = False, operand: str = "e4m3") -> Tensor:
     """One SVDQuantLinear forward on prepared operands; returns [..., N].
 
-    ``operand`` picks the W4A4 MFMA: ``"e4m3"`` (FP8 MFMA, default) or ``"i8"`` (INT8 MFMA);
-    both compute the same exact integer group sums.
+    ``operand`` picks the W4A4 MFMA: ``"e4m3"`` (FP8 MFMA, default), ``"e3m2"`` (FP6 MFMA, twice
+    the FP8 rate) or ``"i8"`` (INT8 MFMA); all compute the same exact integer group sums.
     """
     if not x.is_cuda:
         raise RuntimeError("HIP gfx950 backend needs a GPU tensor")
@@ -161,7 +161,7 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
         x2 = _pad_cols(x2, prep.kp)
     if mode == "w4a4":
         if operand not in ops.OPERAND_NAMES:
-            raise ValueError(f"operand must be 'e4m3' or 'i8', got {operand!r}")
+            raise ValueError(f"operand must be 'e4m3', 'e3m2' or 'i8', got {operand!r}")
         opc = ops.OPERAND_NAMES[operand]
         qa, sx, _, _, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
                                           prep.group_size, prep.rtp, opc, False, False, exact_div, True)

@@ -22,6 +22,7 @@ SVDQ_ACT_EXACT_DIV = 4
 SVDQ_ACT_OPERAND_E4M3 = 8
 SVDQ_ACT_OPERAND_I8 = 16
 SVDQ_ACT_SX_PAIRS = 32
+SVDQ_ACT_OPERAND_E3M2 = 64
 
 STATUS = {0: "SVDQ_OK", -1: "SVDQ_ERR_ARG", -2: "SVDQ_ERR_SHAPE", -3: "SVDQ_ERR_ALIGN",
           -4: "SVDQ_ERR_UNSUPPORTED", -5: "SVDQ_ERR_LAUNCH"}

@@ -54,7 +54,18 @@ def _(smooth):
     return smooth.new_empty(2 * smooth.numel(), dtype=torch.float32)
 
 
-OPERAND_NONE, OPERAND_E4M3, OPERAND_I8 = -1, 0, 1
+OPERAND_NONE, OPERAND_E4M3, OPERAND_I8, OPERAND_E3M2 = -1, 0, 1, 2
+_OPERANDS = (OPERAND_E4M3, OPERAND_I8, OPERAND_E3M2)
+
+
+def operand_bytes(rows: int, k: int, operand: int) -> int:
+    """Bytes of an [rows, K] W4A4 operand in format ``operand``: one per code for e4m3 / int8; the
+    planar e3m2 layout holds 6 bits per code with rows padded to an even count."""
+    return ((rows + 1) & ~1) * k * 3 // 4 if operand == OPERAND_E3M2 else rows * k
+
+
+def _operand_shape(rows: int, k: int, operand: int) -> tuple:
+    return (operand_bytes(rows, k, operand),) if operand == OPERAND_E3M2 else (rows, k)
 
 
 @torch.library.custom_op("svdq::prepare_weight_scales", mutates_args=())
@@ -64,7 +75,7 @@ def prepare_weight_scales(weight_scales: Tensor, operand: int) -> Tensor:
     _need(weight_scales.is_cuda, RuntimeError, "svdq::prepare_weight_scales needs a GPU tensor")
     _check_dev("weight_scales", weight_scales, weight_scales.device, torch.float16)
     _need(weight_scales.dim() == 2, ValueError, f"weight_scales must be [N, K/G], got {tuple(weight_scales.shape)}")
-    _need(operand in (OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
+    _need(operand in _OPERANDS, ValueError, f"operand={operand}")
     n, ng = weight_scales.shape
     out = torch.empty((ng, n), dtype=torch.int32, device=weight_scales.device)
     lib.call("svdq_prepare_weight_scales", _vp(weight_scales), _vp(out), n, ng, operand, _stream(weight_scales.device))
@@ -78,22 +89,26 @@ def _(weight_scales, operand):
 
 @torch.library.custom_op("svdq::prepare_weight_operand", mutates_args=())
 def prepare_weight_operand(qweight: Tensor, operand: int) -> Tensor:
-    """[N, K] uint8 W4A4 weight operand: the packed INT4 codes [N, K/2] expanded to one MFMA
-    operand code per weight (same byte order and format as ``act_quant``'s ``qa``), per layer."""
+    """W4A4 weight operand, per layer: the packed INT4 codes [N, K/2] as MFMA operand codes in the
+    layout and format of ``act_quant``'s ``qa``: uint8 [N, K] for e4m3 / int8, the flat planar
+    e3m2 bytes (``operand_bytes(N, K, OPERAND_E3M2)``) for e3m2."""
     _need(qweight.is_cuda, RuntimeError, "svdq::prepare_weight_operand needs a GPU tensor")
     _check_dev("qweight", qweight, qweight.device, torch.uint8)
     _need(qweight.dim() == 2, ValueError, f"qweight must be [N, K/2], got {tuple(qweight.shape)}")
-    _need(operand in (OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
+    _need(operand in _OPERANDS, ValueError, f"operand={operand}")
     n, k = qweight.shape[0], qweight.shape[1] * 2
-    out = torch.empty((n, k), dtype=torch.uint8, device=qweight.device)
+    out = torch.empty(_operand_shape(n, k, operand), dtype=torch.uint8, device=qweight.device)
     lib.call("svdq_prepare_weight_operand", _vp(qweight), _vp(out), n, k, operand, _stream(qweight.device))
     return out
 
 
 @prepare_weight_operand.register_fake
 def _(qweight, operand):
-    return qweight.new_empty((qweight.shape[0], qweight.shape[1] * 2), dtype=torch.uint8)
-OPERAND_NAMES = {"e4m3": OPERAND_E4M3, "fp8": OPERAND_E4M3, "i8": OPERAND_I8, "int8": OPERAND_I8}
+    return qweight.new_empty(_operand_shape(qweight.shape[0], qweight.shape[1] * 2, operand), dtype=torch.uint8)
+
+
+OPERAND_NAMES = {"e4m3": OPERAND_E4M3, "fp8": OPERAND_E4M3, "i8": OPERAND_I8, "int8": OPERAND_I8,
+                 "e3m2": OPERAND_E3M2, "fp6": OPERAND_E3M2}
 
 
 @torch.library.custom_op("svdq::act_quant", mutates_args=())
@@ -102,8 +117,9 @@ def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
               want_xhat: bool, exact: bool, sx_pairs: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Smoothing + A4 quantization + low-rank / LoRA down projections, one pass over x.
 
-    ``operand`` selects the W4A4 GEMM operand codes written (``OPERAND_E4M3`` / ``OPERAND_I8``)
-    or none (``OPERAND_NONE``: x_hat only, the W4A16 path).  Returns
+    ``operand`` selects the W4A4 GEMM operand codes written (``OPERAND_E4M3`` / ``OPERAND_I8`` /
+    ``OPERAND_E3M2``, the last in the flat planar layout) or none (``OPERAND_NONE``: x_hat only,
+    the W4A16 path).  Returns
     ``(qa uint8 [M, K], sx bf16 [M, K/G], qx uint8 [M, K/2], xhat bf16 [M, K], mid f32 [S + 1, M, rtp])``
     where ``mid`` is the pass's workspace: ``mid[0]`` holds the GEMM epilogue operand (bf16 hi and
     lo planes per row, see ``mid_values``), ``mid[1:]`` one partial per K split; outputs not
@@ -130,12 +146,12 @@ def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
         _need(lora_mult is not None and lora_mult.numel() == rl, ValueError, "lora_mult must have rl entries")
         _check_dev("lora_mult", lora_mult, dev, torch.float32)
     _need(k % group_size == 0, ValueError, f"K={k} must be a multiple of group_size={group_size}")
-    _need(operand in (OPERAND_NONE, OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
+    _need(operand == OPERAND_NONE or operand in _OPERANDS, ValueError, f"operand={operand}")
     quant = operand != OPERAND_NONE
     _need(quant or not sx_pairs, ValueError, "sx_pairs needs an operand format")
 
     splits = _splits(m, k, group_size, rtp)
-    qa = torch.empty((m, k) if quant else (0,), dtype=torch.uint8, device=dev)
+    qa = torch.empty(_operand_shape(m, k, operand) if quant else (0,), dtype=torch.uint8, device=dev)
     sx_shape = ((k // group_size, m) if sx_pairs else (m, k // group_size)) if quant else (0,)
     sx = torch.empty(sx_shape, dtype=torch.int32 if sx_pairs else torch.bfloat16, device=dev)
     qx = torch.empty((m, k // 2) if packed else (0,), dtype=torch.uint8, device=dev)
@@ -143,6 +159,7 @@ def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
     mid = torch.empty((splits + 1, m, rtp), dtype=torch.float32, device=dev)
     flags = ((lib.SVDQ_ACT_OPERAND_E4M3 if operand == OPERAND_E4M3 else 0)
              | (lib.SVDQ_ACT_OPERAND_I8 if operand == OPERAND_I8 else 0)
+             | (lib.SVDQ_ACT_OPERAND_E3M2 if operand == OPERAND_E3M2 else 0)
              | (lib.SVDQ_ACT_PACKED if packed else 0) | (lib.SVDQ_ACT_XHAT if want_xhat else 0)
              | (lib.SVDQ_ACT_EXACT_DIV if exact else 0) | (lib.SVDQ_ACT_SX_PAIRS if sx_pairs else 0))
     lib.call("svdq_act_quant", _vp(x), k, _vp(srs), _vp(l2), r, _vp(lora_down), rl, _vp(lora_mult),
@@ -156,7 +173,7 @@ def act_quant(x: Tensor, srs: Tensor, l2: Tensor, lora_down: Optional[Tensor],
 def _(x, srs, l2, lora_down, lora_mult, group_size, rtp, operand, packed, want_xhat, exact, sx_pairs=False):
     m, k = x.shape
     quant = operand != OPERAND_NONE
-    qa = x.new_empty((m, k) if quant else (0,), dtype=torch.uint8)
+    qa = x.new_empty(_operand_shape(m, k, operand) if quant else (0,), dtype=torch.uint8)
     sx_shape = ((k // group_size, m) if sx_pairs else (m, k // group_size)) if quant else (0,)
     sx = x.new_empty(sx_shape, dtype=torch.int32 if sx_pairs else torch.bfloat16)
     qx = x.new_empty((m, k // 2) if packed else (0,), dtype=torch.uint8)
@@ -232,17 +249,19 @@ def w4a4_gemm(qa: Tensor, sx_pairs: Tensor, weight_operand: Tensor, weight_scale
     _need(qa.is_cuda, RuntimeError, "svdq::w4a4_gemm needs GPU tensors")
     dev = qa.device
     _check_dev("qa", qa, dev, torch.uint8)
-    m, k = qa.shape
     _check_dev("sx_pairs", sx_pairs, dev, torch.int32)
-    _need(tuple(sx_pairs.shape) == (k // group_size, m), ValueError, "sx_pairs must be [K/G, M]")
-    _need(operand in (OPERAND_E4M3, OPERAND_I8), ValueError, f"operand={operand}")
+    _need(sx_pairs.dim() == 2, ValueError, "sx_pairs must be [K/G, M]")
+    _need(operand in _OPERANDS, ValueError, f"operand={operand}")
+    m, k = sx_pairs.shape[1], sx_pairs.shape[0] * group_size
+    _need(tuple(qa.shape) == _operand_shape(m, k, operand), ValueError,
+          f"qa must be {_operand_shape(m, k, operand)} for M={m}, K={k}, got {tuple(qa.shape)}")
     _check_dev("weight_operand", weight_operand, dev, torch.uint8)
-    _need(weight_operand.dim() == 2 and weight_operand.shape[1] == k, ValueError,
-          f"weight_operand must be [N, {k}], got {tuple(weight_operand.shape)}")
     _check_dev("weight_scale_pairs", weight_scale_pairs, dev, torch.int32)
-    n = weight_operand.shape[0]
-    _need(tuple(weight_scale_pairs.shape) == (k // group_size, n), ValueError,
-          f"weight_scale_pairs must be [{k // group_size}, {n}], got {tuple(weight_scale_pairs.shape)}")
+    _need(weight_scale_pairs.dim() == 2 and weight_scale_pairs.shape[0] == k // group_size, ValueError,
+          f"weight_scale_pairs must be [{k // group_size}, N], got {tuple(weight_scale_pairs.shape)}")
+    n = weight_scale_pairs.shape[1]
+    _need(tuple(weight_operand.shape) == _operand_shape(n, k, operand), ValueError,
+          f"weight_operand must be {_operand_shape(n, k, operand)}, got {tuple(weight_operand.shape)}")
     _check_epilogue(mid, l1cat, bias, m, n, dev)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
     lib.call("svdq_w4a4_gemm", _vp(qa), operand, _vp(sx_pairs), _vp(weight_operand), _vp(weight_scale_pairs), _vp(mid),
@@ -252,7 +271,8 @@ def w4a4_gemm(qa: Tensor, sx_pairs: Tensor, weight_operand: Tensor, weight_scale
 
 @w4a4_gemm.register_fake
 def _(qa, sx_pairs, weight_operand, weight_scale_pairs, mid, l1cat, bias, group_size, operand, out_f32):
-    return qa.new_empty((qa.shape[0], weight_operand.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)
+    return qa.new_empty((sx_pairs.shape[1], weight_scale_pairs.shape[1]),
+                        dtype=torch.float32 if out_f32 else torch.bfloat16)
 
 
 @torch.library.custom_op("svdq::w4a16_gemm", mutates_args=())

@@ -67,3 +67,50 @@ def operand_bytes(q: np.ndarray, fmt: str) -> np.ndarray:
 
 def rel_l2(a, b) -> float:
     return sim.rel_l2(a, b)
+
+
+def e3m2_code(q: np.ndarray) -> np.ndarray:
+    """6-bit e3m2 (OCP FP6 "bf6": sign, 3 exponent bits with bias 3, 2 mantissa bits) codes of
+    integers q in [-8, 7], from the format definition: |q| = 2^e (1 + m/4), code = s<<5 | (e+3)<<2 | m."""
+    q = np.asarray(q, np.int64)
+    a = np.abs(q)
+    e = np.floor(np.log2(np.maximum(a, 1))).astype(np.int64)
+    m = np.rint((a / 2.0 ** e - 1.0) * 4).astype(np.int64)
+    mag = np.where(a == 0, 0, ((e + 3) << 2) | m)
+    return (mag | ((q < 0).astype(np.int64) << 5)).astype(np.uint8)
+
+
+def e3m2_value(code: np.ndarray) -> np.ndarray:
+    """Decode 6-bit e3m2 codes (normal: 2^(E-3) (1 + M/4); subnormal E = 0: 2^-2 M/4)."""
+    c = np.asarray(code, np.int64)
+    s, ex, mt = (c >> 5) & 1, (c >> 2) & 7, c & 3
+    v = np.where(ex == 0, mt / 4.0 * 2.0 ** -2, (1 + mt / 4.0) * 2.0 ** (ex - 3))
+    return np.where(s == 1, -v, v)
+
+
+def e3m2_planar(q: np.ndarray) -> np.ndarray:
+    """Flat planar e3m2 operand bytes of int codes q [R, K] (the layout of svdq_act_quant's e3m2
+    qa): per k-step t and half h the 32 codes of a row are contiguous little-endian 6-bit fields
+    (field f = column 64 t + 32 h + f) in 24 bytes, bytes 0-15 in plane Q[t][h][Rp][16], bytes
+    16-23 in plane P[t][h][Rp][8] after all Q planes; Rp = R rounded up to even, padding zero."""
+    r, k = q.shape
+    rp, t = (r + 1) & ~1, k // 64
+    c = e3m2_code(q).astype(np.uint8).reshape(r, t, 2, 32)
+    bits = np.zeros((r, t, 2, 192), np.uint8)
+    for b in range(6):
+        bits[..., np.arange(32) * 6 + b] = (c >> b) & 1
+    v24 = np.packbits(bits.reshape(r, t, 2, 24, 8), axis=-1, bitorder="little").reshape(r, t, 2, 24)
+    qp = np.zeros((t, 2, rp, 16), np.uint8)
+    pp = np.zeros((t, 2, rp, 8), np.uint8)
+    qp[:, :, :r] = v24[..., :16].transpose(1, 2, 0, 3)
+    pp[:, :, :r] = v24[..., 16:].transpose(1, 2, 0, 3)
+    return np.concatenate([qp.ravel(), pp.ravel()])
+
+
+def e3m2_rows(buf: np.ndarray, r: int, k: int) -> np.ndarray:
+    """The written rows of a flat planar e3m2 operand as [K/64, 2, R, 24] (padding rows dropped)."""
+    rp, t = (r + 1) & ~1, k // 64
+    buf = np.asarray(buf, np.uint8).ravel()
+    qp = buf[:t * 2 * rp * 16].reshape(t, 2, rp, 16)[:, :, :r]
+    pp = buf[t * 2 * rp * 16:].reshape(t, 2, rp, 8)[:, :, :r]
+    return np.concatenate([qp, pp], axis=-1)

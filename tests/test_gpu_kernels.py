@@ -15,8 +15,8 @@ import torch
 from oracle import numerics as nm
 from oracle import pack as op
 from oracle import sim, synth
-from tests.gpu_util import (bf16_bits_of, bf16_tensor, device_adapters, operand_bytes, rel_l2,
-                            to_device_state)
+from tests.gpu_util import (bf16_bits_of, bf16_tensor, device_adapters, e3m2_planar, e3m2_rows, operand_bytes,
+                            rel_l2, to_device_state)
 from tests.golden_io import load_layer_fixture
 
 pytestmark = pytest.mark.gpu
@@ -54,8 +54,8 @@ def test_w4a4_gemm_layout_identity(dev):
     mid = torch.zeros((1, m, 32), dtype=torch.float32, device=dev)
     l1 = torch.zeros((n, 32), dtype=torch.bfloat16, device=dev)
     expect = qw[:, :m].T.astype(np.float32)
-    for fmt in ("e4m3", "i8"):
-        qa = torch.from_numpy(operand_bytes(q, fmt)).to(dev)
+    for fmt in ("e4m3", "i8", "e3m2"):
+        qa = torch.from_numpy(e3m2_planar(q) if fmt == "e3m2" else operand_bytes(q, fmt)).to(dev)
         opc = ops.OPERAND_NAMES[fmt]
         y = ops.w4a4_gemm(qa, sx, ops.prepare_weight_operand(qwt, opc), ops.prepare_weight_scales(sw, opc), mid, l1,
                           None, 64, opc, True).cpu().numpy()
@@ -65,14 +65,20 @@ def test_w4a4_gemm_layout_identity(dev):
             pytest.fail(f"{fmt}: {len(bad)} mismatches, first {bad[:4].tolist()}; row matches {rows}")
 
 
-@pytest.mark.parametrize("fmt", ["e4m3", "i8"])
-def test_weight_operand_matches_unpacked_codes(dev, fmt):
+@pytest.mark.parametrize("fmt", ["e4m3", "i8", "e3m2"])
+@pytest.mark.parametrize("n", [300, 301])
+def test_weight_operand_matches_unpacked_codes(dev, fmt, n):
     """The per-layer expanded weight operand holds exactly the oracle's unpacked codes."""
     _, ops = _ops()
     rng = np.random.default_rng(5)
-    packed = rng.integers(0, 256, size=(300, 448), dtype=np.uint8)   # every nibble value, K = 896
+    packed = rng.integers(0, 256, size=(n, 448), dtype=np.uint8)   # every nibble value, K = 896
     out = ops.prepare_weight_operand(torch.from_numpy(packed).to(dev), ops.OPERAND_NAMES[fmt]).cpu().numpy()
-    assert np.array_equal(out, operand_bytes(op.unpack_int4(packed), fmt))
+    codes = op.unpack_int4(packed)
+    if fmt == "e3m2":
+        assert out.size == ((n + 1) & ~1) * 896 * 3 // 4
+        assert np.array_equal(e3m2_rows(out, n, 896), e3m2_rows(e3m2_planar(codes), n, 896))
+    else:
+        assert np.array_equal(out, operand_bytes(codes, fmt))
 
 
 @pytest.mark.parametrize("name", ["w4a4_small_g64.npz", "w4a4_small_g128.npz"])
@@ -89,6 +95,10 @@ def test_act_quant_golden_bit_exact(dev, name):
     assert np.array_equal(sxp.cpu().numpy().view(np.uint32), (bits | (bits << 16)).T)
     (qa8, sx8, qx8, _, _), _ = _run_act(x, st, dev, operand="i8", packed=True)
     assert np.array_equal(qa8.cpu().numpy(), operand_bytes(codes, "i8"))
+    (qa6, sx6, _, _, _), _ = _run_act(x, st, dev, operand="e3m2", packed=False, sx_pairs=True)
+    m, k = codes.shape
+    assert np.array_equal(e3m2_rows(qa6.cpu().numpy(), m, k), e3m2_rows(e3m2_planar(codes), m, k))
+    assert np.array_equal(sx6.cpu().numpy().view(np.uint32), (bits | (bits << 16)).T)
     assert np.array_equal(qx8.cpu().numpy(), fx["qx_packed"]) and np.array_equal(bf16_bits_of(sx8), fx["sx"])
     (_, _, _, xh16, _), _ = _run_act(x, st, dev, operand=None, packed=False, xhat=True)
     assert np.array_equal(bf16_bits_of(xh16), fx["xhat"])
@@ -160,7 +170,7 @@ def _layer_outputs(x_np, st, dev, mode, out_f32, operand="e4m3"):
 
 
 def _check_layer(x, st, dev, mode, ref):
-    for operand in (("e4m3", "i8") if mode == "w4a4" else ("e4m3",)):
+    for operand in (("e4m3", "i8", "e3m2") if mode == "w4a4" else ("e4m3",)):
         y32 = _layer_outputs(x, st, dev, mode, True, operand)
         e32 = rel_l2(y32, ref)
         y16 = _layer_outputs(x, st, dev, mode, False, operand)
