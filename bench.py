@@ -8,8 +8,10 @@ on the GPU by the package converter (smoothing, rank-32 SVD, INT4 residual), ran
 A step is one full layer forward (activation pass + W4A4 GEMM with the low-rank epilogue)
 with its inputs resident in HBM.  ``value`` = effective TOPS = 2*M*N*K / step time.
 
-``roofline`` prices the dominant kernel, the W4A4 GEMM, against the MI355X dense FP8 / INT8
-MFMA peak (5.0 P(FL)OP/s; the GEMM runs exact INT4 codes on the FP8 MFMA).  Its average launch
+``roofline`` prices the dominant kernel, the W4A4 GEMM, against the MI355X dense peak of the
+MFMA it issues: the FP6 MFMA (10.1 PFLOP/s; every INT4 code is an exact e3m2 value) by default,
+the FP8 one (5.0) with ``--operand e4m3``; ``int8_dense_peak_frac`` restates the achieved rate
+against the dense INT8 peak (5.0 POP/s) the BASELINE north star names.  Its average launch
 duration is measured here with HIP events on the stream the kernel is launched on (torch's
 current stream, which the custom ops use).  ``traffic`` (HBM bytes per launch) comes from the
 rocprofv3 FETCH_SIZE / WRITE_SIZE passes committed in profiles/w4a4_gemm_ffup_traffic.md
@@ -38,8 +40,13 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "W4A4 SVDQuantLinear eff. TOPS @M4096 K6144 N16384; ms/denoise step @1024px"
-MFMA_PEAK_TFLOPS = 5000.0   # MI355X dense FP8 / INT8 MFMA
+MFMA_PEAK_TFLOPS = {"e3m2": 10100.0, "e4m3": 5000.0, "i8": 5000.0}   # MI355X dense MFMA peaks
+INT8_PEAK_TOPS = 5000.0
 HBM_PEAK_GBS = 8000.0
+MFMA_NAME = {"e3m2": "FP6", "e4m3": "FP8", "i8": "INT8"}
+KERNEL_NAME = {"e3m2": "w4a4_e3m2_kernel<64,false> (FP6 MFMA on exact INT4 codes)",
+               "e4m3": "w4a4_kernel<64,0,false> (FP8 MFMA on exact INT4 codes)",
+               "i8": "w4a4_kernel<64,1,false> (INT8 MFMA on 16*q)"}
 TRAFFIC_SUMMARY = ROOT / "profiles" / "w4a4_gemm_ffup_traffic.md"
 # (name, N, K) of the 8 quantized linears of one Krea-2 block
 BLOCK_SHAPES = [("to_q", 6144, 6144), ("to_gate", 6144, 6144), ("to_k", 1536, 6144), ("to_v", 1536, 6144),
@@ -57,6 +64,8 @@ def parse():
     ap.add_argument("--n", type=int, default=16384)
     ap.add_argument("--rank", type=int, default=32)
     ap.add_argument("--group", type=int, default=64)
+    ap.add_argument("--operand", default="e3m2", choices=["e3m2", "e4m3", "i8"],
+                    help="W4A4 MFMA operand format (e3m2 = FP6 MFMA, the default path)")
     ap.add_argument("--cpu-reps", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-block", action="store_true", help="skip the config 1/2/4 extra lines")
@@ -225,7 +234,7 @@ def main() -> int:
     m, k, n, r, g = args.m, args.k, args.n, args.rank, args.group
     log(f"device {torch.cuda.get_device_name(dev)}; building state M={m} K={k} N={n} r={r} g={g}")
     x, ds, prep = make_layer(n, k, m, r, g, dev, seed=1)
-    opc = ops.OPERAND_E4M3
+    opc = ops.OPERAND_NAMES[args.operand]
     wop, wsp = prep.weight_operand(opc), prep.weight_scale_pairs(opc)
     qa, sx, _, _, mid = ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False, True)
     torch.cuda.synchronize()
@@ -246,7 +255,7 @@ def main() -> int:
         return 0
 
     def step():
-        return backend.forward_prepared(x, prep, mode="w4a4")
+        return backend.forward_prepared(x, prep, mode="w4a4", operand=args.operand)
 
     log(f"warmup {args.warmup}")
     for _ in range(args.warmup):
@@ -277,8 +286,8 @@ def main() -> int:
     splits = mid.shape[0] - 1
     # x, srs, l2 read; codes, scales, split partials written; partials re-read and the final
     # hi / lo operand written by the finalize kernel
-    act_bytes = (2 * m * k + 8 * k + 2 * r * k + m * k + 4 * m * (k // g) + 2 * 4 * m * prep.rtp * splits
-                 + 4 * m * prep.rtp)
+    act_bytes = (2 * m * k + 8 * k + 2 * r * k + ops.operand_bytes(m, k, opc) + 4 * m * (k // g)
+                 + 2 * 4 * m * prep.rtp * splits + 4 * m * prep.rtp)
     gemm_tflops = flops / (ms_gemm * 1e-3) / 1e12
     traffic = read_traffic()
     result = {
@@ -292,19 +301,21 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "e4m3",
+        "dtype": args.operand,
         "data": "synthetic (X ~ N(0,1) with 1% x20 outlier channels; random-init W ~ N(0,0.02) quantized on device)",
         "config": {"workload": "config1 ff.up: W4A4 SVDQuantLinear forward (fused smooth + A4 quant + low-rank "
-                               "down; exact INT4-code GEMM on the FP8 MFMA + low-rank up epilogue, bf16 out)",
-                   "M": m, "K": k, "N": n, "rank": r, "group": g},
+                               f"down; exact INT4-code GEMM on the {MFMA_NAME[args.operand]} MFMA + low-rank up "
+                               "epilogue, bf16 out)",
+                   "M": m, "K": k, "N": n, "rank": r, "group": g, "operand": args.operand},
         "kernels": {"act_quant_ms": round(ms_act, 4), "w4a4_gemm_ms": round(ms_gemm, 4),
                     "act_quant_GBps": round(act_bytes / (ms_act * 1e-3) / 1e9, 1),
                     "act_quant_hbm_frac": round(act_bytes / (ms_act * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "step_host_wall_ms": round(wall, 4)},
-        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(gemm_tflops / MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "w4a4_kernel<64,0,false> (FP8 MFMA on exact INT4 codes)",
-                     "algorithmic_ops_per_launch": flops},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": MFMA_PEAK_TFLOPS[args.operand],
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / MFMA_PEAK_TFLOPS[args.operand], 4),
+                     "traffic": traffic if args.operand == "e3m2" else None,
+                     "kernel": KERNEL_NAME[args.operand], "algorithmic_ops_per_launch": flops,
+                     "int8_dense_peak_frac": round(gemm_tflops / INT8_PEAK_TOPS, 4)},
     }
     if not args.no_block:
         log("block line: 8 linears of config 1")

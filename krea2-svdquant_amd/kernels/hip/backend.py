@@ -141,11 +141,11 @@ def _flatten(x: Tensor) -> tuple[Tensor, tuple[int, ...]]:
 
 
 def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_f32: bool = False,
-                     exact_div: bool = False, operand: str = "e4m3") -> Tensor:
+                     exact_div: bool = False, operand: str = "e3m2") -> Tensor:
     """One SVDQuantLinear forward on prepared operands; returns [..., N].
 
-    ``operand`` picks the W4A4 MFMA: ``"e4m3"`` (FP8 MFMA, default), ``"e3m2"`` (FP6 MFMA, twice
-    the FP8 rate) or ``"i8"`` (INT8 MFMA); all compute the same exact integer group sums.
+    ``operand`` picks the W4A4 MFMA: ``"e3m2"`` (FP6 MFMA, default: twice the FP8 rate),
+    ``"e4m3"`` (FP8 MFMA) or ``"i8"`` (INT8 MFMA); all compute the same exact integer group sums.
     """
     if not x.is_cuda:
         raise RuntimeError("HIP gfx950 backend needs a GPU tensor")
@@ -179,7 +179,7 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
 
 
 def svdquant_linear_hip_gfx950(x: Tensor, state: SVDQuantLinearState, *, adapters: Sequence = (),
-                               mode: str = "w4a4", out_f32: bool = False, operand: str = "e4m3") -> Tensor:
+                               mode: str = "w4a4", out_f32: bool = False, operand: str = "e3m2") -> Tensor:
     """Stateless backend entry (prepares the layer on every call; modules cache it)."""
     return forward_prepared(x, prepare_layer(state, adapters, x.device), mode=mode, out_f32=out_f32,
                             operand=operand)
