@@ -147,10 +147,7 @@ __device__ __forceinline__ void split_hi_lo(const float* v, u32x4& hi, u32x4& lo
 // XCD-aware block order: hardware hands consecutive workgroup ids to the 8 XCDs round-robin;
 // remap so that each XCD receives a contiguous range of output tiles (shared A rows / B columns
 // stay within one L2), then walk tiles in column-major groups of `group_m` block-rows.
-__device__ __forceinline__ void tile_coords(int bid, int nbm, int nbn, int group_m, int& bm, int& bn) {
-  const int nblk = nbm * nbn;
-  int lin = bid;
-  if (nblk % 8 == 0) lin = (bid % 8) * (nblk / 8) + bid / 8;
+__device__ __forceinline__ void tile_of_linear(int lin, int nbm, int nbn, int group_m, int& bm, int& bn) {
   const int per_group = group_m * nbn;
   const int gid = lin / per_group;
   const int first_m = gid * group_m;
@@ -159,5 +156,30 @@ __device__ __forceinline__ void tile_coords(int bid, int nbm, int nbn, int group
   bm = first_m + in % gm;
   bn = in / gm;
 }
+__device__ __forceinline__ void tile_coords(int bid, int nbm, int nbn, int group_m, int& bm, int& bn) {
+  const int nblk = nbm * nbn;
+  int lin = bid;
+  if (nblk % 8 == 0) lin = (bid % 8) * (nblk / 8) + bid / 8;
+  tile_of_linear(lin, nbm, nbn, group_m, bm, bn);
+}
+
+// Persistent walk over the same order: workgroup b of `nwg` (resident one per CU, dispatched
+// round-robin over the 8 XCDs) takes the tiles of its XCD's contiguous range, slot by slot, so
+// the XCD's workgroups work on neighbouring tiles at any time.  first / step / end in linear
+// tile indices.
+__device__ __forceinline__ void tile_walk(int b, int nwg, int nblk, int& first, int& step, int& end) {
+  if (nblk % 8 == 0 && nwg % 8 == 0) {
+    const int range = nblk / 8, base = (b % 8) * range;
+    first = base + b / 8;
+    step = nwg / 8;
+    end = base + range;
+  } else {
+    first = b;
+    step = nwg;
+    end = nblk;
+  }
+}
+
+
 
 }  // namespace svdq

@@ -29,21 +29,52 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4
 
 
 // acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store (directly, or through the
-// wave's 8 KB LDS region `stage` when it is given).  mid is the activation
+// wave's 4 KB LDS region `stage` when it is given).  mid is the activation
 // pass's finalized operand, bf16 hi and lo planes per row ([M, 2, RTp]); both planes go through
 // the bf16 MFMA, so the low-rank term carries the f32 mid to 2^-18.  Two 16-column steps per
 // iteration, their twelve loads issued together (one memory latency per 32 columns of RTp).
 template <bool OUT_F32>
 __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2], int m0, int n0,
-                                         int lr, int h, uint8_t* stage) {
+                                         int lr, int h, uint8_t* stage, const uint8_t* lmid = nullptr,
+                                         const uint8_t* ll1 = nullptr, int wr = 0, int wc = 0) {
   const int RTp = p.RTp;
+  if (lmid != nullptr) {
+    // RTp == 32, operands prefetched into LDS by the GEMM's last stage: the tile's mid rows
+    // (128 bytes: hi plane, lo plane; 16-byte chunk c of row r at c ^ ((r >> 1) & 7)) and l1cat
+    // rows (64 bytes; chunk c of row r at c ^ ((r >> 2) & 3)); wr / wc = the wave's first
+    // row / column in the tile.  Conflict-free: 16 consecutive rows hit 16 distinct bank groups.
+    u32x4 ahi[2][2], alo[2][2], b[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r = wr + 32 * i + lr, sw = (r >> 1) & 7;
+        ahi[u][i] = ld16(lmid + r * 128 + 16 * ((2 * u + h) ^ sw));
+        alo[u][i] = ld16(lmid + r * 128 + 16 * ((4 + 2 * u + h) ^ sw));
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int c = wc + 32 * j + lr;
+        b[u][j] = ld16(ll1 + c * 64 + 16 * ((2 * u + h) ^ ((c >> 2) & 3)));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = mfma_bf16_32x32x16(ahi[u][i], b[u][j], acc[i][j]);
+          acc[i][j] = mfma_bf16_32x32x16(alo[u][i], b[u][j], acc[i][j]);
+        }
+  }
   const uint16_t* arow[2];
   const uint16_t* brow[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) arow[i] = p.midp + (long)min(m0 + 32 * i + lr, p.M - 1) * (2 * RTp) + 8 * h;
 #pragma unroll
   for (int j = 0; j < 2; ++j) brow[j] = p.l1cat + (long)min(n0 + 32 * j + lr, p.N - 1) * RTp + 8 * h;
-  for (int s = 0; s < RTp / 16; s += 2) {
+  for (int s = 0; s < (lmid != nullptr ? 0 : RTp / 16); s += 2) {
     u32x4 ahi[2][2], alo[2][2], b[2][2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -95,21 +126,24 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
     }
     return;
   }
-  // Staged: per 32-row half of the wave tile, the values go to the wave's LDS region (rows of
-  // 64 values, 16-byte chunk c of row r at c ^ (CPR / 2) when (r >> 2) is odd, so the two
-  // half-waves, 4 rows apart, write disjoint banks) and come back as 16-byte row chunks for
-  // coalesced stores.
+  // Staged: in passes of 4 KB (32 rows of bf16, 16 rows of f32 out of the wave's 64), the values
+  // go to the wave's LDS region (rows of 64 values; 16-byte chunk c of row r at c ^ (CPR / 2) when
+  // (r >> 2) is odd, so the two half-waves, 4 rows apart, write disjoint banks) and come back as
+  // 16-byte row chunks for coalesced stores.
   constexpr int ES = OUT_F32 ? 4 : 2;         // bytes per value
   constexpr int CPR = 64 * ES / 16;           // 16-byte chunks per row
   constexpr int VPC = 16 / ES;                // values per chunk
+  constexpr int RP = 4096 / (64 * ES);        // rows per pass: 32 or 16
+  constexpr int RPB = 16 * RP / 32;           // accumulator registers per 32-row sub-tile and pass
   const bool vec = (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && p.ldy % VPC == 0;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int q = 0; q < 64 / RP; ++q) {
+    const int i = q * RP / 32, rq = (q * RP) % 32;   // sub-tile, first row of the pass in it
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 8 * (r >> 2) + 4 * h + (r & 3), col = 32 * j + lr;
+      for (int r = RPB * (rq / RP); r < RPB * (rq / RP + 1); ++r) {
+        const int row = 8 * (r >> 2) + 4 * h + (r & 3) - rq, col = 32 * j + lr;
         const int pos = (col / VPC) ^ ((row >> 2) & 1 ? CPR / 2 : 0);
         uint8_t* dst = stage + row * (64 * ES) + pos * 16 + (col % VPC) * ES;
         const float v = acc[i][j][r] + bv[j];
@@ -117,11 +151,11 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
         else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
       }
 #pragma unroll
-    for (int it = 0; it < CPR / 2; ++it) {
+    for (int it = 0; it < RP * CPR / 64; ++it) {
       const int idx = 64 * it + (h << 5 | lr), row = idx / CPR, c = idx % CPR;
       const int pos = c ^ ((row >> 2) & 1 ? CPR / 2 : 0);
       const u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * (64 * ES) + pos * 16);
-      const int m = m0 + 32 * i + row, n = n0 + c * VPC;
+      const int m = m0 + 32 * i + rq + row, n = n0 + c * VPC;
       if (m >= p.M) continue;
       uint8_t* out = reinterpret_cast<uint8_t*>(p.y) + ((long)m * p.ldy + n) * ES;
       if (vec && n + VPC <= p.N) {
@@ -430,7 +464,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   // No DMA is in flight (none goes out in the last stage); once every wave is past its last
   // reads, the operand buffers hold the output staging regions.
   __syncthreads();
-  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, sA + wave * 8192);
+  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, sA + wave * 4096);
 }
 
 // W4A4 GEMM on the FP6 MFMA (e3m2 operands, v_mfma_scale_f32_32x32x64_f8f6f4 with format 3 on
@@ -491,6 +525,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
   for (int c = 0; c < 2; ++c) bq_o[c] = (uint32_t)min(n0 + 64 * c + lane, p.N - 1) * 16u;
   const uint32_t bp_o = (uint32_t)min(n0 + 2 * lane, Np - 2) * 8u;
   const long aP0 = (long)nkt * 2 * Mp * 16, bP0 = (long)nkt * 2 * Np * 16;   // P region offsets
+  const bool epi_lds = p.RTp == 32;   // the epilogue's mid / l1cat rows fit the free buffer
   if (tid < NBUF * GPS * 4) {
     sX[tid / (4 * GPS)][(tid / 4) % GPS][TBM + tid % 4] = 0u;
     sW[tid / (4 * GPS)][(tid / 4) % GPS][TBN + tid % 4] = 0u;
@@ -632,6 +667,18 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
         for (int d = hh * PER; d < (hh + 1) * PER; ++d)
           if (d < NDMA) dma(s + 1, nbuf, d);
       }
+      // last stage, RTp == 32: the epilogue's low-rank operands -> the free buffer nbuf (its A Q
+      // area: 256 mid rows of 128 bytes; its B Q area: 128 l1cat rows of 64 bytes), swizzled
+      // for the epilogue's reads
+      if (!more && epi_lds && hh == 0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int idx = (4 * wave + c) * 64 + lane, r = idx >> 3, ch = (idx & 7) ^ ((r >> 1) & 7);
+          dma16(p.midp, (uint32_t)min(m0 + r, p.M - 1) * 128u + 16u * ch, ldsAQ + nbuf * AQ + (4 * wave + c) * 1024);
+        }
+        const int idx = wave * 64 + lane, r = idx >> 2, ch = (idx & 3) ^ ((r >> 2) & 3);
+        dma16(p.l1cat, (uint32_t)min(n0 + r, p.N - 1) * 64u + 16u * ch, ldsBQ + nbuf * BQ + wave * 1024);
+      }
       if (!RM) {
         if (!last) {
           if (hg + 1 < H) read_half(buf, (hh + 1) >> 1, (hh + 1) & 1, 0, 0);
@@ -648,10 +695,13 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(P[j][r], S[j][r], acc[i][j][r]);
     }
   }
-  // No DMA is in flight (none goes out in the last stage); once every wave is past its last
-  // reads, the A planes hold the output staging regions.
+  // Only the epilogue operands' DMA can be in flight; once every wave is past its last reads,
+  // the last stage's A planes hold the output staging regions.
+  const int lbuf = (nstages - 1) & 1;
+  if (epi_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[0][0] + wave * 8192);
+  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[lbuf][0] + wave * 4096,
+                    epi_lds ? &sAQ[lbuf ^ 1][0] : nullptr, epi_lds ? &sBQ[lbuf ^ 1][0] : nullptr, 64 * wm, 64 * wn);
 }
 
 // Weight operand of the W4A4 GEMM, once per layer: each packed dword (8 nibbles, k0 in the
