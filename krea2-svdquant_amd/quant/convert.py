@@ -118,7 +118,9 @@ def convert_linear(weight: torch.Tensor, bias: torch.Tensor | None, x_absmax: to
 
     ``x_absmax=None`` gives identity smoothing (the reference's uncalibrated conversion).  The
     smoothing scale is rounded to bf16 first and the migration uses that stored value; the
-    residual subtracts the bf16-rounded factors that the runtime will use.
+    migrated weight ``W * s`` is rounded to the weight's own dtype, as the reference converter
+    does for its bf16 weights (``convert_simulated.py:188-194``; a no-op for fp32 weights), and
+    the residual subtracts the bf16-rounded factors that the runtime will use.
     """
     if weight.ndim != 2:
         raise ValueError("linear weight must be [out_features, in_features]")
@@ -128,7 +130,7 @@ def convert_linear(weight: torch.Tensor, bias: torch.Tensor | None, x_absmax: to
         smooth = torch.ones(k, device=w.device, dtype=torch.bfloat16)
     else:
         smooth = compute_smooth_scale(x_absmax.to(w.device), w, *smooth_clamp).to(torch.bfloat16)
-    migrated = w * smooth.float().unsqueeze(0)
+    migrated = (w * smooth.float().unsqueeze(0)).to(weight.dtype).float()
     l1, l2 = svd_lowrank(migrated, rank, oversample=oversample, niter=niter, exact=exact_svd, seed=seed)
     l1, l2 = l1.to(torch.bfloat16), l2.to(torch.bfloat16)
     residual = migrated - l1.float() @ l2.float()

@@ -94,3 +94,58 @@ def test_full_size_ffup_codes_exact_and_rows_sampled(dev):
     b = ds.bias.float()
     hom = ((y2 - b) - 2 * (y - b)).norm() / (y - b).norm()
     assert hom.item() < 1e-6
+
+
+def test_checkpoint_and_lora_loaders_end_to_end(dev, tmp_path):
+    """Dense model -> converter (SVD and quantization on the GPU) -> safetensors checkpoint ->
+    reader into a fresh model -> LoRA file -> fused forward of every loaded layer, each against
+    the oracle evaluation of the state the reader built (with the loaded adapter)."""
+    from torch import nn
+    from safetensors.torch import save_file
+    from krea2_svdquant_amd.quant.checkpoint import convert_transformer
+    from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
+    from krea2_svdquant_amd.runtime.load import load_svdquant_transformer
+    from krea2_svdquant_amd.runtime.lora import load_svdquant_lora_adapters
+
+    def dense(seed):
+        torch.manual_seed(seed)
+        root = nn.Module()
+        blk = nn.Module()
+        blk.attn = nn.Module()
+        blk.attn.to_q = nn.Linear(512, 384)
+        blk.attn.to_k = nn.Linear(512, 128, bias=False)
+        blk.ff = nn.Module()
+        blk.ff.up = nn.Linear(512, 640, bias=False)
+        for lin in (blk.attn.to_q, blk.attn.to_k, blk.ff.up):
+            nn.init.normal_(lin.weight, std=0.02)
+        root.transformer_blocks = nn.ModuleList([blk])
+        return root
+
+    x = synth.make_activation(80, 512, seed=51)
+    absmax = {"transformer_blocks.0.attn.to_q": torch.from_numpy(np.abs(x).max(0)),
+              "transformer_blocks.0.ff.up": torch.from_numpy(np.abs(x).max(0))}
+    meta = convert_transformer(dense(50), tmp_path / "ckpt", absmax=absmax, group_size=64, attn_rank=32,
+                               mlp_rank=64, svd_device=dev, seed=7, log=None)
+    assert set(meta["layers"]) == {"transformer_blocks.0.attn.to_q", "transformer_blocks.0.attn.to_k",
+                                   "transformer_blocks.0.ff.up"}
+    model = dense(99)
+    rep = load_svdquant_transformer(model, tmp_path / "ckpt", backend="auto")["_load_report"]
+    assert len(rep["replaced"]) == 3 and not rep["missing"]
+    model.to(dev)
+    ad = synth.make_adapter(384, 512, rank=16, seed=52)
+    save_file({"transformer.transformer_blocks.0.attn.to_q.lora_A.weight": torch.from_numpy(ad.down).to(torch.bfloat16),
+               "transformer.transformer_blocks.0.attn.to_q.lora_B.weight": torch.from_numpy(ad.up).to(torch.bfloat16),
+               "transformer.transformer_blocks.0.attn.to_q.alpha": torch.tensor(8.0)}, tmp_path / "lora.safetensors")
+    lrep = load_svdquant_lora_adapters(model, tmp_path / "lora.safetensors", scale=0.8)
+    assert lrep["loaded"] == ["transformer_blocks.0.attn.to_q"]
+    xd = bf16_tensor(x, dev)
+    blk = model.transformer_blocks[0]
+    for mod, adapters in ((blk.attn.to_q, [sim.Adapter(ad.down, ad.up, scale=0.8, network_alpha=8.0)]),
+                          (blk.attn.to_k, []), (blk.ff.up, [])):
+        assert isinstance(mod, SVDQuantLinear)
+        y = mod(xd).float().cpu().numpy()
+        st = from_device_state(mod.state)
+        st.adapters.extend(adapters)
+        e = rel_l2(y, nm.bf16(sim.w4a4_eval(x, st)["y"].astype(np.float32)))
+        print(f"  loaded {tuple(st.shape)} adapters={len(adapters)} rel_l2={e:.3e}")
+        assert e < 1e-3
