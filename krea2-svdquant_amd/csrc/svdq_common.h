@@ -163,23 +163,4 @@ __device__ __forceinline__ void tile_coords(int bid, int nbm, int nbn, int group
   tile_of_linear(lin, nbm, nbn, group_m, bm, bn);
 }
 
-// Persistent walk over the same order: workgroup b of `nwg` (resident one per CU, dispatched
-// round-robin over the 8 XCDs) takes the tiles of its XCD's contiguous range, slot by slot, so
-// the XCD's workgroups work on neighbouring tiles at any time.  first / step / end in linear
-// tile indices.
-__device__ __forceinline__ void tile_walk(int b, int nwg, int nblk, int& first, int& step, int& end) {
-  if (nblk % 8 == 0 && nwg % 8 == 0) {
-    const int range = nblk / 8, base = (b % 8) * range;
-    first = base + b / 8;
-    step = nwg / 8;
-    end = base + range;
-  } else {
-    first = b;
-    step = nwg;
-    end = nblk;
-  }
-}
-
-
-
 }  // namespace svdq

@@ -14,6 +14,7 @@
 // INT4 nibbles; the activation operand is written in the same order, so the permutation
 // cancels in every dot product.
 #include <algorithm>
+#include <type_traits>
 
 #include "svdq_common.h"
 #include "svdq_kernels.h"
@@ -482,7 +483,13 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
 // share of the scale tiles: 12 DMA instructions per wave per stage for G = 64) and waited for
 // before the barrier that ends stage s.  Rows of the planes are padded to an even count so that a
 // 16-byte DMA lane carries two 8-byte P rows.
-template <int G, bool OUT_F32>
+//
+// FULL (K a multiple of 2 KB): every stage holds KB columns and the stages pair up, so the main
+// loop runs two stages per iteration with the buffer of each a compile-time constant (LDS
+// offsets fold into the read and DMA instructions), no step carries a bound check, the last
+// stage is peeled (no DMA, the epilogue's prefetch), and the DMA sources are wave-uniform
+// pointers advanced one stage at a time.  Other K take the general loop.
+template <int G, bool OUT_F32, bool FULL>
 __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
   constexpr int TBM = 256, TBN = 128, NBUF = 2;
   constexpr int KB = 256;                     // K columns per pipeline stage
@@ -621,12 +628,169 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
 #undef SVDQ_FRAGS6_1
 #undef SVDQ_FRAGS6_2
 
+  // last stage, RTp == 32: the epilogue's low-rank operands -> the free buffer (its A Q area:
+  // 256 mid rows of 128 bytes; its B Q area: 128 l1cat rows of 64 bytes), swizzled for the
+  // epilogue's reads
+  auto epi_prefetch = [&](int fbuf) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = (4 * wave + c) * 64 + lane, r = idx >> 3, ch = (idx & 7) ^ ((r >> 1) & 7);
+      dma16(p.midp, (uint32_t)min(m0 + r, p.M - 1) * 128u + 16u * ch, ldsAQ + fbuf * AQ + (4 * wave + c) * 1024);
+    }
+    const int idx = wave * 64 + lane, r = idx >> 2, ch = (idx & 3) ^ ((r >> 2) & 3);
+    dma16(p.l1cat, (uint32_t)min(n0 + r, p.N - 1) * 64u + 16u * ch, ldsBQ + fbuf * BQ + wave * 1024);
+  };
+  // This step's fragments in place and the previous step's rescale issued before the next reads
+  // go out (keeps one register set live per step).
+  auto step_fence = [&](int i, int ai, int bi) {
+    asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(faq[ai][0]),
+                 "+v"(fap[ai][KS - 1]), "+v"(fbq[bi][0][0]), "+v"(fbp[bi][0][KS - 1]), "+v"(fbq[bi][1][0]),
+                 "+v"(fbp[bi][1][KS - 1]), "+v"(xop[i]), "+v"(wop_[bi][0]), "+v"(wop_[bi][1])::"memory");
+  };
+
   // Stage 0 landed everywhere; stage s + 1 goes out during stage s.
 #pragma unroll
   for (int d = 0; d < NDMA; ++d) dma(0, 0, d);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   read_half(0, 0, 0, 0, 0);
+
+  if constexpr (FULL) {
+    // DMA sources of stage 1 (advanced per stage) and wave-uniform LDS bases.
+    const uint8_t* gAQ = p.qa + (long)(8 + wave) * Mp * 16;
+    const uint8_t* gAP = p.qa + aP0 + (long)(8 + wave) * Mp * 8;
+    const uint8_t* gBQ = p.qwe + (long)(8 + wave) * Np * 16;
+    const uint8_t* gBP = p.qwe + bP0 + (long)(8 + wave) * Np * 8;
+    const uint32_t* gX = p.sxp + (long)GPS * p.M;
+    const uint32_t* gW = p.swp + (long)GPS * p.N;
+    const uint32_t lAQ = ldsAQ + wave * TBM * 16, lAP = ldsAP + wave * TBM * 8, lBQ = ldsBQ + wave * TBN * 16,
+                   lBP = ldsBP + wave * TBN * 8;
+    uint32_t sx_o[SXD], lX[SXD], sw_o[SWD], lW[SWD];
+#pragma unroll
+    for (int d = 0; d < SXD; ++d) {
+      const int w0 = (512 * d + 64 * wave) % (GPS * TBM), j = w0 / TBM, r0 = w0 % TBM;
+      sx_o[d] = 4u * ((uint32_t)j * (uint32_t)p.M + (uint32_t)min(m0 + r0 + lane, p.M - 1));
+      lX[d] = ldsX + 4 * (j * XS + r0);
+    }
+#pragma unroll
+    for (int d = 0; d < SWD; ++d) {
+      const int w0 = (512 * d + 64 * wave) % (GPS * TBN), j = w0 / TBN, r0 = w0 % TBN;
+      sw_o[d] = 4u * ((uint32_t)j * (uint32_t)p.N + (uint32_t)min(n0 + r0 + lane, p.N - 1));
+      lW[d] = ldsW + 4 * (j * WS + r0);
+    }
+    const long stA = 8L * Mp, stB = 8L * Np;   // bytes per stage / 16 (Q) and / 8 (P)
+    // Per-lane LDS bases of the fragment reads; every read is base + a compile-time offset
+    // (buffer, plane, sub-tile).  The bases are re-declared opaque at each stage so that the
+    // compiler folds the offsets into the instructions instead of keeping one address register
+    // per offset across the loop.
+    typedef const __attribute__((address_space(3))) uint8_t* lds_u8;
+    typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
+    typedef const __attribute__((address_space(3))) u32x2* lds_u32x2;
+    typedef const __attribute__((address_space(3))) uint32_t* lds_u32;
+    lds_u8 rAQ = (lds_u8)&sAQ[0][(h * TBM + 64 * wm + lr) * 16];
+    lds_u8 rAP = (lds_u8)&sAP[0][(h * TBM + 64 * wm + lr) * 8];
+    lds_u8 rBQ = (lds_u8)&sBQ[0][(h * TBN + 64 * wn + lr) * 16];
+    // (the two column sub-tiles' 8-byte parts get separate bases: merged into one ds_read2_b64,
+    // they would have to be copied next to their 16-byte parts)
+    lds_u8 rBP = (lds_u8)&sBP[0][(h * TBN + 64 * wn + lr) * 8], rBP1 = rBP + 32 * 8;
+    lds_u8 rX = (lds_u8)&sX[0][0][0] + xo0;
+    lds_u8 rW0 = (lds_u8)&sW[0][0][0] + wo0, rW1 = (lds_u8)&sW[0][0][0] + wo1;
+    auto read_half_full = [&](int buf, int gi, int i, int ai, int bi) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int pl2 = (gi * KS + ks) * 2;   // plane pair of this k-step; the lane's half picks one
+        faq[ai][ks] = *(lds_u32x4)(rAQ + buf * AQ + (pl2 * TBM + 32 * i) * 16);
+        fap[ai][ks] = *(lds_u32x2)(rAP + buf * AP + (pl2 * TBM + 32 * i) * 8);
+        if (i == 0) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            fbq[bi][j][ks] = *(lds_u32x4)(rBQ + buf * BQ + (pl2 * TBN + 32 * j) * 16);
+            fbp[bi][j][ks] = *(lds_u32x2)((j ? rBP1 : rBP) + buf * BP + pl2 * TBN * 8);
+          }
+        }
+      }
+      xop[i][0] = *(lds_u32)(rX + 4 * ((buf * GPS + gi) * XS) + (i ? xo1 - xo0 : 0));
+      if (i == 0) {
+        wop_[bi][0][0] = *(lds_u32)(rW0 + 4 * ((buf * GPS + gi) * WS));
+        wop_[bi][1][0] = *(lds_u32)(rW1 + 4 * ((buf * GPS + gi) * WS));
+      }
+    };
+    auto dma_next = [&](int nb, int d) {
+      if (d < 4) dma16(gAQ, aq_o[d], lAQ + nb * AQ + 64 * d * 16);
+      else if (d < 6) dma16(gAP, ap_o[d - 4], lAP + nb * AP + 128 * (d - 4) * 8);
+      else if (d < 8) dma16(gBQ, bq_o[d - 6], lBQ + nb * BQ + 64 * (d - 6) * 16);
+      else if (d == 8) dma16(gBP, bp_o, lBP + nb * BP);
+      else if (d < 9 + SXD) dma4(gX, sx_o[d - 9], lX[d - 9] + 4 * nb * GPS * XS);
+      else dma4(gW, sw_o[d - 9 - SXD], lW[d - 9 - SXD] + 4 * nb * GPS * WS);
+    };
+    auto stage = [&](auto buf_c, auto last_c) {
+      constexpr int buf = decltype(buf_c)::value, nbuf = buf ^ 1;
+      constexpr bool LASTST = decltype(last_c)::value;
+      asm volatile("" : "+v"(rAQ), "+v"(rAP), "+v"(rBQ), "+v"(rBP), "+v"(rBP1), "+v"(rX), "+v"(rW0), "+v"(rW1));
+#pragma unroll
+      for (int hh = 0; hh < HPS; ++hh) {
+        const int i = hh & 1, gi = hh >> 1;
+        const int ai = RM ? i : 0, bi = RM ? (gi & 1) : 0;
+        const bool last = hh == HPS - 1;
+        step_fence(i, ai, bi);
+        if (RM) {
+          if (last) {
+            if (!LASTST) {
+              asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+              frag_fence();
+              asm volatile("s_barrier" ::: "memory");
+              read_half_full(nbuf, 0, 0, 0, 0);
+            }
+          } else {
+            read_half_full(buf, (hh + 1) >> 1, (hh + 1) & 1, (hh + 1) & 1, ((hh + 1) >> 1) & 1);
+          }
+        }
+        f32x16 P[2], S[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          P[j] = mfma_p6(ai, bi, j);
+          S[j] = mfma_bf16_32x32x16(xop[i], wop_[bi][j], f32x16{});
+        }
+        if (!LASTST && hh < NPART) {
+#pragma unroll
+          for (int d = hh * PER; d < (hh + 1) * PER; ++d)
+            if (d < NDMA) dma_next(nbuf, d);
+        }
+        if (LASTST && hh == 0 && epi_lds) epi_prefetch(nbuf);
+        if (!RM) {
+          if (!last) {
+            read_half_full(buf, (hh + 1) >> 1, (hh + 1) & 1, 0, 0);
+          } else if (!LASTST) {
+            asm volatile("" : "+v"(P[0]), "+v"(P[1]), "+v"(S[0]), "+v"(S[1])::"memory");
+            asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+            read_half_full(nbuf, 0, 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(P[j][r], S[j][r], acc[i][j][r]);
+      }
+      if (!LASTST) {
+        gAQ += stA * 16;
+        gAP += stA * 8;
+        gBQ += stB * 16;
+        gBP += stB * 8;
+        gX += (long)GPS * p.M;
+        gW += (long)GPS * p.N;
+      }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using NO = std::integral_constant<bool, false>;
+    using YES = std::integral_constant<bool, true>;
+    for (int s = 0; s + 2 < nstages; s += 2) {
+      stage(B0{}, NO{});
+      stage(B1{}, NO{});
+    }
+    stage(B0{}, NO{});
+    stage(B1{}, YES{});
+  } else {
   for (int s = 0; s < nstages; ++s) {
     const bool more = s + 1 < nstages;
     const int buf = s & 1, nbuf = buf ^ 1;
@@ -637,11 +801,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
       const int i = hh & 1, gi = hh >> 1;
       const int ai = RM ? i : 0, bi = RM ? (gi & 1) : 0;
       const bool last = hh == HPS - 1;
-      // This step's fragments in place and the previous step's rescale issued before the next
-      // reads go out (keeps one register set live per step).
-      asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(faq[ai][0]),
-                   "+v"(fap[ai][KS - 1]), "+v"(fbq[bi][0][0]), "+v"(fbp[bi][0][KS - 1]), "+v"(fbq[bi][1][0]),
-                   "+v"(fbp[bi][1][KS - 1]), "+v"(xop[i]), "+v"(wop_[bi][0]), "+v"(wop_[bi][1])::"memory");
+      step_fence(i, ai, bi);
       if (RM) {
         if (last) {
           if (more) {
@@ -667,18 +827,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
         for (int d = hh * PER; d < (hh + 1) * PER; ++d)
           if (d < NDMA) dma(s + 1, nbuf, d);
       }
-      // last stage, RTp == 32: the epilogue's low-rank operands -> the free buffer nbuf (its A Q
-      // area: 256 mid rows of 128 bytes; its B Q area: 128 l1cat rows of 64 bytes), swizzled
-      // for the epilogue's reads
-      if (!more && epi_lds && hh == 0) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int idx = (4 * wave + c) * 64 + lane, r = idx >> 3, ch = (idx & 7) ^ ((r >> 1) & 7);
-          dma16(p.midp, (uint32_t)min(m0 + r, p.M - 1) * 128u + 16u * ch, ldsAQ + nbuf * AQ + (4 * wave + c) * 1024);
-        }
-        const int idx = wave * 64 + lane, r = idx >> 2, ch = (idx & 3) ^ ((r >> 2) & 3);
-        dma16(p.l1cat, (uint32_t)min(n0 + r, p.N - 1) * 64u + 16u * ch, ldsBQ + nbuf * BQ + wave * 1024);
-      }
+      if (!more && epi_lds && hh == 0) epi_prefetch(nbuf);
       if (!RM) {
         if (!last) {
           if (hg + 1 < H) read_half(buf, (hh + 1) >> 1, (hh + 1) & 1, 0, 0);
@@ -694,6 +843,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(P[j][r], S[j][r], acc[i][j][r]);
     }
+  }
   }
   // Only the epilogue operands' DMA can be in flight; once every wave is past its last reads,
   // the last stage's A planes hold the output staging regions.
@@ -872,16 +1022,21 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
   SVDQ_W4A4(128, 1)
 #undef SVDQ_W4A4
   if (mode == 2) {
-    if (G == 64) {
-      if (out_f32) w4a4_e3m2_kernel<64, true><<<grid, 512, 0, st>>>(p);
-      else w4a4_e3m2_kernel<64, false><<<grid, 512, 0, st>>>(p);
-      return hipGetLastError();
-    }
-    if (G == 128) {
-      if (out_f32) w4a4_e3m2_kernel<128, true><<<grid, 512, 0, st>>>(p);
-      else w4a4_e3m2_kernel<128, false><<<grid, 512, 0, st>>>(p);
-      return hipGetLastError();
-    }
+    const bool full = p.K % 512 == 0;   // two full 256-column stages per main-loop iteration
+#define SVDQ_E3M2(GG)                                                                  \
+  if (G == GG) {                                                                       \
+    if (full) {                                                                        \
+      if (out_f32) w4a4_e3m2_kernel<GG, true, true><<<grid, 512, 0, st>>>(p);           \
+      else w4a4_e3m2_kernel<GG, false, true><<<grid, 512, 0, st>>>(p);                  \
+    } else {                                                                           \
+      if (out_f32) w4a4_e3m2_kernel<GG, true, false><<<grid, 512, 0, st>>>(p);          \
+      else w4a4_e3m2_kernel<GG, false, false><<<grid, 512, 0, st>>>(p);                 \
+    }                                                                                  \
+    return hipGetLastError();                                                          \
+  }
+    SVDQ_E3M2(64)
+    SVDQ_E3M2(128)
+#undef SVDQ_E3M2
   }
   return hipErrorInvalidValue;
 }

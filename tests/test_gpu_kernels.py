@@ -197,6 +197,12 @@ def test_layer_golden(dev, name, mode):
     (33, 128, 896, 128, 64, 64, False),   # group 128: 7 stages
     (70, 100, 256, 64, 32, 0, True),      # two stages; N % 8 != 0 (element stores at the tile edge)
     (50, 136, 128, 128, 32, 32, False),   # group 128: a single stage
+    # K a multiple of 512: the e3m2 kernel's paired-stage main loop (the others take its
+    # general loop); rank 32 without LoRA puts the epilogue operands in LDS
+    (300, 264, 512, 64, 32, 0, True),     # two stages: only the peeled pair
+    (130, 200, 1536, 64, 32, 0, False),   # six stages
+    (96, 384, 1024, 128, 32, 0, True),    # group 128, four stages
+    (64, 130, 2560, 128, 32, 16, True),   # group 128, ten stages, LoRA
 ])
 @pytest.mark.parametrize("mode", ["w4a4", "w4a16"])
 def test_layer_random_shapes(dev, m, n, k, g, r, rl, bias, mode):
