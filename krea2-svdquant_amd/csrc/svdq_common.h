@@ -144,6 +144,37 @@ __device__ __forceinline__ void split_hi_lo(const float* v, u32x4& hi, u32x4& lo
   }
 }
 
+// VGPR banks of the rescale FMA acc += P * S.  The FMA reads three VGPRs; the register file
+// has four banks (register index mod 4) and three operands in one bank issue at about half
+// rate (measured: 1.85x the time of three distinct banks).  The allocator starts the MFMA result
+// tuples P and S and the accumulator tuple in the same bank, so register r of each lands in
+// one bank.  Two rotations put the operands of every FMA in three consecutive banks:
+//  * S one register ahead: the scale MFMA's A operand (rows of sx) is read with the rows
+//    permuted so that S register r + 1 holds the row of P register r (D layout: register r of
+//    lane half h holds row 8 (r / 4) + 4 h + r % 4);
+//  * the accumulator two registers ahead: logical register r lives in acc[(r + 2) % 16], undone
+//    once before the epilogue.
+__device__ __forceinline__ int scale_row_perm(int row) {   // row in 0..31
+  const int reg = 4 * (row >> 3) + (row & 3);              // D register of this row
+  const int prev = (reg + 15) & 15;                        // one register earlier
+  return 8 * (prev >> 2) + (row & 4) + (prev & 3);
+}
+__device__ __forceinline__ void rescale_acc(f32x16& acc, const f32x16& P, const f32x16& S) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[(r + 2) & 15] = __builtin_fmaf(P[r], S[(r + 1) & 15], acc[(r + 2) & 15]);
+}
+__device__ __forceinline__ void unrotate_acc(f32x16 (&acc)[2][2]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f32x16 t;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) t[r] = acc[i][j][(r + 2) & 15];
+      acc[i][j] = t;
+    }
+}
+
 // XCD-aware block order: hardware hands consecutive workgroup ids to the 8 XCDs round-robin;
 // remap so that each XCD receives a contiguous range of output tiles (shared A rows / B columns
 // stay within one L2), then walk tiles in column-major groups of `group_m` block-rows.

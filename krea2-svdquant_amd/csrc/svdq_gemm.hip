@@ -318,7 +318,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   // Scale-MFMA operands: persistent tuples, word 0 reloaded from LDS, words 1-3 stay zero.
   // A = (sx, sx) of the lane's row; B = (hi, lo) of the lane's column for lanes 0-31 and zero
   // for lanes 32-63 (they read the zero word).
-  const int xo0 = 4 * (64 * wm + lr), xo1 = xo0 + 128;
+  const int xo0 = 4 * (64 * wm + scale_row_perm(lr)), xo1 = xo0 + 128;   // rows permuted: see rescale_acc
   const int wo0 = 4 * (h ? TBN : 64 * wn + lr), wo1 = 4 * (h ? TBN : 64 * wn + 32 + lr);
   u32x4 xop[2] = {u32x4{}, u32x4{}};
 
@@ -457,14 +457,14 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const f32x16 pf = MODE == 0 ? P[j] : __builtin_convertvector(PI[j], f32x16);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(pf[r], S[j][r], acc[i][j][r]);
+        rescale_acc(acc[i][j], pf, S[j]);
       }
     }
   }
   // No DMA is in flight (none goes out in the last stage); once every wave is past its last
   // reads, the operand buffers hold the output staging regions.
   __syncthreads();
+  unrotate_acc(acc);
   epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, sA + wave * 4096);
 }
 
@@ -573,7 +573,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  const int xo0 = 4 * (64 * wm + lr), xo1 = xo0 + 128;
+  const int xo0 = 4 * (64 * wm + scale_row_perm(lr)), xo1 = xo0 + 128;   // rows permuted: see rescale_acc
   const int wo0 = 4 * (h ? TBN : 64 * wn + lr), wo1 = 4 * (h ? TBN : 64 * wn + 32 + lr);
   u32x4 xop[2] = {u32x4{}, u32x4{}};
 
@@ -768,8 +768,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(P[j][r], S[j][r], acc[i][j][r]);
+          rescale_acc(acc[i][j], P[j], S[j]);
       }
       if (!LASTST) {
         gAQ += stA * 16;
@@ -840,8 +839,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(P[j][r], S[j][r], acc[i][j][r]);
+        rescale_acc(acc[i][j], P[j], S[j]);
     }
   }
   }
@@ -850,6 +848,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
   const int lbuf = (nstages - 1) & 1;
   if (epi_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  unrotate_acc(acc);
   epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[lbuf][0] + wave * 4096,
                     epi_lds ? &sAQ[lbuf ^ 1][0] : nullptr, epi_lds ? &sBQ[lbuf ^ 1][0] : nullptr, 64 * wm, 64 * wn);
 }
