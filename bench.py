@@ -68,7 +68,9 @@ def parse():
                     help="W4A4 MFMA operand format (e3m2 = FP6 MFMA, the default path)")
     ap.add_argument("--cpu-reps", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-block", action="store_true", help="skip the config 1/2/4 extra lines")
+    ap.add_argument("--no-block", action="store_true", help="skip the config 1-4 extra lines")
+    ap.add_argument("--lines", default="block,w4a16,lora,denoise",
+                    help="extra lines to run (comma list of block, w4a16, lora, denoise)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="counter pass for rocprofv3: one copy kernel of known size, then GEMM launches")
     return ap.parse_args()
@@ -220,6 +222,54 @@ def lora_line(args, dev) -> dict:
                                    "up in the GEMM epilogue), M=16384"}
 
 
+def denoise_line(args, dev) -> dict:
+    """the 28-block stand-in Krea-2 denoiser, 1024px (4096 latent + 256 text
+    tokens, one stream of M=4352), batch 1, 8 Euler steps, every block resident in HBM."""
+    import torch
+    from krea2_svdquant_amd.runtime.krea2_standin import Krea2Dims, Krea2StandInTransformer
+    dims = Krea2Dims()
+    model = Krea2StandInTransformer.random(dims, rank=args.rank, group_size=args.group, device=dev, seed=3)
+    gen = torch.Generator(device=dev).manual_seed(4)
+    text = torch.randn(256, dims.hidden, device=dev, generator=gen).to(torch.bfloat16)
+    latent = torch.randn(4096, dims.hidden, device=dev, generator=gen).to(torch.bfloat16)
+    steps, dt = 8, -1.0 / 8
+    lat = model.denoise_step(text, latent, dt)      # warm-up: builds every layer's kernel operands
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    lat = latent
+    a.record()
+    for _ in range(steps):
+        lat = model.denoise_step(text, lat, dt)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    # one more step with HIP events around every quantized linear: their share of the step
+    pairs = []
+
+    def timed(name, mod, x):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        y = mod(x)
+        e1.record()
+        pairs.append((e0, e1))
+        return y
+    torch.cuda.synchronize()
+    model.forward(torch.cat([text, lat], 0), linear=timed)
+    torch.cuda.synchronize()
+    lin_ms = sum(e0.elapsed_time(e1) for e0, e1 in pairs)
+    finite = bool(torch.isfinite(lat.float()).all())
+    hbm_gb = torch.cuda.max_memory_allocated(dev) / 1e9
+    del model
+    torch.cuda.empty_cache()
+    return {"ms_per_denoise_step": round(ms, 3), "ms_8_steps": round(ms * steps, 2),
+            "linears_ms_per_step": round(lin_ms, 3), "rest_ms_per_step": round(ms - lin_ms, 3),
+            "tokens": 4352, "blocks": dims.layers, "peak_hbm_GB": round(hbm_gb, 1), "finite": finite,
+            "note": "stand-in Krea-2 denoiser (diffusers is absent): 28 blocks, 8 W4A4 linears each on this "
+                    "backend; attention (SDPA, 48 q / 12 kv heads), RMS norms, rotary embedding, gates in "
+                    "PyTorch-ROCm; random-init quantized weights, N(0,1) tokens; HIP events around 8 Euler steps "
+                    "after one warm-up step"}
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -318,13 +368,20 @@ def main() -> int:
                      "int8_dense_peak_frac": round(gemm_tflops / INT8_PEAK_TOPS, 4)},
     }
     if not args.no_block:
-        log("block line: 8 linears of config 1")
+        lines = set(args.lines.split(","))
         del qa, sx, mid
-        result["block_config1"] = block_line(args, dev)
-        log("config 2: W4A16 block at M=2304")
-        result["w4a16_config2"] = w4a16_line(args, dev)
-        log("config 4: M=16384 with fused LoRA r64")
-        result["lora_config4"] = lora_line(args, dev)
+        if "block" in lines:
+            log("block line: 8 linears of config 1")
+            result["block_config1"] = block_line(args, dev)
+        if "w4a16" in lines:
+            log("config 2: W4A16 block at M=2304")
+            result["w4a16_config2"] = w4a16_line(args, dev)
+        if "lora" in lines:
+            log("config 4: M=16384 with fused LoRA r64")
+            result["lora_config4"] = lora_line(args, dev)
+        if "denoise" in lines:
+            log("config 3: 28-block denoise steps at 1024px")
+            result["denoise_config3"] = denoise_line(args, dev)
     if not args.no_cpu_baseline:
         log("cpu baseline (whole layer)")
         result["cpu_baseline"] = cpu_baseline(ds, x, args.cpu_reps)

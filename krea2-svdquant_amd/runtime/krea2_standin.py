@@ -1,0 +1,228 @@
+"""Stand-in Krea-2 denoiser: whole denoise steps over the quantized linears of this package.
+
+The reference wraps diffusers' ``Krea2Transformer2DModel`` (``src/krea2_svdquant/transformer.py:46-59``),
+which is not installed here and whose block internals the reference does not contain.  This
+module builds a transformer with the public dimensions the reference states (``README.md:27-37``:
+28 blocks, hidden 6144, 48 query heads and 12 KV heads of 128, MLP 16384) and the eight
+quantized linears per block under the reference's module names (``README.md:41-51``:
+``transformer_blocks.{i}.attn.to_q`` ... ``transformer_blocks.{i}.ff.down``), so the checkpoint
+reader and the module replacement address them as they would in the real model.
+
+What the block computes around those linears is this module's own choice (single stream over
+the concatenated text and latent tokens, modulation vectors fixed per block):
+
+    h = rms_norm(x) * (1 + scale_a) + shift_a
+    q, k, v = to_q(h), to_k(h), to_v(h);  per-head RMS norm of q and k;  rotary embedding on q, k
+    a = softmax(q k^T / sqrt(d)) v  (48 query heads over 12 KV heads, PyTorch SDPA)
+    x = x + gate_a * to_out.0(a * sigmoid(to_gate(h)))
+    h = rms_norm(x) * (1 + scale_f) + shift_f
+    x = x + gate_f * ff.down(silu(ff.gate(h)) * ff.up(h))
+
+A denoise step is the 28 blocks over [text | latent] tokens followed by the Euler update of the
+latent tokens, ``latent += dt * velocity``.  Attention, norms and elementwise work run in
+PyTorch-ROCm; every quantized linear runs on the gfx950 kernels (``SVDQuantLinear``).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Callable, Optional
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from ..quant.state import SVDQuantLinearState
+from .linear import SVDQuantLinear
+
+LINEAR_NAMES = ("attn.to_q", "attn.to_k", "attn.to_v", "attn.to_gate", "attn.to_out.0",
+                "ff.gate", "ff.up", "ff.down")
+
+
+@dataclass(frozen=True)
+class Krea2Dims:
+    """Public dimensions of Krea-2-Turbo's denoiser (reference ``README.md:27-37``)."""
+    layers: int = 28
+    hidden: int = 6144
+    heads: int = 48
+    kv_heads: int = 12
+    head_dim: int = 128
+    mlp: int = 16384
+
+    def linear_shapes(self) -> dict[str, tuple[int, int]]:
+        """(out_features, in_features) of each quantized linear of a block."""
+        h, kv = self.hidden, self.kv_heads * self.head_dim
+        return {"attn.to_q": (self.heads * self.head_dim, h), "attn.to_k": (kv, h), "attn.to_v": (kv, h),
+                "attn.to_gate": (h, h), "attn.to_out.0": (h, self.heads * self.head_dim),
+                "ff.gate": (self.mlp, h), "ff.up": (self.mlp, h), "ff.down": (h, self.mlp)}
+
+
+def random_quantized_state(n: int, k: int, *, rank: int = 32, group_size: int = 64,
+                           device: torch.device | str = "cuda", generator: torch.Generator | None = None
+                           ) -> SVDQuantLinearState:
+    """A random-init layer in the checkpoint layout, drawn directly in quantized form.
+
+    Codes are uniform over the 16 INT4 values, fp16 group scales sit where a N(0, 0.02) weight's
+    would (amax / 7 of a 64-sample group), the smoothing scale is uniform in [1, 4] and the
+    factors are small Gaussians.  The kernels' work does not depend on the values, so this
+    stands in for converting 224 dense random layers when only time is measured.
+    """
+    dev = torch.device(device)
+    g = generator
+
+    def randn(*shape):
+        return torch.randn(*shape, device=dev, generator=g)
+
+    kp = (k + group_size - 1) // group_size * group_size
+    qweight = torch.randint(0, 256, (n, kp // 2), device=dev, generator=g, dtype=torch.uint8)
+    scales = (0.02 * 2.5 / 7.0) * (0.8 + 0.4 * torch.rand(n, kp // group_size, device=dev, generator=g))
+    smooth = 1.0 + 3.0 * torch.rand(k, device=dev, generator=g)
+    return SVDQuantLinearState(
+        smooth_scale=smooth.to(torch.bfloat16), qweight=qweight, weight_scales=scales.to(torch.float16),
+        l1=(randn(n, rank) * 0.05).to(torch.bfloat16), l2=(randn(rank, k) / math.sqrt(k)).to(torch.bfloat16),
+        bias=None, group_size=group_size, original_shape=(n, k), qweight_packed=True, padded_in_features=kp)
+
+
+def rms_norm(x: Tensor, eps: float = 1e-6) -> Tensor:
+    """RMS norm over the last dimension (no learned weight), in x's dtype with an fp32 reduction."""
+    return F.rms_norm(x, (x.shape[-1],), eps=eps)
+
+
+def rope_tables(tokens: int, head_dim: int, device, dtype, theta: float = 10000.0) -> tuple[Tensor, Tensor]:
+    """cos / sin tables [tokens, head_dim] of the rotate-half rotary embedding."""
+    inv = 1.0 / theta ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim)
+    ang = torch.arange(tokens, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos().to(dtype), ang.sin().to(dtype)
+
+
+def apply_rope(t: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    """t [T, heads, d] rotated by position: t * cos + rotate_half(t) * sin."""
+    d = t.shape[-1] // 2
+    rot = torch.cat([-t[..., d:], t[..., :d]], dim=-1)
+    return t * cos[:, None, :] + rot * sin[:, None, :]
+
+
+LinearFn = Callable[[str, nn.Module, Tensor], Tensor]
+
+
+def _module_linear(name: str, mod: nn.Module, x: Tensor) -> Tensor:
+    return mod(x)
+
+
+class _Attn(nn.Module):
+    def __init__(self, layers: dict[str, nn.Module]):
+        super().__init__()
+        self.to_q, self.to_k, self.to_v = layers["attn.to_q"], layers["attn.to_k"], layers["attn.to_v"]
+        self.to_gate = layers["attn.to_gate"]
+        self.to_out = nn.ModuleList([layers["attn.to_out.0"]])
+
+
+class _FF(nn.Module):
+    def __init__(self, layers: dict[str, nn.Module]):
+        super().__init__()
+        self.gate, self.up, self.down = layers["ff.gate"], layers["ff.up"], layers["ff.down"]
+
+
+class Krea2StandInBlock(nn.Module):
+    """One block: the eight quantized linears (``attn.*``, ``ff.*``) plus modulation vectors."""
+
+    def __init__(self, dims: Krea2Dims, layers: dict[str, nn.Module], modulation: Tensor):
+        super().__init__()
+        if set(layers) != set(LINEAR_NAMES):
+            raise ValueError(f"block needs exactly the linears {LINEAR_NAMES}, got {sorted(layers)}")
+        if tuple(modulation.shape) != (6, dims.hidden):
+            raise ValueError(f"modulation must be [6, {dims.hidden}], got {tuple(modulation.shape)}")
+        self.dims = dims
+        self.attn = _Attn(layers)
+        self.ff = _FF(layers)
+        self.register_buffer("modulation", modulation.contiguous(), persistent=True)
+
+    def linears(self) -> dict[str, nn.Module]:
+        a, f = self.attn, self.ff
+        return {"attn.to_q": a.to_q, "attn.to_k": a.to_k, "attn.to_v": a.to_v, "attn.to_gate": a.to_gate,
+                "attn.to_out.0": a.to_out[0], "ff.gate": f.gate, "ff.up": f.up, "ff.down": f.down}
+
+    def forward(self, x: Tensor, cos: Tensor, sin: Tensor, linear: LinearFn = _module_linear,
+                modulation: Optional[Tensor] = None) -> Tensor:
+        """x [T, hidden] -> [T, hidden].  ``linear(name, module, input)`` evaluates a quantized
+        linear (default: the module itself); ``modulation`` overrides the block's buffer (a
+        reference evaluation on another device passes its own copy)."""
+        d = self.dims
+        mod = self.modulation if modulation is None else modulation
+        shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = (m.to(x.dtype) for m in mod)
+        lin = self.linears()
+        t = x.shape[0]
+
+        h = rms_norm(x) * (1 + scale_a) + shift_a
+        q = linear("attn.to_q", lin["attn.to_q"], h).view(t, d.heads, d.head_dim)
+        k = linear("attn.to_k", lin["attn.to_k"], h).view(t, d.kv_heads, d.head_dim)
+        v = linear("attn.to_v", lin["attn.to_v"], h).view(t, d.kv_heads, d.head_dim)
+        q = apply_rope(rms_norm(q), cos, sin)
+        k = apply_rope(rms_norm(k), cos, sin)
+        a = attention(q, k, v)                                   # [T, heads * head_dim]
+        a = a * torch.sigmoid(linear("attn.to_gate", lin["attn.to_gate"], h))
+        x = x + gate_a * linear("attn.to_out.0", lin["attn.to_out.0"], a)
+
+        h = rms_norm(x) * (1 + scale_f) + shift_f
+        f = F.silu(linear("ff.gate", lin["ff.gate"], h)) * linear("ff.up", lin["ff.up"], h)
+        return x + gate_f * linear("ff.down", lin["ff.down"], f)
+
+
+def attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """Softmax attention of q [T, H, d] over k, v [T, Hkv, d] (H a multiple of Hkv) -> [T, H*d].
+
+    On the GPU only the fused SDPA kernels are allowed (flash / memory-efficient); the math
+    path's batched products on transposed bf16 views are kept out.  Elsewhere (the CPU
+    reference evaluation) SDPA picks its own path.
+    """
+    t, heads, dh = q.shape
+    qh, kh, vh = (z.transpose(0, 1).unsqueeze(0) for z in (q, k, v))
+    if q.is_cuda:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            o = F.scaled_dot_product_attention(qh, kh, vh, enable_gqa=True)
+    else:
+        o = F.scaled_dot_product_attention(qh, kh, vh, enable_gqa=True)
+    return o.squeeze(0).transpose(0, 1).reshape(t, heads * dh)
+
+
+class Krea2StandInTransformer(nn.Module):
+    """``transformer_blocks`` of stand-in blocks; ``forward`` is one pass of the denoiser."""
+
+    def __init__(self, dims: Krea2Dims, blocks: list[Krea2StandInBlock]):
+        super().__init__()
+        self.dims = dims
+        self.transformer_blocks = nn.ModuleList(blocks)
+
+    @classmethod
+    def random(cls, dims: Krea2Dims = Krea2Dims(), *, rank: int = 32, group_size: int = 64,
+               backend: str = "hip_gfx950", device: torch.device | str = "cuda", seed: int = 0
+               ) -> "Krea2StandInTransformer":
+        """Random-init model with every quantized linear resident on ``device``."""
+        dev = torch.device(device)
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        blocks = []
+        for _ in range(dims.layers):
+            layers = {name: SVDQuantLinear(random_quantized_state(n, k, rank=rank, group_size=group_size,
+                                                                  device=dev, generator=gen), backend=backend)
+                      for name, (n, k) in dims.linear_shapes().items()}
+            mod = torch.randn(6, dims.hidden, device=dev, generator=gen) * 0.1
+            mod[2] = mod[2].abs() + 0.2   # attention gate
+            mod[5] = mod[5].abs() + 0.2   # MLP gate
+            blocks.append(Krea2StandInBlock(dims, layers, mod.to(torch.bfloat16)))
+        return cls(dims, blocks)
+
+    def forward(self, tokens: Tensor, linear: LinearFn = _module_linear) -> Tensor:
+        """tokens [T, hidden] -> [T, hidden] through every block."""
+        cos, sin = rope_tables(tokens.shape[0], self.dims.head_dim, tokens.device, tokens.dtype)
+        x = tokens
+        for blk in self.transformer_blocks:
+            x = blk(x, cos, sin, linear)
+        return x
+
+    def denoise_step(self, text: Tensor, latent: Tensor, dt: float) -> Tensor:
+        """One Euler step of the flow: the denoiser over [text | latent], then
+        ``latent + dt * velocity`` for the latent tokens."""
+        out = self.forward(torch.cat([text, latent], dim=0))
+        return latent + dt * out[text.shape[0]:]

@@ -1,0 +1,62 @@
+"""CPU checks of the stand-in Krea-2 denoiser's glue (no kernel calls)."""
+import math
+
+import pytest
+import torch
+
+from krea2_svdquant_amd.runtime import krea2_standin as ks
+
+
+def test_dims_match_reference_readme():
+    # README.md:27-37 of the reference: 28 layers, hidden 6144, 48 heads, 12 kv heads, d 128, MLP 16384
+    d = ks.Krea2Dims()
+    assert (d.layers, d.hidden, d.heads, d.kv_heads, d.head_dim, d.mlp) == (28, 6144, 48, 12, 128, 16384)
+    shapes = d.linear_shapes()
+    assert shapes["attn.to_q"] == (6144, 6144) and shapes["attn.to_k"] == (1536, 6144)
+    assert shapes["ff.up"] == (16384, 6144) and shapes["ff.down"] == (6144, 16384)
+    assert tuple(shapes) == ks.LINEAR_NAMES
+
+
+def test_random_state_layout_and_module_names():
+    from krea2_svdquant_amd.config import SVDQuantConfig
+    from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
+    dims = ks.Krea2Dims(layers=2, hidden=256, heads=2, kv_heads=1, head_dim=128, mlp=512)
+    model = ks.Krea2StandInTransformer.random(dims, device="cpu", seed=1)
+    names = [n for n, m in model.named_modules() if isinstance(m, SVDQuantLinear)]
+    assert names == [f"transformer_blocks.{i}.{t}" for i in range(2) for t in SVDQuantConfig().target_modules]
+    st = model.transformer_blocks[1].ff.down.state
+    assert st.qweight.dtype == torch.uint8 and tuple(st.qweight.shape) == (256, 256)
+    assert st.weight_scales.dtype == torch.float16 and tuple(st.weight_scales.shape) == (256, 8)
+    assert tuple(st.l1.shape) == (256, 32) and tuple(st.l2.shape) == (32, 512)
+    assert st.smooth_scale.dtype == torch.bfloat16 and float(st.smooth_scale.float().min()) >= 1.0
+
+
+def test_rope_is_a_rotation_of_each_pair():
+    cos, sin = ks.rope_tables(17, 128, "cpu", torch.float64)
+    t = torch.randn(17, 3, 128, dtype=torch.float64)
+    r = ks.apply_rope(t, cos, sin)
+    # pairs (j, j + 64) rotate by the same angle: their norms are kept, position 0 is the identity
+    pn = lambda z: z[..., :64] ** 2 + z[..., 64:] ** 2  # noqa: E731
+    assert torch.allclose(pn(r), pn(t))
+    assert torch.equal(r[0], t[0])
+    ang = 5 * 10000.0 ** (-2 * 3 / 128)
+    assert math.isclose(float(r[5, 0, 3]), float(t[5, 0, 3]) * math.cos(ang) - float(t[5, 0, 67]) * math.sin(ang),
+                        rel_tol=1e-5, abs_tol=1e-6)
+
+
+def test_gqa_attention_equals_per_head_softmax():
+    torch.manual_seed(0)
+    q = torch.randn(9, 4, 16, dtype=torch.float64)
+    k = torch.randn(9, 2, 16, dtype=torch.float64)
+    v = torch.randn(9, 2, 16, dtype=torch.float64)
+    out = ks.attention(q, k, v)
+    for h in range(4):
+        kv = h // 2          # heads share KV heads in contiguous groups
+        w = torch.softmax(q[:, h] @ k[:, kv].T / 4.0, dim=-1)
+        assert torch.allclose(out[:, 16 * h:16 * (h + 1)], w @ v[:, kv])
+
+
+def test_block_rejects_wrong_linear_set():
+    dims = ks.Krea2Dims(layers=1, hidden=256, heads=2, kv_heads=1, head_dim=128, mlp=512)
+    with pytest.raises(ValueError):
+        ks.Krea2StandInBlock(dims, {"attn.to_q": torch.nn.Identity()}, torch.zeros(6, 256))
