@@ -31,48 +31,57 @@ constexpr float kRcp7 = 0.142857149f;               // RN(1/7)
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// x_hat = bf16(x / s) for the lane's row over 64 columns (8 chunks of 8), plus its absmax.
-// EXACT selects IEEE division; otherwise the reciprocal-corrected division (div_rcp), exact
-// while quotients are normal floats.  `range_bad` flags a nonzero x whose quotient left
-// [2^-90, 2^100].  SIGNED_ZERO restores the sign of a zero quotient (-0 / s), which the
-// correction step loses; only x_hat itself needs it.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2 as_u16x2(uint32_t v) { return __builtin_bit_cast(u16x2, v); }
+
 // The scale vectors are read through the constant address space: they are read-only while
 // the kernel runs, the addresses are wave-uniform, so they become scalar loads and SGPR
 // operands instead of per-lane vector loads.
 typedef const __attribute__((address_space(4))) float* cfloat_ptr;
 
-template <bool EXACT, bool SIGNED_ZERO>
-__device__ __forceinline__ void smooth64(const u32x4 (&xr)[8], cfloat_ptr sv, cfloat_ptr rv, u32x4 (&xh)[8],
-                                         float& am, bool& range_bad) {
-  bool bad = false;
+// x_hat = bf16(RN(x * RN(1/s))) for the lane's row over 64 columns.  This equals the reference's
+// bf16(x / s) (float32 division, then bf16) whenever the quotient lies in [2^-90, 2^100] and
+// RN(1/s) is finite: x and s carry 8 significant bits, so x / s is never a bf16 rounding midpoint
+// and stays at least 2^-17 (relative) away from one, while the product is within 2^-23 of x / s
+// (exhaustive check over every bf16 pair: tests/native/smooth_exhaustive.c).  Signed zeros
+// come out as IEEE division gives them.
+// amx: packed maximum of the |x_hat| bit patterns (inf and NaN compare largest, so a quotient
+// the product cannot represent always shows in the group maximum).  XHAT callers also get the
+// packed maximum of the |x| bit patterns and the minimum of |x| - 1 (a zero wraps to 0xFFFF and
+// drops out), for the range test of every element.
+template <bool XHAT>
+__device__ __forceinline__ void smooth64_fast(const u32x4 (&xr)[8], cfloat_ptr rv, u32x4 (&xh)[8], u16x2& amx,
+                                              u16x2& xmx, u16x2& xmn) {
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint32_t d = xr[c][e];
-      const float s0 = sv[8 * c + 2 * e], s1 = sv[8 * c + 2 * e + 1];
-      const float xa = bf16lo(d), xb = bf16hi(d);
-      float qa, qb;
-      if (EXACT) {
-        qa = xa / s0;
-        qb = xb / s1;
-      } else {
-        qa = div_rcp(xa, s0, rv[8 * c + 2 * e]);
-        qb = div_rcp(xb, s1, rv[8 * c + 2 * e + 1]);
-        const bool ba = !(fabsf(qa) >= 0x1p-90f && fabsf(qa) <= 0x1p100f) && xa != 0.0f;
-        const bool bb = !(fabsf(qb) >= 0x1p-90f && fabsf(qb) <= 0x1p100f) && xb != 0.0f;
-        bad = bad || ba || bb;
-        if (SIGNED_ZERO) {
-          qa = __builtin_copysignf(qa, __uint_as_float(__float_as_uint(xa) ^ (__float_as_uint(s0) & 0x80000000u)));
-          qb = __builtin_copysignf(qb, __uint_as_float(__float_as_uint(xb) ^ (__float_as_uint(s1) & 0x80000000u)));
-        }
+      const uint32_t pk = pack_bf16x2(bf16lo(d) * rv[8 * c + 2 * e], bf16hi(d) * rv[8 * c + 2 * e + 1]);
+      xh[c][e] = pk;
+      amx = __builtin_elementwise_max(amx, as_u16x2(pk & 0x7FFF7FFFu));
+      if (XHAT) {
+        const u16x2 ax = as_u16x2(d & 0x7FFF7FFFu);
+        xmx = __builtin_elementwise_max(xmx, ax);
+        xmn = __builtin_elementwise_min(xmn, ax - (u16x2){1, 1});
       }
-      const uint32_t pk = pack_bf16x2(qa, qb);
+    }
+  }
+}
+
+// IEEE division for a group the fast path does not cover (or SVDQ_ACT_EXACT_DIV); am = the
+// group's max |x_hat| as a float.
+__device__ __forceinline__ void smooth64_exact(const u32x4 (&xr)[8], cfloat_ptr sv, u32x4 (&xh)[8], float& am) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t d = xr[c][e];
+      const uint32_t pk = pack_bf16x2(bf16lo(d) / sv[8 * c + 2 * e], bf16hi(d) / sv[8 * c + 2 * e + 1]);
       xh[c][e] = pk;
       am = fmaxf(am, fmaxf(fabsf(bf16lo(pk)), fabsf(bf16hi(pk))));
     }
   }
-  range_bad = bad;
 }
 
 // OPER: GEMM operand codes written (0 none, 1 e4m3, 2 int8 16*q, 3 e3m2 planar).  The e3m2 layout
@@ -116,24 +125,38 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) xr[b][c] = ld16(p.x + rowc * p.ldx + g * G + 64 * b + 8 * c);
 
-    float am = 0.0f;
-    bool bad = false;
+    u16x2 amx = {0, 0}, xmx = {0, 0}, xmn = {0xFFFF, 0xFFFF};
 #pragma unroll
-    for (int b = 0; b < HB; ++b) {
-      bool bb;
-      smooth64<false, XHAT>(xr[b], sv + g * G + 64 * b, rv + g * G + 64 * b, xh[b], am, bb);
-      bad = bad || bb;
+    for (int b = 0; b < HB; ++b) smooth64_fast<XHAT>(xr[b], rv + g * G + 64 * b, xh[b], amx, xmx, xmn);
+    const uint32_t amb = amx[0] > amx[1] ? amx[0] : amx[1];
+    float am = bf16f((uint16_t)amb);
+    bool bad;
+    if (XHAT) {
+      // x_hat needs every element exact: every nonzero quotient inside [2^-90, 2^100] (bounded by
+      // the row's |x| range over the group's |s| range) and every s normal, so RN(1/s) is finite.
+      // The s bit patterns are wave-uniform: scalar minimum / maximum.
+      uint32_t smn = 0xFFFFFFFFu, smx = 0u;
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        const uint32_t sb = __float_as_uint(sv[g * G + j]) & 0x7FFFFFFFu;
+        smn = min(smn, sb);
+        smx = max(smx, sb);
+      }
+      const uint32_t xm1 = xmn[0] < xmn[1] ? xmn[0] : xmn[1];   // 0xFFFF: no nonzero element
+      const float xmax = bf16f(xmx[0] > xmx[1] ? xmx[0] : xmx[1]), xmin = bf16f((uint16_t)(xm1 + 1));
+      bad = smn < 0x00800000u || smx > 0x7F800000u ||
+            (xm1 != 0xFFFFu && !(xmin >= 0x1p-90f * __uint_as_float(smx) && xmax <= 0x1p100f * __uint_as_float(smn)));
+    } else {
+      // Only codes and scales are written: they follow from the group absmax and, per element,
+      // from the element's own quotient.  With the absmax inside [2^-90, 2^100] no quotient
+      // leaves the range from above, and one below the normal range (< 2^-126, the only inexact
+      // case) is under 2^-33 of the scale, so its code is 0 either way.
+      bad = amb != 0u && !(am >= 0x1p-90f && am <= 0x1p100f);
     }
-    // Codes and scales only depend on elements within 2^-4 of the group absmax, so an absmax
-    // inside [2^-90, 2^100] keeps them exact; x_hat itself needs every element.
-    if (!XHAT) bad = am != 0.0f && !(am >= 0x1p-90f && am <= 0x1p100f);
     if (p.exact || __any(bad)) {
       am = 0.0f;
 #pragma unroll
-      for (int b = 0; b < HB; ++b) {
-        bool unused;
-        smooth64<true, XHAT>(xr[b], sv + g * G + 64 * b, rv + g * G + 64 * b, xh[b], am, unused);
-      }
+      for (int b = 0; b < HB; ++b) smooth64_exact(xr[b], sv + g * G + 64 * b, xh[b], am);
     }
 
     if (QUANT) {
