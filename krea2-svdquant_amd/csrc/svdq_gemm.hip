@@ -22,10 +22,12 @@
 namespace svdq {
 namespace {
 
-constexpr int BM = 128, BN = 128, NTHR = 256;
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+// byte E of v as a float (one v_cvt_f32_ubyteE)
+template <int E>
+__device__ __forceinline__ float ubyte_f32(uint32_t v) { return (float)((v >> (8 * E)) & 0xFFu); }
 
 
 
@@ -907,68 +909,119 @@ __global__ void weight_scale_pairs_kernel(const uint16_t* __restrict__ sw, uint3
 }
 
 // --------------------------------------------------------------------------- W4A16
-template <int G, bool OUT_F32>
-__global__ void __launch_bounds__(NTHR) w4a16_kernel(GemmParams p) {
-  constexpr int ROWH = 2 * G + 16;            // LDS bytes per bf16 row (padded)
-  constexpr int ALPR = 2 * G / 16;            // 16-byte loads per A row per stage
-  constexpr int ALPT = BM * ALPR / NTHR;      // A loads per thread
-  constexpr int BLPR = G / 32;                // 16-byte packed loads per B row
-  constexpr int BLPT = BN * BLPR / NTHR;      // B loads per thread
-  constexpr int KS = G / 16;                  // K=16 MFMA steps per group
-  __shared__ __attribute__((aligned(16))) uint8_t sA[2][BM * ROWH];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[2][BN * ROWH];
+// The reference pytorch_sim math on the bf16 MFMA: y = x_hat @ W^T with W = bf16(q * bf16(sw))
+// (quant/svd.py:119-163, dequantization pack.py:26-44 in bf16), plus the low-rank epilogue.
+//
+// Block tile (64 WM) x 128: WM x 2 waves, wave tile 64 x 64 = 2 x 2 sub-tiles of 32 x 32 on
+// v_mfma_f32_32x32x16_bf16.  A stage is 64 columns of K (one k-group for G = 64, half of one for
+// G = 128), double-buffered in LDS: the next stage's x_hat rows (16 bytes per thread and load,
+// 8 threads per 128-byte row segment) and packed weight codes (8 bytes = 16 codes per thread)
+// are loaded into registers three stages ahead (a ring of three register sets), then written to
+// the other buffer one stage ahead -- the weights dequantized on the way (v_cvt_f32_ubyte + one exact FMA per code +
+// RNE pack) -- with one barrier per stage.  LDS rows are 64 bf16 plus 16 bytes of padding (144-byte
+// pitch): the fragment reads (16 lanes on 16 consecutive rows) and the staging writes hit
+// distinct bank groups.
+template <int G, int WM, bool OUT_F32>
+__global__ void __launch_bounds__(WM * 128, 1) w4a16_kernel(GemmParams p) {
+  constexpr int NT = WM * 128;                // threads
+  constexpr int TBM = 64 * WM, TBN = 128, KB = 64;
+  constexpr int PITCH = 2 * KB + 16;          // LDS bytes per row
+  constexpr int ALD = TBM * 8 / NT;           // 16-byte A loads per thread and stage (= 4)
+  constexpr int BROWS = NT / 4;               // weight rows staged per pass (4 threads per row)
+  constexpr int BLD = TBN / BROWS;            // weight passes per stage (1 or 2)
+  static_assert(ALD * NT == TBM * 8 && BLD * BROWS == TBN, "staging split");
+  __shared__ __attribute__((aligned(16))) uint8_t sA[2][TBM * PITCH];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[2][TBN * PITCH];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int nbm = (p.M + BM - 1) / BM, nbn = (p.N + BN - 1) / BN;
+  const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
   int bm, bn;
-  tile_coords(blockIdx.x, nbm, nbn, 8, bm, bn);
-  const int m0 = bm * BM, n0 = bn * BN;
-  const int K = p.K, ngroups = K / G, kp = K / 2;
+  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
+  const int m0 = bm * TBM, n0 = bn * TBN;
+  const int K = p.K, ngroups = K / G, kp = K / 2, nst = K / KB;
 
-  u32x4 ra[ALPT], rb[BLPT];
-  float wsc[BLPT];
+  // staging assignments: A chunk (row, 16-byte chunk) = (idx / 8, idx % 8), idx = tid + NT * i;
+  // weights: row tid / 4 (+ BROWS per pass), 16 codes = chunks 2 (tid % 4) and 2 (tid % 4) + 1
+  const uint16_t* arow[ALD];
+  int aoff[ALD];
+#pragma unroll
+  for (int i = 0; i < ALD; ++i) {
+    const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
+    arow[i] = p.xhat + (long)min(m0 + r, p.M - 1) * p.ldxh + 8 * c;
+    aoff[i] = r * PITCH + 16 * c;
+  }
+  const int bq = tid & 3;
+  const uint8_t* brow[BLD];
+  const uint16_t* bsc[BLD];
+  int boff[BLD];
+#pragma unroll
+  for (int i = 0; i < BLD; ++i) {
+    const int r = (tid >> 2) + BROWS * i, n = min(n0 + r, p.N - 1);
+    brow[i] = p.qw + (long)n * kp + 8 * bq;
+    bsc[i] = p.sw + (long)n * ngroups;
+    boff[i] = r * PITCH + 32 * bq;
+  }
 
-  auto gload = [&](int g) {
+  // D register sets: stage s + D is loaded at the start of stage s (three stages of MFMA work
+  // cover the load latency); set q holds the stages s with s % D == q.  The loads are issued as
+  // inline asm and waited for explicitly: every stage issues the same LPS loads (past the last
+  // stage they re-read it), so before stage s + 1 is stored exactly the 2 LPS loads of the two
+  // newer sets may still be in flight.  (Left to the compiler, its wait analysis lost track of the
+  // sets across the loop and drained every load before each store.)
+  constexpr int D = 3;
+  constexpr int LPS = ALD + 2 * BLD;          // loads per stage and thread
+  u32x4 ra[D][ALD];
+  u32x2 rb[D][BLD];
+  uint32_t rs[D][BLD];                        // fp16 scale bits
+  auto gload_set = [&](int st, u32x4 (&da)[ALD], u32x2 (&db)[BLD], uint32_t (&ds)[BLD]) {
+    const int k0 = st * KB;
 #pragma unroll
-    for (int i = 0; i < ALPT; ++i) {
-      const int idx = tid + NTHR * i, row = idx / ALPR, part = idx % ALPR;
-      ra[i] = ld16(p.xhat + (long)min(m0 + row, p.M - 1) * p.ldxh + g * G + 8 * part);
-    }
+    for (int i = 0; i < ALD; ++i)
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(da[i]) : "v"(arow[i] + k0) : "memory");
 #pragma unroll
-    for (int i = 0; i < BLPT; ++i) {
-      const int idx = tid + NTHR * i, row = idx / BLPR, part = idx % BLPR;
-      const int n = min(n0 + row, p.N - 1);
-      rb[i] = ld16(p.qw + (long)n * kp + g * (G / 2) + 16 * part);
-      wsc[i] = round_bf16(half_bits_to_float(p.sw[(long)n * ngroups + g]));
+    for (int i = 0; i < BLD; ++i) {
+      asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(db[i]) : "v"(brow[i] + k0 / 2) : "memory");
+      asm volatile("global_load_ushort %0, %1, off" : "=v"(ds[i]) : "v"(bsc[i] + k0 / G) : "memory");
     }
   };
-  auto lstore = [&](int buf) {
+  auto gload = [&](int st, auto q_c) {
+    constexpr int q = decltype(q_c)::value;
+    gload_set(st, ra[q], rb[q], rs[q]);
+  };
+  // a set landed: at most the two newer sets' loads (issued after it) still in flight
+  auto wait_regs = [&](u32x4 (&da)[ALD], u32x2 (&db)[BLD], uint32_t (&ds)[BLD]) {
+    static_assert(2 * LPS < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%c0)" ::"i"(2 * LPS) : "memory");
 #pragma unroll
-    for (int i = 0; i < ALPT; ++i) {
-      const int idx = tid + NTHR * i, row = idx / ALPR, part = idx % ALPR;
-      st16(&sA[buf][row * ROWH + 16 * part], ra[i]);
-    }
+    for (int i = 0; i < ALD; ++i) asm volatile("" : "+v"(da[i]));
 #pragma unroll
-    for (int i = 0; i < BLPT; ++i) {
-      const int idx = tid + NTHR * i, row = idx / BLPR, part = idx % BLPR;
-      const float s = wsc[i], ns8 = -8.0f * s;
-      uint32_t o[16];
+    for (int i = 0; i < BLD; ++i) asm volatile("" : "+v"(db[i]), "+v"(ds[i]));
+  };
+  auto wait_set = [&](auto q_c) {
+    constexpr int q = decltype(q_c)::value;
+    wait_regs(ra[q], rb[q], rs[q]);
+  };
+  // bf16(q * s), q = nibble - 8: nibble * s and 8 s are exact, so one FMA gives q * s exactly
+  auto lstore = [&](int buf, auto q_c) {
+    constexpr int q = decltype(q_c)::value;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t v = rb[i][d];
+    for (int i = 0; i < ALD; ++i) *reinterpret_cast<u32x4*>(&sA[buf][aoff[i]]) = ra[q][i];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float w0 = __builtin_fmaf((float)((v >> (8 * e)) & 0xFu), s, ns8);
-          const float w1 = __builtin_fmaf((float)((v >> (8 * e + 4)) & 0xFu), s, ns8);
-          o[4 * d + e] = pack_bf16x2(w0, w1);
-        }
+    for (int i = 0; i < BLD; ++i) {
+      const float sc = round_bf16(half_bits_to_float((uint16_t)rs[q][i])), ns8 = -8.0f * sc;   // bf16 scale, as the sim
+      uint32_t o[8];
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const uint32_t v = rb[q][i][d], lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+        o[4 * d + 0] = pack_bf16x2(__builtin_fmaf(ubyte_f32<0>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<0>(hi), sc, ns8));
+        o[4 * d + 1] = pack_bf16x2(__builtin_fmaf(ubyte_f32<1>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<1>(hi), sc, ns8));
+        o[4 * d + 2] = pack_bf16x2(__builtin_fmaf(ubyte_f32<2>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<2>(hi), sc, ns8));
+        o[4 * d + 3] = pack_bf16x2(__builtin_fmaf(ubyte_f32<3>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<3>(hi), sc, ns8));
       }
-      uint8_t* dst = &sB[buf][row * ROWH + 64 * part];
-      st16(dst, u32x4{o[0], o[1], o[2], o[3]});
-      st16(dst + 16, u32x4{o[4], o[5], o[6], o[7]});
-      st16(dst + 32, u32x4{o[8], o[9], o[10], o[11]});
-      st16(dst + 48, u32x4{o[12], o[13], o[14], o[15]});
+      *reinterpret_cast<u32x4*>(&sB[buf][boff[i]]) = u32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<u32x4*>(&sB[buf][boff[i] + 16]) = u32x4{o[4], o[5], o[6], o[7]};
     }
   };
 
@@ -978,30 +1031,63 @@ __global__ void __launch_bounds__(NTHR) w4a16_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  gload(0);
-  lstore(0);
+  const int ra0 = (64 * wm + lr) * PITCH + 16 * h, rb0 = (64 * wn + lr) * PITCH + 16 * h;
+  using Q0 = std::integral_constant<int, 0>;
+  using Q1 = std::integral_constant<int, 1>;
+  using Q2 = std::integral_constant<int, 2>;
+  // Loads past the last stage re-read it (clamped index) and the last stage's store fills the
+  // unused buffer, so the main loop is branch-free: the compiler then counts exactly which loads
+  // are still in flight at each LDS store (a guarded body made it wait for all of them).
+  gload(0, Q0{});
+  gload(min(1, nst - 1), Q1{});
+  gload(min(2, nst - 1), Q2{});
+  wait_set(Q0{});
+  lstore(0, Q0{});
   __syncthreads();
-
-  for (int g = 0; g < ngroups; ++g) {
-    const int buf = g & 1;
-    if (g + 1 < ngroups) gload(g + 1);
+  // stage st: its data is in LDS buffer st % 2; set q (= st % D) is free, so stage st + D goes
+  // out into it; then stage st + 1 moves from its set into the other buffer.  The main loop is
+  // branch-free (clamped loads, and the last stage's store fills the unused buffer).
+  auto stage = [&](int st, auto q_c) {
+    constexpr int q = decltype(q_c)::value;
+    using QN = std::integral_constant<int, (q + 1) % D>;
+    const int buf = st & 1;
+    gload(min(st + D, nst - 1), q_c);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+    for (int ks = 0; ks < KB / 16; ++ks) {
       u32x4 a[2], b[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) a[i] = ld16(&sA[buf][(64 * wm + 32 * i + lr) * ROWH + 32 * ks + 16 * h]);
+      for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const u32x4*>(&sA[buf][ra0 + 32 * i * PITCH + 32 * ks]);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) b[j] = ld16(&sB[buf][(64 * wn + 32 * j + lr) * ROWH + 32 * ks + 16 * h]);
+      for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const u32x4*>(&sB[buf][rb0 + 32 * j * PITCH + 32 * ks]);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16_32x32x16(a[i], b[j], acc[i][j]);
     }
-    if (g + 1 < ngroups) lstore(buf ^ 1);
+    wait_set(QN{});     // sets q + 2 (stage st + 2) and q (stage st + 3) may still be in flight
+    lstore(buf ^ 1, QN{});
     __syncthreads();
+  };
+  int st = 0;
+  for (; st + D <= nst; st += D) {
+    stage(st, Q0{});
+    stage(st + 1, Q1{});
+    stage(st + 2, Q2{});
   }
-
-  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, nullptr);
+  if (st < nst) stage(st, Q0{});
+  if (st + 1 < nst) stage(st + 1, Q1{});
+  // The re-reads past the last stage are never stored: wait for them and mark every set as used
+  // after the wait, so that no register of an in-flight load is handed to other values before.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int q = 0; q < D; ++q) {
+#pragma unroll
+    for (int i = 0; i < ALD; ++i) asm volatile("" ::"v"(ra[q][i]));
+#pragma unroll
+    for (int i = 0; i < BLD; ++i) asm volatile("" ::"v"(rb[q][i]), "v"(rs[q][i]));
+  }
+  // the last barrier passed: every wave is done with the A buffers, which now stage the output
+  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sA[0][0] + wave * 4096);
 }
 
 }  // namespace
@@ -1062,17 +1148,23 @@ hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, 
 }
 
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st) {
-  const dim3 grid(((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN));
-  if (G == 64) {
-    if (out_f32) w4a16_kernel<64, true><<<grid, NTHR, 0, st>>>(p);
-    else w4a16_kernel<64, false><<<grid, NTHR, 0, st>>>(p);
-  } else if (G == 128) {
-    if (out_f32) w4a16_kernel<128, true><<<grid, NTHR, 0, st>>>(p);
-    else w4a16_kernel<128, false><<<grid, NTHR, 0, st>>>(p);
-  } else {
-    return hipErrorInvalidValue;
+  // 256-row tiles (8 waves) when they fill the chip, 128-row tiles (4 waves) otherwise
+  const long tiles256 = (long)((p.M + 255) / 256) * ((p.N + 127) / 128);
+  const bool big = tiles256 >= 256;
+  const int tbm = big ? 256 : 128;
+  const dim3 grid(((p.M + tbm - 1) / tbm) * ((p.N + 127) / 128));
+#define SVDQ_W4A16(GG, WW)                                                                 \
+  if (G == GG && (WW == 4) == big) {                                                      \
+    if (out_f32) w4a16_kernel<GG, WW, true><<<grid, WW * 128, 0, st>>>(p);                 \
+    else w4a16_kernel<GG, WW, false><<<grid, WW * 128, 0, st>>>(p);                        \
+    return hipGetLastError();                                                             \
   }
-  return hipGetLastError();
+  SVDQ_W4A16(64, 4)
+  SVDQ_W4A16(64, 2)
+  SVDQ_W4A16(128, 4)
+  SVDQ_W4A16(128, 2)
+#undef SVDQ_W4A16
+  return hipErrorInvalidValue;
 }
 
 }  // namespace svdq
