@@ -1090,6 +1090,154 @@ __global__ void __launch_bounds__(WM * 128, 1) w4a16_kernel(GemmParams p) {
   epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sA[0][0] + wave * 4096);
 }
 
+// W4A16 on large grids: one wave per SIMD with a 128 x 128 register tile (4 x 4 sub-tiles of
+// 32 x 32; the accumulators live in AGPRs, only MFMAs touch them before the epilogue), block tile
+// 256 x 256 on 4 waves.  (Two waves per SIMD with 128 x 64 tiles measured the same or slower.)  Per 64-column stage a wave issues 64 MFMAs (2048 cycles of the SIMD's
+// MFMA pipe) and, spread between them, its share of the next stage: 8 x_hat chunks and one weight
+// row (64 codes dequantized as in w4a16_kernel) written to the other LDS buffer, so one instruction
+// stream keeps the MFMA pipe, the VALU and the LDS busy together.  Loads run two stages ahead with
+// the same exact-count asm waits; LDS rows have the 144-byte pitch of w4a16_kernel.
+template <int G, bool OUT_F32>
+__global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
+  constexpr int NT = 256, TBM = 256, TBN = 256, KB = 64;
+  constexpr int PITCH = 2 * KB + 16;
+  constexpr int ALD = TBM * 8 / NT;           // 8 x_hat chunks per thread and stage
+  constexpr int LPS = ALD + 3;                // + two 16-byte weight loads + one scale
+  constexpr int D = 2;                        // register sets (stages in flight)
+  __shared__ __attribute__((aligned(16))) uint8_t sA[2][TBM * PITCH];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[2][TBN * PITCH];
+
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
+  int bm, bn;
+  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
+  const int m0 = bm * TBM, n0 = bn * TBN;
+  const int K = p.K, ngroups = K / G, kp = K / 2, nst = K / KB;
+
+  const uint16_t* arow[ALD];
+  int aoff[ALD];
+#pragma unroll
+  for (int i = 0; i < ALD; ++i) {
+    const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
+    arow[i] = p.xhat + (long)min(m0 + r, p.M - 1) * p.ldxh + 8 * c;
+    aoff[i] = r * PITCH + 16 * c;
+  }
+  const int nrow = min(n0 + tid, p.N - 1);     // weight row of this thread
+  const uint8_t* brow = p.qw + (long)nrow * kp;
+  const uint16_t* bsc = p.sw + (long)nrow * ngroups;
+  const int boff = tid * PITCH;
+
+  u32x4 ra[D][ALD], rb[D][2];
+  uint32_t rs[D];
+  auto gload_set = [&](int st, u32x4 (&da)[ALD], u32x4 (&db)[2], uint32_t& ds) {
+    const int k0 = st * KB;
+#pragma unroll
+    for (int i = 0; i < ALD; ++i)
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(da[i]) : "v"(arow[i] + k0) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(db[0]) : "v"(brow + k0 / 2) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(db[1]) : "v"(brow + k0 / 2 + 16) : "memory");
+    asm volatile("global_load_ushort %0, %1, off" : "=v"(ds) : "v"(bsc + k0 / G) : "memory");
+  };
+  auto gload = [&](int st, auto q_c) {
+    constexpr int q = decltype(q_c)::value;
+    gload_set(st, ra[q], rb[q], rs[q]);
+  };
+  auto wait_regs = [&](u32x4 (&da)[ALD], u32x4 (&db)[2], uint32_t& ds) {
+    static_assert((D - 1) * LPS < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%c0)" ::"i"((D - 1) * LPS) : "memory");
+#pragma unroll
+    for (int i = 0; i < ALD; ++i) asm volatile("" : "+v"(da[i]));
+    asm volatile("" : "+v"(db[0]), "+v"(db[1]), "+v"(ds));
+  };
+  auto wait_set = [&](auto q_c) {
+    constexpr int q = decltype(q_c)::value;
+    wait_regs(ra[q], rb[q], rs[q]);
+  };
+  // part `pt` (0..3) of a set's move to LDS buffer buf: x_hat chunks 2 pt, 2 pt + 1 and the weight
+  // row's 16 codes of k 16 pt .. 16 pt + 15 (bf16(q * bf16(s)), one exact FMA per code)
+  auto lstore_part = [&](int buf, auto q_c, int pt) {
+    constexpr int q = decltype(q_c)::value;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&sA[buf][aoff[2 * pt + i]]) = ra[q][2 * pt + i];
+    const float sc = round_bf16(half_bits_to_float((uint16_t)rs[q])), ns8 = -8.0f * sc;
+    const u32x4 w = rb[q][pt >> 1];
+    uint32_t o[8];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const uint32_t v = w[2 * (pt & 1) + d], lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+      o[4 * d + 0] = pack_bf16x2(__builtin_fmaf(ubyte_f32<0>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<0>(hi), sc, ns8));
+      o[4 * d + 1] = pack_bf16x2(__builtin_fmaf(ubyte_f32<1>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<1>(hi), sc, ns8));
+      o[4 * d + 2] = pack_bf16x2(__builtin_fmaf(ubyte_f32<2>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<2>(hi), sc, ns8));
+      o[4 * d + 3] = pack_bf16x2(__builtin_fmaf(ubyte_f32<3>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<3>(hi), sc, ns8));
+    }
+    *reinterpret_cast<u32x4*>(&sB[buf][boff + 32 * pt]) = u32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<u32x4*>(&sB[buf][boff + 32 * pt + 16]) = u32x4{o[4], o[5], o[6], o[7]};
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  const int ra0 = (128 * wm + lr) * PITCH + 16 * h, rb0 = (128 * wn + lr) * PITCH + 16 * h;
+  using Q0 = std::integral_constant<int, 0>;
+  using Q1 = std::integral_constant<int, 1>;
+  gload(0, Q0{});
+  gload(min(1, nst - 1), Q1{});
+  wait_set(Q0{});
+#pragma unroll
+  for (int pt = 0; pt < 4; ++pt) lstore_part(0, Q0{}, pt);
+  __syncthreads();
+  // stage st (LDS buffer st % 2, set q = st % D): stage st + D goes out into set q; stage st + 1
+  // (set q + 1) moves to the other buffer, a quarter per k-step.
+  auto stage = [&](int st, auto q_c) {
+    constexpr int q = decltype(q_c)::value;
+    using QN = std::integral_constant<int, (q + 1) % D>;
+    const int buf = st & 1;
+    gload(min(st + D, nst - 1), q_c);   // set q was moved to LDS during the previous stage
+    wait_set(QN{});                      // set q + 1 landed; the D - 1 newer sets may be in flight
+#pragma unroll
+    for (int ks = 0; ks < KB / 16; ++ks) {
+      u32x4 a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const u32x4*>(&sA[buf][ra0 + 32 * i * PITCH + 32 * ks]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4*>(&sB[buf][rb0 + 32 * j * PITCH + 32 * ks]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16_32x32x16(a[i], b[j], acc[i][j]);
+      lstore_part(buf ^ 1, QN{}, ks);
+    }
+    __syncthreads();
+  };
+  int st = 0;
+  for (; st + D <= nst; st += D) {
+    stage(st, Q0{});
+    stage(st + 1, Q1{});
+  }
+  if (st < nst) stage(st, Q0{});
+  // the re-reads past the last stage are never stored: wait for them and mark every set used
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int q = 0; q < D; ++q) {
+#pragma unroll
+    for (int i = 0; i < ALD; ++i) asm volatile("" ::"v"(ra[q][i]));
+    asm volatile("" ::"v"(rb[q][0]), "v"(rb[q][1]), "v"(rs[q]));
+  }
+  // epilogue per 64 x 64 quadrant of the wave tile (the A buffers stage the output)
+#pragma unroll
+  for (int qi = 0; qi < 2; ++qi)
+#pragma unroll
+    for (int qj = 0; qj < 2; ++qj) {
+      f32x16 part[2][2] = {{acc[2 * qi][2 * qj], acc[2 * qi][2 * qj + 1]}, {acc[2 * qi + 1][2 * qj], acc[2 * qi + 1][2 * qj + 1]}};
+      epilogue<OUT_F32>(p, part, m0 + 128 * wm + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st) {
@@ -1148,21 +1296,31 @@ hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, 
 }
 
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st) {
-  // 256-row tiles (8 waves) when they fill the chip, 128-row tiles (4 waves) otherwise
-  const long tiles256 = (long)((p.M + 255) / 256) * ((p.N + 127) / 128);
-  const bool big = tiles256 >= 256;
-  const int tbm = big ? 256 : 128;
-  const dim3 grid(((p.M + tbm - 1) / tbm) * ((p.N + 127) / 128));
-#define SVDQ_W4A16(GG, WW)                                                                 \
-  if (G == GG && (WW == 4) == big) {                                                      \
-    if (out_f32) w4a16_kernel<GG, WW, true><<<grid, WW * 128, 0, st>>>(p);                 \
-    else w4a16_kernel<GG, WW, false><<<grid, WW * 128, 0, st>>>(p);                        \
+  // 256 x 256 tiles (one wave per SIMD) when they cover the chip at least half, else 128 x 128
+  // tiles (two workgroups of 4 waves per CU)
+  const long tiles_wide = (long)((p.M + 255) / 256) * ((p.N + 255) / 256);
+  if (tiles_wide >= 128) {
+    const dim3 grid((unsigned)tiles_wide);
+#define SVDQ_W4A16W(GG)                                                                    \
+  if (G == GG) {                                                                          \
+    if (out_f32) w4a16_wide_kernel<GG, true><<<grid, 256, 0, st>>>(p);                    \
+    else w4a16_wide_kernel<GG, false><<<grid, 256, 0, st>>>(p);                           \
     return hipGetLastError();                                                             \
   }
-  SVDQ_W4A16(64, 4)
-  SVDQ_W4A16(64, 2)
-  SVDQ_W4A16(128, 4)
-  SVDQ_W4A16(128, 2)
+    SVDQ_W4A16W(64)
+    SVDQ_W4A16W(128)
+#undef SVDQ_W4A16W
+    return hipErrorInvalidValue;
+  }
+  const dim3 grid(((p.M + 127) / 128) * ((p.N + 127) / 128));
+#define SVDQ_W4A16(GG)                                                                     \
+  if (G == GG) {                                                                          \
+    if (out_f32) w4a16_kernel<GG, 2, true><<<grid, 256, 0, st>>>(p);                       \
+    else w4a16_kernel<GG, 2, false><<<grid, 256, 0, st>>>(p);                              \
+    return hipGetLastError();                                                             \
+  }
+  SVDQ_W4A16(64)
+  SVDQ_W4A16(128)
 #undef SVDQ_W4A16
   return hipErrorInvalidValue;
 }

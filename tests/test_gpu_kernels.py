@@ -214,6 +214,17 @@ def test_layer_random_shapes(dev, m, n, k, g, r, rl, bias, mode):
     _check_layer(x, st, dev, mode, ref)
 
 
+@pytest.mark.parametrize("m,n,k,g,bias", [
+    (2304, 4096, 512, 64, False),    # 144 tiles of 256 x 256: the one-wave-per-SIMD W4A16 kernel
+    (2100, 4300, 576, 64, True),     # partial last tiles in M and N; 9 stages (odd: the tail stage)
+    (2048, 4352, 640, 128, False),   # group 128
+])
+def test_w4a16_wide_tiles(dev, m, n, k, g, bias):
+    x = synth.make_activation(m, k, seed=17)
+    st = synth.make_layer(n, k, x, rank=32, group_size=g, seed=18, bias=bias)
+    _check_layer(x, st, dev, "w4a16", sim.w4a16_eval(x, st)["y"])
+
+
 def test_outputs_deterministic(dev):
     x = synth.make_activation(300, 2048, seed=21)
     st = synth.make_layer(640, 2048, x, rank=32, group_size=64, seed=22, bias=True)
