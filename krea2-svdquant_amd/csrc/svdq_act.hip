@@ -90,7 +90,9 @@ __device__ __forceinline__ void smooth64_exact(const u32x4 (&xr)[8], cfloat_ptr 
 // (at byte 0), the last 8 in plane P[t][h][Rp][8] (at byte Rp K / 2) -- rows contiguous, so the
 // lanes (rows) of a wave store whole 1 KB / 512 B runs and the GEMM's DMA and LDS reads stream
 // whole planes.
-template <int G, int NT, int OPER, bool XHAT>
+// QX: the canonical packed codes may be requested (p.qx checked at run time); without it the
+// kernel carries no nibble-packing code at all.
+template <int G, int NT, int OPER, bool XHAT, bool QX>
 __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
   constexpr int HB = G / 64;             // 64-column blocks per group
   constexpr bool QUANT = OPER != 0;
@@ -118,12 +120,22 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[a][t] = f32x16{};
 
-  for (int g = gb + wave; g < ge; g += 4) {
-    u32x4 xr[HB][8], xh[HB][8];
+  // Without LoRA, x of the wave's next group is loaded into xr as soon as the current group's xr
+  // is dead (after the smoothing and its exact fallback): the loads overlap the quantization, the
+  // stores and the low-rank MFMAs with no extra registers.  With LoRA the raw x feeds the LoRA
+  // down projection, so each group is loaded when it starts.
+  constexpr bool LORA = NT > TR_MIN;
+  u32x4 xr[HB][8];
+  auto load_x = [&](int g) {
 #pragma unroll
     for (int b = 0; b < HB; ++b)
 #pragma unroll
       for (int c = 0; c < 8; ++c) xr[b][c] = ld16(p.x + rowc * p.ldx + g * G + 64 * b + 8 * c);
+  };
+  if (!LORA && gb + wave < ge) load_x(gb + wave);
+  for (int g = gb + wave; g < ge; g += 4) {
+    u32x4 xh[HB][8];
+    if (LORA) load_x(g);
 
     u16x2 amx = {0, 0}, xmx = {0, 0}, xmn = {0xFFFF, 0xFFFF};
 #pragma unroll
@@ -158,6 +170,7 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
 #pragma unroll
       for (int b = 0; b < HB; ++b) smooth64_exact(xr[b], sv + g * G + 64 * b, xh[b], am);
     }
+    if (!LORA && g + 4 < ge) load_x(g + 4);
 
     if (QUANT) {
       const float sc = round_bf16(div_rcp(fmaxf(am, kBf16OneEMinus8), 7.0f, kRcp7));
@@ -199,7 +212,7 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
               *reinterpret_cast<u32x2*>(p.qa + mp * (K / 2) + plane * 8) = u32x2{f[4], f[5]};
             }
           }
-          if (OPER == 2 || p.qx) {
+          if (OPER == 2 || (QX && p.qx)) {
             uint32_t w = 0;
 #pragma unroll
             for (int e = 0; e < 8; ++e) w |= (uint32_t)((int)t[e] + 8) << (4 * e);
@@ -218,7 +231,7 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(od + 16 * q) = op[q];
           }
-          if (p.qx) {
+          if (QX && p.qx) {
             uint8_t* dst = p.qx + rowc * (K / 2) + (g * G + 64 * b) / 2;
             *reinterpret_cast<u32x4*>(dst) = u32x4{nib[0], nib[1], nib[2], nib[3]};
             *reinterpret_cast<u32x4*>(dst + 16) = u32x4{nib[4], nib[5], nib[6], nib[7]};
@@ -351,13 +364,13 @@ __global__ void prepare_smooth_kernel(const uint16_t* __restrict__ s, float* __r
   }
 }
 
-template <int G, int OPER, bool XHAT>
+template <int G, int OPER, bool XHAT, bool QX>
 hipError_t launch_act_nt(const ActParams& p, int nt, dim3 grid, hipStream_t st) {
   switch (nt) {
-    case 1: act_kernel<G, 1, OPER, XHAT><<<grid, 256, 0, st>>>(p); break;
-    case 2: act_kernel<G, 2, OPER, XHAT><<<grid, 256, 0, st>>>(p); break;
-    case 3: act_kernel<G, 3, OPER, XHAT><<<grid, 256, 0, st>>>(p); break;
-    case 4: act_kernel<G, 4, OPER, XHAT><<<grid, 256, 0, st>>>(p); break;
+    case 1: act_kernel<G, 1, OPER, XHAT, QX><<<grid, 256, 0, st>>>(p); break;
+    case 2: act_kernel<G, 2, OPER, XHAT, QX><<<grid, 256, 0, st>>>(p); break;
+    case 3: act_kernel<G, 3, OPER, XHAT, QX><<<grid, 256, 0, st>>>(p); break;
+    case 4: act_kernel<G, 4, OPER, XHAT, QX><<<grid, 256, 0, st>>>(p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -365,11 +378,12 @@ hipError_t launch_act_nt(const ActParams& p, int nt, dim3 grid, hipStream_t st) 
 
 template <int G>
 hipError_t launch_act_g(const ActParams& p, int nt, int oper, bool xhat, dim3 grid, hipStream_t st) {
-  if (oper == 3 && !xhat) return launch_act_nt<G, 3, false>(p, nt, grid, st);
-  if (oper == 1 && !xhat) return launch_act_nt<G, 1, false>(p, nt, grid, st);
-  if (oper == 1 && xhat) return launch_act_nt<G, 1, true>(p, nt, grid, st);
-  if (oper == 2 && !xhat) return launch_act_nt<G, 2, false>(p, nt, grid, st);
-  if (oper == 0 && xhat) return launch_act_nt<G, 0, true>(p, nt, grid, st);
+  if (oper == 3 && !xhat && !p.qx) return launch_act_nt<G, 3, false, false>(p, nt, grid, st);
+  if (oper == 3 && !xhat) return launch_act_nt<G, 3, false, true>(p, nt, grid, st);
+  if (oper == 1 && !xhat) return launch_act_nt<G, 1, false, true>(p, nt, grid, st);
+  if (oper == 1 && xhat) return launch_act_nt<G, 1, true, true>(p, nt, grid, st);
+  if (oper == 2 && !xhat) return launch_act_nt<G, 2, false, true>(p, nt, grid, st);
+  if (oper == 0 && xhat) return launch_act_nt<G, 0, true, true>(p, nt, grid, st);
   return hipErrorInvalidValue;
 }
 

@@ -768,9 +768,13 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
             read_half_full(nbuf, 0, 0, 0, 0);
           }
         }
+        // the rescale FMAs at raised priority: they issue ahead of the other wave's fragment reads
+        // and DMA while its MFMAs run (2-3% on ff.up)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           rescale_acc(acc[i][j], P[j], S[j]);
+        __builtin_amdgcn_s_setprio(0);
       }
       if (!LASTST) {
         gAQ += stA * 16;
@@ -839,9 +843,11 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
           read_half(nbuf, 0, 0, 0, 0);
         }
       }
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         rescale_acc(acc[i][j], P[j], S[j]);
+      __builtin_amdgcn_s_setprio(0);
     }
   }
   }
