@@ -148,6 +148,33 @@ int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* 
                     const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group, void* y,
                     int64_t ldy, int out_f32, hipStream_t stream);
 
+/* Elementwise ops the GEMMs can apply to their bf16 output before the store (the `_epi` entry
+ * points).  With o = the bf16 layer output (the y above), a = aux[m][n] (bf16) and g = vec[n] (bf16);
+ * every step rounds to bf16 as the unfused torch op on bf16 tensors does. */
+#define SVDQ_EPI_NONE 0           /* y                                                      */
+#define SVDQ_EPI_MUL_SIGMOID 1    /* bf16(a * bf16(sigmoid(o)))   gated attention output    */
+#define SVDQ_EPI_SILU_MUL 2       /* bf16(bf16(silu(a)) * o)      SwiGLU, a = the gate      */
+#define SVDQ_EPI_RESIDUAL_GATE 3  /* bf16(a + bf16(g * o))        gated residual, a = x     */
+
+/* svdq_w4a4_gemm / svdq_w4a16_gemm with an elementwise op fused into the store.  No reference
+ * counterpart inside the reference: they fold the elementwise torch ops that a DiT block applies
+ * to a quantized linear's output (SwiGLU of ff.gate / ff.up, the sigmoid output gate of
+ * attention, the gated residual of to_out.0 and ff.down) into the GEMM's one bf16 store, for
+ * the callers around Krea2Transformer2DModel's linears (reference README.md:41-51 names them).
+ *   epi  : SVDQ_EPI_*; out_f32 must be 0 when epi != SVDQ_EPI_NONE
+ *   aux  : bf16 [M, ldaux], ldaux >= N (may not alias y); read by 16-byte loads when it is
+ *          16-byte aligned with ldaux % 8 == 0 (and vec 16-byte aligned), else per element
+ *   vec  : bf16 [N] (SVDQ_EPI_RESIDUAL_GATE only)
+ *   other arguments as in svdq_w4a4_gemm / svdq_w4a16_gemm. */
+int svdq_w4a4_gemm_epi(const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
+                       const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                       void* y, int64_t ldy, int out_f32, int epi, const void* aux, int64_t ldaux, const void* vec,
+                       hipStream_t stream);
+int svdq_w4a16_gemm_epi(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const void* mid,
+                        const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group, void* y,
+                        int64_t ldy, int out_f32, int epi, const void* aux, int64_t ldaux, const void* vec,
+                        hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

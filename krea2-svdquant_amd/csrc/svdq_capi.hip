@@ -188,12 +188,42 @@ int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int ope
                   "prepare_weight_operand");
 }
 
+static int epi_checks(const char* who, int epi, const void* aux, int64_t ldaux, const void* vec, int N,
+                      int out_f32) {
+  if (epi == SVDQ_EPI_NONE) return SVDQ_OK;
+  if (epi != SVDQ_EPI_MUL_SIGMOID && epi != SVDQ_EPI_SILU_MUL && epi != SVDQ_EPI_RESIDUAL_GATE)
+    return fail(SVDQ_ERR_ARG, "%s: epilogue op %d", who, epi);
+  if (out_f32) return fail(SVDQ_ERR_ARG, "%s: epilogue ops need bf16 output (out_f32 = 0)", who);
+  if (!aux || (epi == SVDQ_EPI_RESIDUAL_GATE && !vec)) return fail(SVDQ_ERR_ARG, "%s: null epilogue operand", who);
+  if (ldaux < N) return fail(SVDQ_ERR_SHAPE, "%s: ldaux=%lld < N=%d", who, (long long)ldaux, N);
+  if (reinterpret_cast<uintptr_t>(aux) % 2 || reinterpret_cast<uintptr_t>(vec) % 2)
+    return fail(SVDQ_ERR_ALIGN, "%s: aux and vec must be 2-byte aligned (bf16)", who);
+  return SVDQ_OK;
+}
+
+static void set_epi(svdq::GemmParams& p, int epi, const void* aux, int64_t ldaux, const void* vec) {
+  p.epi = epi;
+  p.aux = static_cast<const uint16_t*>(aux);
+  p.ldaux = ldaux;
+  p.evec = static_cast<const uint16_t*>(vec);
+  p.aux_vec = aligned16(aux) && ldaux % 8 == 0 && (vec == nullptr || aligned16(vec));
+}
+
 int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
                    const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
                    void* y, int64_t ldy, int out_f32, hipStream_t stream) {
+  return svdq_w4a4_gemm_epi(qa, operand, sxp, qwe, swp, mid, l1cat, RTp, bias, M, N, K, group, y, ldy, out_f32,
+                            SVDQ_EPI_NONE, nullptr, 0, nullptr, stream);
+}
+
+int svdq_w4a4_gemm_epi(const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
+                       const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                       void* y, int64_t ldy, int out_f32, int epi, const void* aux, int64_t ldaux, const void* vec,
+                       hipStream_t stream) {
   const void* sw = swp;
   if (int e = gemm_common_checks("w4a4_gemm", qwe, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
     return e;
+  if (int e = epi_checks("w4a4_gemm", epi, aux, ldaux, vec, N, out_f32)) return e;
   if (!qa || !sxp) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
   if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8 && operand != SVDQ_OPERAND_E3M2)
     return fail(SVDQ_ERR_ARG, "w4a4_gemm: operand format %d", operand);
@@ -211,20 +241,31 @@ int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe
   p.qa = static_cast<const uint8_t*>(qa);
   p.sxp = static_cast<const uint32_t*>(sxp);
   p.swp = static_cast<const uint32_t*>(swp);
+  set_epi(p, epi, aux, ldaux, vec);
   return launched(svdq::launch_w4a4(p, group, operand, out_f32 == 1, stream), "w4a4_gemm");
 }
 
 int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const void* mid,
                     const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group, void* y,
                     int64_t ldy, int out_f32, hipStream_t stream) {
+  return svdq_w4a16_gemm_epi(xhat, ldxh, qw, sw, mid, l1cat, RTp, bias, M, N, K, group, y, ldy, out_f32,
+                             SVDQ_EPI_NONE, nullptr, 0, nullptr, stream);
+}
+
+int svdq_w4a16_gemm_epi(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const void* mid,
+                        const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group, void* y,
+                        int64_t ldy, int out_f32, int epi, const void* aux, int64_t ldaux, const void* vec,
+                        hipStream_t stream) {
   if (int e = gemm_common_checks("w4a16_gemm", qw, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
     return e;
+  if (int e = epi_checks("w4a16_gemm", epi, aux, ldaux, vec, N, out_f32)) return e;
   if (!xhat) return fail(SVDQ_ERR_ARG, "w4a16_gemm: null pointer");
   if (ldxh < K || ldxh % 8 || !aligned16(xhat))
     return fail(SVDQ_ERR_ALIGN, "w4a16_gemm: xhat must be 16-byte aligned with ldxh >= K, ldxh %% 8 == 0");
   svdq::GemmParams p = gemm_params(qw, sw, mid, l1cat, RTp, bias, M, N, K, y, ldy);
   p.xhat = static_cast<const uint16_t*>(xhat);
   p.ldxh = ldxh;
+  set_epi(p, epi, aux, ldaux, vec);
   return launched(svdq::launch_w4a16(p, group, out_f32 == 1, stream), "w4a16_gemm");
 }
 

@@ -31,12 +31,44 @@ __device__ __forceinline__ float ubyte_f32(uint32_t v) { return (float)((v >> (8
 
 
 
+// GemmParams::epi on one element: y = the bf16-rounded layer output, a = the aux element, g = the
+// column's evec element.  Each op rounds its result to bf16 as the unfused torch ops on bf16
+// tensors do (float math inside one op, bf16 out): sigmoid and silu as 1 / (1 + exp(-v)) and
+// v / (1 + exp(-v)) in float.  The caller rounds the returned value.
+__device__ __forceinline__ float epi_op(int epi, float y, float a, float g) {
+  if (epi == 1) return a * round_bf16(1.0f / (1.0f + expf(-y)));   // a * sigmoid(y)
+  if (epi == 2) return round_bf16(a / (1.0f + expf(-a))) * y;      // silu(a) * y
+  return a + round_bf16(g * y);                                     // a + g * y
+}
+
+// epi on a chunk of 8 bf16 outputs (row m, columns n..n+7; columns >= N are left as they are);
+// aux and evec by 16-byte loads when their layout allows, else element by element.
+__device__ __forceinline__ u32x4 epi_chunk(const GemmParams& p, u32x4 v, int m, int n) {
+  const uint16_t* ar = p.aux + (long)m * p.ldaux + n;
+  u32x4 a, g = u32x4{};
+  if (p.aux_vec && n + 8 <= p.N) {
+    a = ld16(ar);
+    if (p.epi == 3) g = ld16(p.evec + n);
+  } else {
+    a = u32x4{};
+    for (int e = 0; e < min(8, p.N - n); ++e) {
+      a[e / 2] |= (uint32_t)ar[e] << (16 * (e % 2));
+      if (p.epi == 3) g[e / 2] |= (uint32_t)p.evec[n + e] << (16 * (e % 2));
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    v[d] = pack_bf16x2(epi_op(p.epi, bf16lo(v[d]), bf16lo(a[d]), bf16lo(g[d])),
+                       epi_op(p.epi, bf16hi(v[d]), bf16hi(a[d]), bf16hi(g[d])));
+  return v;
+}
+
 // acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store (directly, or through the
 // wave's 4 KB LDS region `stage` when it is given).  mid is the activation
 // pass's finalized operand, bf16 hi and lo planes per row ([M, 2, RTp]); both planes go through
 // the bf16 MFMA, so the low-rank term carries the f32 mid to 2^-18.  Two 16-column steps per
 // iteration, their twelve loads issued together (one memory latency per 32 columns of RTp).
-template <bool OUT_F32>
+template <bool OUT_F32, bool EPI = false>
 __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2], int m0, int n0,
                                          int lr, int h, uint8_t* stage, const uint8_t* lmid = nullptr,
                                          const uint8_t* ll1 = nullptr, int wr = 0, int wc = 0) {
@@ -120,11 +152,15 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
         for (int r = 0; r < 16; ++r) {
           const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
           if (m >= p.M) continue;
-          const float v = acc[i][j][r] + bv[j];
-          if (OUT_F32)
+          float v = acc[i][j][r] + bv[j];
+          if (OUT_F32) {
             reinterpret_cast<float*>(p.y)[(long)m * p.ldy + n] = v;
-          else
+          } else {
+            if (EPI)
+              v = epi_op(p.epi, round_bf16(v), bf16f(p.aux[(long)m * p.ldaux + n]),
+                         p.epi == 3 ? bf16f(p.evec[n]) : 0.0f);
             reinterpret_cast<uint16_t*>(p.y)[(long)m * p.ldy + n] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+          }
         }
     }
     return;
@@ -157,9 +193,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
     for (int it = 0; it < RP * CPR / 64; ++it) {
       const int idx = 64 * it + (h << 5 | lr), row = idx / CPR, c = idx % CPR;
       const int pos = c ^ ((row >> 2) & 1 ? CPR / 2 : 0);
-      const u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * (64 * ES) + pos * 16);
+      u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * (64 * ES) + pos * 16);
       const int m = m0 + 32 * i + rq + row, n = n0 + c * VPC;
       if (m >= p.M) continue;
+      if (!OUT_F32 && EPI) v = epi_chunk(p, v, m, n);
       uint8_t* out = reinterpret_cast<uint8_t*>(p.y) + ((long)m * p.ldy + n) * ES;
       if (vec && n + VPC <= p.N) {
         st16(out, v);
@@ -223,7 +260,7 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 // before the last step of a stage, after which the first fragments of the next stage are read.
 // With G == 128 (twice the fragment registers, one set) the next fragments are read after the
 // step's MFMAs, and the barrier follows the last step's MFMAs.
-template <int G, int MODE, bool OUT_F32>
+template <int G, int MODE, bool OUT_F32, bool EPI = false>
 __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   constexpr int TBM = 256, TBN = 128, NT = 512, NBUF = 3;
   constexpr int KB = 128;                     // K columns per pipeline stage
@@ -467,7 +504,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   // reads, the operand buffers hold the output staging regions.
   __syncthreads();
   unrotate_acc(acc);
-  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, sA + wave * 4096);
+  epilogue<OUT_F32, EPI>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, sA + wave * 4096);
 }
 
 // W4A4 GEMM on the FP6 MFMA (e3m2 operands, v_mfma_scale_f32_32x32x64_f8f6f4 with format 3 on
@@ -491,7 +528,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
 // offsets fold into the read and DMA instructions), no step carries a bound check, the last
 // stage is peeled (no DMA, the epilogue's prefetch), and the DMA sources are wave-uniform
 // pointers advanced one stage at a time.  Other K take the general loop.
-template <int G, bool OUT_F32, bool FULL>
+template <int G, bool OUT_F32, bool FULL, bool EPI = false>
 __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
   constexpr int TBM = 256, TBN = 128, NBUF = 2;
   constexpr int KB = 256;                     // K columns per pipeline stage
@@ -857,7 +894,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
   if (epi_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   unrotate_acc(acc);
-  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[lbuf][0] + wave * 4096,
+  epilogue<OUT_F32, EPI>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[lbuf][0] + wave * 4096,
                     epi_lds ? &sAQ[lbuf ^ 1][0] : nullptr, epi_lds ? &sBQ[lbuf ^ 1][0] : nullptr, 64 * wm, 64 * wn);
 }
 
@@ -927,7 +964,7 @@ __global__ void weight_scale_pairs_kernel(const uint16_t* __restrict__ sw, uint3
 // RNE pack) -- with one barrier per stage.  LDS rows are 64 bf16 plus 16 bytes of padding (144-byte
 // pitch): the fragment reads (16 lanes on 16 consecutive rows) and the staging writes hit
 // distinct bank groups.
-template <int G, int WM, bool OUT_F32>
+template <int G, int WM, bool OUT_F32, bool EPI = false>
 __global__ void __launch_bounds__(WM * 128, 1) w4a16_kernel(GemmParams p) {
   constexpr int NT = WM * 128;                // threads
   constexpr int TBM = 64 * WM, TBN = 128, KB = 64;
@@ -1093,7 +1130,7 @@ __global__ void __launch_bounds__(WM * 128, 1) w4a16_kernel(GemmParams p) {
     for (int i = 0; i < BLD; ++i) asm volatile("" ::"v"(rb[q][i]), "v"(rs[q][i]));
   }
   // the last barrier passed: every wave is done with the A buffers, which now stage the output
-  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sA[0][0] + wave * 4096);
+  epilogue<OUT_F32, EPI>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sA[0][0] + wave * 4096);
 }
 
 // W4A16 on large grids: one wave per SIMD with a 128 x 128 register tile (4 x 4 sub-tiles of
@@ -1103,7 +1140,7 @@ __global__ void __launch_bounds__(WM * 128, 1) w4a16_kernel(GemmParams p) {
 // row (64 codes dequantized as in w4a16_kernel) written to the other LDS buffer, so one instruction
 // stream keeps the MFMA pipe, the VALU and the LDS busy together.  Loads run two stages ahead with
 // the same exact-count asm waits; LDS rows have the 144-byte pitch of w4a16_kernel.
-template <int G, bool OUT_F32>
+template <int G, bool OUT_F32, bool EPI = false>
 __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
   constexpr int NT = 256, TBM = 256, TBN = 256, KB = 64;
   constexpr int PITCH = 2 * KB + 16;
@@ -1235,13 +1272,27 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
     asm volatile("" ::"v"(rb[q][0]), "v"(rb[q][1]), "v"(rs[q]));
   }
   // epilogue per 64 x 64 quadrant of the wave tile (the A buffers stage the output)
-#pragma unroll
-  for (int qi = 0; qi < 2; ++qi)
-#pragma unroll
-    for (int qj = 0; qj < 2; ++qj) {
+  if constexpr (EPI) {
+    // written out per quadrant: with the fused op the unrolled loop below is too large for the
+    // unroller, and a rolled loop would index the accumulators at run time (scratch)
+    auto quadrant = [&](auto qi_c, auto qj_c) {
+      constexpr int qi = decltype(qi_c)::value, qj = decltype(qj_c)::value;
       f32x16 part[2][2] = {{acc[2 * qi][2 * qj], acc[2 * qi][2 * qj + 1]}, {acc[2 * qi + 1][2 * qj], acc[2 * qi + 1][2 * qj + 1]}};
-      epilogue<OUT_F32>(p, part, m0 + 128 * wm + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096);
-    }
+      epilogue<OUT_F32, EPI>(p, part, m0 + 128 * wm + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096);
+    };
+    quadrant(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    quadrant(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+    quadrant(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+    quadrant(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+  } else {
+#pragma unroll
+    for (int qi = 0; qi < 2; ++qi)
+#pragma unroll
+      for (int qj = 0; qj < 2; ++qj) {
+        f32x16 part[2][2] = {{acc[2 * qi][2 * qj], acc[2 * qi][2 * qj + 1]}, {acc[2 * qi + 1][2 * qj], acc[2 * qi + 1][2 * qj + 1]}};
+        epilogue<OUT_F32>(p, part, m0 + 128 * wm + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096);
+      }
+  }
 }
 
 }  // namespace
@@ -1252,6 +1303,7 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
 #define SVDQ_W4A4(GG, MM)                                                        \
   if (G == GG && mode == MM) {                                                   \
     if (out_f32) SVDQ_W4A4_KERNEL<GG, MM, true><<<grid, 512, 0, st>>>(p);         \
+    else if (p.epi) SVDQ_W4A4_KERNEL<GG, MM, false, true><<<grid, 512, 0, st>>>(p); \
     else SVDQ_W4A4_KERNEL<GG, MM, false><<<grid, 512, 0, st>>>(p);                \
     return hipGetLastError();                                                    \
   }
@@ -1266,9 +1318,11 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
   if (G == GG) {                                                                       \
     if (full) {                                                                        \
       if (out_f32) w4a4_e3m2_kernel<GG, true, true><<<grid, 512, 0, st>>>(p);           \
+      else if (p.epi) w4a4_e3m2_kernel<GG, false, true, true><<<grid, 512, 0, st>>>(p); \
       else w4a4_e3m2_kernel<GG, false, true><<<grid, 512, 0, st>>>(p);                  \
     } else {                                                                           \
       if (out_f32) w4a4_e3m2_kernel<GG, true, false><<<grid, 512, 0, st>>>(p);          \
+      else if (p.epi) w4a4_e3m2_kernel<GG, false, false, true><<<grid, 512, 0, st>>>(p); \
       else w4a4_e3m2_kernel<GG, false, false><<<grid, 512, 0, st>>>(p);                 \
     }                                                                                  \
     return hipGetLastError();                                                          \
@@ -1310,6 +1364,7 @@ hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st
 #define SVDQ_W4A16W(GG)                                                                    \
   if (G == GG) {                                                                          \
     if (out_f32) w4a16_wide_kernel<GG, true><<<grid, 256, 0, st>>>(p);                    \
+    else if (p.epi) w4a16_wide_kernel<GG, false, true><<<grid, 256, 0, st>>>(p);          \
     else w4a16_wide_kernel<GG, false><<<grid, 256, 0, st>>>(p);                           \
     return hipGetLastError();                                                             \
   }
@@ -1322,6 +1377,7 @@ hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st
 #define SVDQ_W4A16(GG)                                                                     \
   if (G == GG) {                                                                          \
     if (out_f32) w4a16_kernel<GG, 2, true><<<grid, 256, 0, st>>>(p);                       \
+    else if (p.epi) w4a16_kernel<GG, 2, false, true><<<grid, 256, 0, st>>>(p);             \
     else w4a16_kernel<GG, 2, false><<<grid, 256, 0, st>>>(p);                              \
     return hipGetLastError();                                                             \
   }

@@ -41,6 +41,13 @@ struct GemmParams {
   void* y;                  // [M, ldy] bf16 or f32
   long ldy;
   int M, N, K;
+  // Elementwise op on the bf16-rounded output (bf16 output only): 0 none, 1 aux * sigmoid(y),
+  // 2 silu(aux) * y, 3 aux + evec[n] * y, each intermediate rounded to bf16 as torch does.
+  int epi;
+  const uint16_t* aux;      // [M, ldaux] bf16 (epi != 0)
+  long ldaux;
+  const uint16_t* evec;     // [N] bf16 (epi == 3)
+  int aux_vec;              // 1: aux (and evec) take 16-byte loads (aligned, ldaux % 8 == 0)
 };
 
 int act_splits(int M, int K, int G);

@@ -140,12 +140,46 @@ def _flatten(x: Tensor) -> tuple[Tensor, tuple[int, ...]]:
     return x.reshape(-1, x.shape[-1]).contiguous(), tuple(x.shape[:-1])
 
 
+def _aligned(t: Tensor) -> Tensor:
+    """``t`` itself when its storage starts on 16 bytes (the kernels' vector loads), else a copy."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _epilogue_operands(epilogue: str, aux: Optional[Tensor], vec: Optional[Tensor], m: int, n: int,
+                       device: torch.device) -> tuple[int, Optional[Tensor], Optional[Tensor]]:
+    if epilogue not in ops.EPILOGUES:
+        raise ValueError(f"epilogue must be one of {sorted(ops.EPILOGUES)}, got {epilogue!r}")
+    epi = ops.EPILOGUES[epilogue]
+    if epi == 0:
+        if aux is not None or vec is not None:
+            raise ValueError("aux / vec given without an epilogue op")
+        return epi, None, None
+    if aux is None or aux.shape[-1] != n or aux.numel() != m * n:
+        raise ValueError(f"epilogue {epilogue!r} needs aux of shape [..., {n}] with {m} rows")
+    if aux.device != device or aux.dtype != torch.bfloat16:
+        raise TypeError(f"aux must be bfloat16 on {device}, got {aux.dtype} on {aux.device}")
+    aux2 = _aligned(aux.reshape(m, n).contiguous())
+    vec2 = None
+    if epi == ops.EPILOGUES["residual_gate"]:
+        if vec is None or vec.numel() != n:
+            raise ValueError(f"epilogue 'residual_gate' needs vec with {n} entries")
+        vec2 = _aligned(vec.to(device, torch.bfloat16).reshape(n).contiguous())
+    elif vec is not None:
+        raise ValueError("vec is only used by epilogue 'residual_gate'")
+    return epi, aux2, vec2
+
+
 def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_f32: bool = False,
-                     exact_div: bool = False, operand: str = "e3m2") -> Tensor:
+                     exact_div: bool = False, operand: str = "e3m2", epilogue: str = "none",
+                     aux: Optional[Tensor] = None, vec: Optional[Tensor] = None) -> Tensor:
     """One SVDQuantLinear forward on prepared operands; returns [..., N].
 
     ``operand`` picks the W4A4 MFMA: ``"e3m2"`` (FP6 MFMA, default: twice the FP8 rate),
     ``"e4m3"`` (FP8 MFMA) or ``"i8"`` (INT8 MFMA); all compute the same exact integer group sums.
+    ``epilogue`` fuses an elementwise op into the GEMM's bf16 store (o = the layer output, bf16
+    rounding after every op as with the unfused torch ops): ``"mul_sigmoid"`` gives
+    ``aux * sigmoid(o)``, ``"silu_mul"`` gives ``silu(aux) * o`` and ``"residual_gate"`` gives
+    ``aux + vec * o``; ``aux`` has the output's shape, ``vec`` is [N].
     """
     if not x.is_cuda:
         raise RuntimeError("HIP gfx950 backend needs a GPU tensor")
@@ -159,6 +193,7 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
         raise ValueError(f"activation K={k} exceeds packed weight K={prep.kp}")
     if k != prep.kp:
         x2 = _pad_cols(x2, prep.kp)
+    epi, aux2, vec2 = _epilogue_operands(epilogue, aux, vec, x2.shape[0], prep.n, x.device)
     if mode == "w4a4":
         if operand not in ops.OPERAND_NAMES:
             raise ValueError(f"operand must be 'e4m3', 'e3m2' or 'i8', got {operand!r}")
@@ -166,13 +201,13 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
         qa, sx, _, _, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
                                           prep.group_size, prep.rtp, opc, False, False, exact_div, True)
         y = ops.w4a4_gemm(qa, sx, prep.weight_operand(opc), prep.weight_scale_pairs(opc), mid, prep.l1cat,
-                          prep.bias, prep.group_size, opc, out_f32)
+                          prep.bias, prep.group_size, opc, out_f32, epi, aux2, vec2)
     elif mode == "w4a16":
         _, _, _, xhat, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
                                            prep.group_size, prep.rtp, ops.OPERAND_NONE, False, True,
                                            exact_div)
         y = ops.w4a16_gemm(xhat, prep.qweight, prep.weight_scales, mid, prep.l1cat, prep.bias,
-                           prep.group_size, out_f32)
+                           prep.group_size, out_f32, epi, aux2, vec2)
     else:
         raise ValueError(f"mode must be 'w4a4' or 'w4a16', got {mode!r}")
     return y.reshape(*lead, prep.n)

@@ -24,6 +24,12 @@ SVDQ_ACT_OPERAND_I8 = 16
 SVDQ_ACT_SX_PAIRS = 32
 SVDQ_ACT_OPERAND_E3M2 = 64
 
+# epilogue ops of the *_gemm_epi entry points
+SVDQ_EPI_NONE = 0
+SVDQ_EPI_MUL_SIGMOID = 1
+SVDQ_EPI_SILU_MUL = 2
+SVDQ_EPI_RESIDUAL_GATE = 3
+
 STATUS = {0: "SVDQ_OK", -1: "SVDQ_ERR_ARG", -2: "SVDQ_ERR_SHAPE", -3: "SVDQ_ERR_ALIGN",
           -4: "SVDQ_ERR_UNSUPPORTED", -5: "SVDQ_ERR_LAUNCH"}
 
@@ -45,6 +51,10 @@ SIGNATURES = {
     "svdq_prepare_weight_operand": (_I, [_P, _P, _I, _I, _I, _P]),
     "svdq_w4a4_gemm": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
     "svdq_w4a16_gemm": (_I, [_P, _L, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
+    "svdq_w4a4_gemm_epi": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I,
+                                _I, _P, _L, _P, _P]),
+    "svdq_w4a16_gemm_epi": (_I, [_P, _L, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I,
+                                 _I, _P, _L, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -237,10 +237,39 @@ def _check_gemm(qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tens
     return n
 
 
+EPILOGUES = {"none": lib.SVDQ_EPI_NONE, "mul_sigmoid": lib.SVDQ_EPI_MUL_SIGMOID,
+             "silu_mul": lib.SVDQ_EPI_SILU_MUL, "residual_gate": lib.SVDQ_EPI_RESIDUAL_GATE}
+
+
+def _check_epi(epi: int, aux: Optional[Tensor], vec: Optional[Tensor], m: int, n: int, out_f32: bool,
+               dev: torch.device) -> None:
+    """Validate the operands of a fused epilogue op (``EPILOGUES``)."""
+    _need(epi in EPILOGUES.values(), ValueError, f"epilogue op {epi}")
+    if epi == lib.SVDQ_EPI_NONE:
+        _need(aux is None and vec is None, ValueError, "aux / vec given without an epilogue op")
+        return
+    _need(not out_f32, ValueError, "epilogue ops need bf16 output")
+    _need(aux is not None, ValueError, "epilogue op needs aux")
+    _check_dev("aux", aux, dev, torch.bfloat16)
+    _need(tuple(aux.shape) == (m, n), ValueError, f"aux must be [{m}, {n}], got {tuple(aux.shape)}")
+    if epi == lib.SVDQ_EPI_RESIDUAL_GATE:
+        _need(vec is not None, ValueError, "residual_gate needs vec")
+        _check_dev("vec", vec, dev, torch.bfloat16)
+        _need(vec.numel() == n, ValueError, f"vec must have {n} entries")
+    else:
+        _need(vec is None, ValueError, "vec is only used by residual_gate")
+
+
+def _epi_args(epi: int, aux: Optional[Tensor], vec: Optional[Tensor], n: int) -> tuple:
+    return (epi, _vp(aux), aux.shape[1] if aux is not None else n, _vp(vec))
+
+
 @torch.library.custom_op("svdq::w4a4_gemm", mutates_args=())
 def w4a4_gemm(qa: Tensor, sx_pairs: Tensor, weight_operand: Tensor, weight_scale_pairs: Tensor, mid: Tensor,
-              l1cat: Tensor, bias: Optional[Tensor], group_size: int, operand: int, out_f32: bool) -> Tensor:
-    """``y = sum_g sx sw (qa . qw)_g + mid @ l1cat^T + bias`` (bf16 or float32 output).
+              l1cat: Tensor, bias: Optional[Tensor], group_size: int, operand: int, out_f32: bool,
+              epi: int = 0, aux: Optional[Tensor] = None, vec: Optional[Tensor] = None) -> Tensor:
+    """``y = sum_g sx sw (qa . qw)_g + mid @ l1cat^T + bias`` (bf16 or float32 output), then the
+    elementwise op ``epi`` (``EPILOGUES``; bf16 output) with ``aux`` [M, N] and ``vec`` [N].
 
     ``sx_pairs`` comes from ``act_quant(..., sx_pairs=True)``; ``weight_operand`` and
     ``weight_scale_pairs`` from ``prepare_weight_operand`` and ``prepare_weight_scales`` with
@@ -263,33 +292,40 @@ def w4a4_gemm(qa: Tensor, sx_pairs: Tensor, weight_operand: Tensor, weight_scale
     _need(tuple(weight_operand.shape) == _operand_shape(n, k, operand), ValueError,
           f"weight_operand must be {_operand_shape(n, k, operand)}, got {tuple(weight_operand.shape)}")
     _check_epilogue(mid, l1cat, bias, m, n, dev)
+    _check_epi(epi, aux, vec, m, n, out_f32, dev)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
-    lib.call("svdq_w4a4_gemm", _vp(qa), operand, _vp(sx_pairs), _vp(weight_operand), _vp(weight_scale_pairs), _vp(mid),
-             _vp(l1cat), mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32), _stream(dev))
+    lib.call("svdq_w4a4_gemm_epi", _vp(qa), operand, _vp(sx_pairs), _vp(weight_operand), _vp(weight_scale_pairs),
+             _vp(mid), _vp(l1cat), mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32),
+             *_epi_args(epi, aux, vec, n), _stream(dev))
     return y
 
 
 @w4a4_gemm.register_fake
-def _(qa, sx_pairs, weight_operand, weight_scale_pairs, mid, l1cat, bias, group_size, operand, out_f32):
+def _(qa, sx_pairs, weight_operand, weight_scale_pairs, mid, l1cat, bias, group_size, operand, out_f32,
+      epi=0, aux=None, vec=None):
     return qa.new_empty((sx_pairs.shape[1], weight_scale_pairs.shape[1]),
                         dtype=torch.float32 if out_f32 else torch.bfloat16)
 
 
 @torch.library.custom_op("svdq::w4a16_gemm", mutates_args=())
 def w4a16_gemm(xhat: Tensor, qweight: Tensor, weight_scales: Tensor, mid: Tensor, l1cat: Tensor,
-               bias: Optional[Tensor], group_size: int, out_f32: bool) -> Tensor:
-    """``y = xhat @ bf16(q * bf16(sw))^T + mid @ l1cat^T + bias`` (bf16 or float32 output)."""
+               bias: Optional[Tensor], group_size: int, out_f32: bool, epi: int = 0, aux: Optional[Tensor] = None,
+               vec: Optional[Tensor] = None) -> Tensor:
+    """``y = xhat @ bf16(q * bf16(sw))^T + mid @ l1cat^T + bias`` (bf16 or float32 output), then the
+    elementwise op ``epi`` as in ``w4a4_gemm``."""
     _need(xhat.is_cuda, RuntimeError, "svdq::w4a16_gemm needs GPU tensors")
     dev = xhat.device
     _check_dev("xhat", xhat, dev, torch.bfloat16)
     m, k = xhat.shape
     n = _check_gemm(qweight, weight_scales, mid, l1cat, bias, m, k, group_size, dev)
+    _check_epi(epi, aux, vec, m, n, out_f32, dev)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
-    lib.call("svdq_w4a16_gemm", _vp(xhat), k, _vp(qweight), _vp(weight_scales), _vp(mid), _vp(l1cat),
-             mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32), _stream(dev))
+    lib.call("svdq_w4a16_gemm_epi", _vp(xhat), k, _vp(qweight), _vp(weight_scales), _vp(mid), _vp(l1cat),
+             mid.shape[2], _vp(bias), m, n, k, group_size, _vp(y), n, int(out_f32), *_epi_args(epi, aux, vec, n),
+             _stream(dev))
     return y
 
 
 @w4a16_gemm.register_fake
-def _(xhat, qweight, weight_scales, mid, l1cat, bias, group_size, out_f32):
+def _(xhat, qweight, weight_scales, mid, l1cat, bias, group_size, out_f32, epi=0, aux=None, vec=None):
     return xhat.new_empty((xhat.shape[0], qweight.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)

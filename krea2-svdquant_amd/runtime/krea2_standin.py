@@ -20,7 +20,9 @@ the concatenated text and latent tokens, modulation vectors fixed per block):
 
 A denoise step is the 28 blocks over [text | latent] tokens followed by the Euler update of the
 latent tokens, ``latent += dt * velocity``.  Attention, norms and elementwise work run in
-PyTorch-ROCm; every quantized linear runs on the gfx950 kernels (``SVDQuantLinear``).
+PyTorch-ROCm; every quantized linear runs on the gfx950 kernels (``SVDQuantLinear``).  With
+``fused=True`` the sigmoid gate, the SwiGLU product and the two gated residual adds run inside
+the stores of to_gate, ff.up, to_out.0 and ff.down instead.
 """
 from __future__ import annotations
 
@@ -144,15 +146,20 @@ class Krea2StandInBlock(nn.Module):
                 "attn.to_out.0": a.to_out[0], "ff.gate": f.gate, "ff.up": f.up, "ff.down": f.down}
 
     def forward(self, x: Tensor, cos: Tensor, sin: Tensor, linear: LinearFn = _module_linear,
-                modulation: Optional[Tensor] = None) -> Tensor:
+                modulation: Optional[Tensor] = None, fused: bool = False) -> Tensor:
         """x [T, hidden] -> [T, hidden].  ``linear(name, module, input)`` evaluates a quantized
         linear (default: the module itself); ``modulation`` overrides the block's buffer (a
-        reference evaluation on another device passes its own copy)."""
+        reference evaluation on another device passes its own copy).  ``fused=True`` runs the
+        modules with the ops that follow to_gate, to_out.0, ff.up and ff.down fused into their
+        kernels' stores (``SVDQuantLinear.forward_epilogue``: the same ops, the same bf16
+        rounding); ``linear`` is then not used."""
         d = self.dims
         mod = self.modulation if modulation is None else modulation
         shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = (m.to(x.dtype) for m in mod)
         lin = self.linears()
         t = x.shape[0]
+        if fused:
+            return self._forward_fused(x, cos, sin, lin, (shift_a, scale_a, gate_a, shift_f, scale_f, gate_f))
 
         h = rms_norm(x) * (1 + scale_a) + shift_a
         q = linear("attn.to_q", lin["attn.to_q"], h).view(t, d.heads, d.head_dim)
@@ -167,6 +174,25 @@ class Krea2StandInBlock(nn.Module):
         h = rms_norm(x) * (1 + scale_f) + shift_f
         f = F.silu(linear("ff.gate", lin["ff.gate"], h)) * linear("ff.up", lin["ff.up"], h)
         return x + gate_f * linear("ff.down", lin["ff.down"], f)
+
+    def _forward_fused(self, x: Tensor, cos: Tensor, sin: Tensor, lin: dict, mods: tuple) -> Tensor:
+        """``forward`` with the gates, SwiGLU and residuals in the linears' epilogues."""
+        d = self.dims
+        shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mods
+        t = x.shape[0]
+        h = rms_norm(x) * (1 + scale_a) + shift_a
+        q = lin["attn.to_q"](h).view(t, d.heads, d.head_dim)
+        k = lin["attn.to_k"](h).view(t, d.kv_heads, d.head_dim)
+        v = lin["attn.to_v"](h).view(t, d.kv_heads, d.head_dim)
+        q = apply_rope(rms_norm(q), cos, sin)
+        k = apply_rope(rms_norm(k), cos, sin)
+        a = attention(q, k, v)
+        a = lin["attn.to_gate"].forward_epilogue(h, "mul_sigmoid", aux=a)
+        x = lin["attn.to_out.0"].forward_epilogue(a, "residual_gate", aux=x, vec=gate_a)
+        h = rms_norm(x) * (1 + scale_f) + shift_f
+        g = lin["ff.gate"](h)
+        f = lin["ff.up"].forward_epilogue(h, "silu_mul", aux=g)
+        return lin["ff.down"].forward_epilogue(f, "residual_gate", aux=x, vec=gate_f)
 
 
 def attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
@@ -213,16 +239,17 @@ class Krea2StandInTransformer(nn.Module):
             blocks.append(Krea2StandInBlock(dims, layers, mod.to(torch.bfloat16)))
         return cls(dims, blocks)
 
-    def forward(self, tokens: Tensor, linear: LinearFn = _module_linear) -> Tensor:
-        """tokens [T, hidden] -> [T, hidden] through every block."""
+    def forward(self, tokens: Tensor, linear: LinearFn = _module_linear, fused: bool = False) -> Tensor:
+        """tokens [T, hidden] -> [T, hidden] through every block (``linear``, ``fused`` as in the
+        block)."""
         cos, sin = rope_tables(tokens.shape[0], self.dims.head_dim, tokens.device, tokens.dtype)
         x = tokens
         for blk in self.transformer_blocks:
-            x = blk(x, cos, sin, linear)
+            x = blk(x, cos, sin, linear, fused=fused)
         return x
 
-    def denoise_step(self, text: Tensor, latent: Tensor, dt: float) -> Tensor:
+    def denoise_step(self, text: Tensor, latent: Tensor, dt: float, fused: bool = False) -> Tensor:
         """One Euler step of the flow: the denoiser over [text | latent], then
         ``latent + dt * velocity`` for the latent tokens."""
-        out = self.forward(torch.cat([text, latent], dim=0))
+        out = self.forward(torch.cat([text, latent], dim=0), fused=fused)
         return latent + dt * out[text.shape[0]:]

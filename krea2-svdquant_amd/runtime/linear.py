@@ -124,6 +124,17 @@ class SVDQuantLinear(nn.Module):
             return self._forward_base(x)
         return forward_prepared(x, self._prepare(x.device, with_adapters=True), mode=self._mode(x.device))
 
+    def forward_epilogue(self, x: torch.Tensor, epilogue: str, aux: torch.Tensor,
+                         vec: torch.Tensor | None = None) -> torch.Tensor:
+        """``forward(x)`` followed by an elementwise op fused into the kernel's store (o = the
+        layer output): ``"mul_sigmoid"`` -> ``aux * sigmoid(o)``, ``"silu_mul"`` ->
+        ``silu(aux) * o``, ``"residual_gate"`` -> ``aux + vec * o``, each op rounded to bf16 as
+        the same torch ops on bf16 tensors are.  Not in the reference module (its blocks run
+        these ops in diffusers); the stand-in Krea-2 block uses it for SwiGLU, the attention
+        output gate and the gated residuals."""
+        prep = self._prepare(x.device, with_adapters=bool(self.lora_adapters))
+        return forward_prepared(x, prep, mode=self._mode(x.device), epilogue=epilogue, aux=aux, vec=vec)
+
     # -- backend plumbing ----------------------------------------------------------------
     def resolved_backend(self, device: torch.device | None = None) -> BackendKind:
         if self.backend is BackendKind.AUTO:

@@ -97,3 +97,26 @@ def test_w4a4_gemm_rejects_operands_beyond_32bit_offsets():
         lib.call("svdq_w4a4_gemm", fake, 0, fake, fake, fake, fake, fake, 32, None, 65536, 128, 65536, 64, fake, 128,
                  0, None)
     assert ei.value.status == -2 and "2^31" in str(ei.value)
+
+
+@pytest.mark.parametrize("fn", ["svdq_w4a4_gemm_epi", "svdq_w4a16_gemm_epi"])
+@pytest.mark.parametrize("epi,out_f32,aux,ldaux,vec,status,needle", [
+    (7, 0, 0x1000, 128, None, -1, "epilogue op 7"),
+    (lib.SVDQ_EPI_SILU_MUL, 1, 0x1000, 128, None, -1, "bf16 output"),
+    (lib.SVDQ_EPI_MUL_SIGMOID, 0, None, 128, None, -1, "null epilogue operand"),
+    (lib.SVDQ_EPI_RESIDUAL_GATE, 0, 0x1000, 128, None, -1, "null epilogue operand"),
+    (lib.SVDQ_EPI_SILU_MUL, 0, 0x1000, 120, None, -2, "ldaux=120"),
+    (lib.SVDQ_EPI_SILU_MUL, 0, 0x1001, 128, None, -3, "2-byte aligned"),
+    (lib.SVDQ_EPI_RESIDUAL_GATE, 0, 0x1000, 136, 0x1003, -3, "2-byte aligned"),
+])
+def test_gemm_epilogue_ops_rejected_before_any_launch(fn, epi, out_f32, aux, ldaux, vec, status, needle):
+    fake = ctypes.c_void_p(0x1000)
+    aux_p = None if aux is None else ctypes.c_void_p(aux)
+    vec_p = None if vec is None else ctypes.c_void_p(vec)
+    if fn == "svdq_w4a4_gemm_epi":
+        args = (fake, 2, fake, fake, fake, fake, fake, 32, None, 128, 128, 128, 64, fake, 128, out_f32)
+    else:
+        args = (fake, 128, fake, fake, fake, fake, 32, None, 128, 128, 128, 64, fake, 128, out_f32)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call(fn, *args, epi, aux_p, ldaux, vec_p, None)
+    assert ei.value.status == status and needle in str(ei.value)

@@ -97,3 +97,24 @@ def test_convert_linear_layout_and_reconstruction():
     target = w * st.smooth_scale.float()
     assert (approx - target).norm() / target.norm() < 0.1
     assert nm.bf16_bits(st.smooth_scale.float().numpy()).dtype == np.uint16
+
+
+def test_epilogue_operand_validation_on_the_host():
+    from krea2_svdquant_amd.kernels.hip import backend
+    cpu = torch.device("cpu")
+    aux = torch.zeros(4, 8, dtype=torch.bfloat16)
+    assert backend._epilogue_operands("none", None, None, 4, 8, cpu) == (0, None, None)
+    with pytest.raises(ValueError, match="epilogue must be one of"):
+        backend._epilogue_operands("gelu", aux, None, 4, 8, cpu)
+    with pytest.raises(ValueError, match="without an epilogue op"):
+        backend._epilogue_operands("none", aux, None, 4, 8, cpu)
+    with pytest.raises(ValueError, match="needs aux"):
+        backend._epilogue_operands("silu_mul", aux[:, :4], None, 4, 8, cpu)
+    with pytest.raises(TypeError, match="bfloat16"):
+        backend._epilogue_operands("silu_mul", aux.float(), None, 4, 8, cpu)
+    with pytest.raises(ValueError, match="needs vec"):
+        backend._epilogue_operands("residual_gate", aux, None, 4, 8, cpu)
+    with pytest.raises(ValueError, match="only used by"):
+        backend._epilogue_operands("mul_sigmoid", aux, torch.zeros(8, dtype=torch.bfloat16), 4, 8, cpu)
+    epi, a2, v2 = backend._epilogue_operands("residual_gate", aux.view(2, 2, 8), torch.ones(8), 4, 8, cpu)
+    assert epi == 3 and tuple(a2.shape) == (4, 8) and v2.dtype == torch.bfloat16
