@@ -16,7 +16,11 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-pytestmark = pytest.mark.gpu
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skip(reason="fused epilogue ops are switched off in the library: two GPU commands that ran the "
+                            "fused stand-in denoiser ended in GPU memory faults whose kernel was not identified"),
+]
 
 OPS = ("residual_gate", "mul_sigmoid", "silu_mul")
 
