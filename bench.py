@@ -301,7 +301,10 @@ def main() -> int:
         for _ in range(3):
             gemm()
         torch.cuda.synchronize()
-        log("pmc pass done: 1 copy of 256 MiB, 3 GEMM launches")
+        for _ in range(3):   # the activation pass (act_kernel + mid_finalize_kernel)
+            ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False, True)
+        torch.cuda.synchronize()
+        log("pmc pass done: 1 copy of 256 MiB, 3 GEMM launches, 3 activation passes")
         return 0
 
     def step():
