@@ -218,11 +218,23 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
 // an operand, so the compiler owns that register.  Issued as inline asm so that the compiler
 // neither orders later LDS reads after it (it cannot tell the pipeline stages apart) nor
 // counts it in its own waits: the kernel waits explicitly.
+// The hazard: gfx9 requires 5 wait states between a VALU instruction that writes an SGPR and a
+// VMEM instruction that reads it.  The compiler inserts them for its own instructions but cannot
+// see the operands of inline asm; under SGPR pressure it restores a spilled base pointer with
+// v_readlane right before a DMA, which then reads a stale address (builds where that happened
+// faulted the GPU).  NOP = true starts the DMA with `s_nop 4` (5 wait states, about 2% of the
+// e3m2 GEMM's time); the kernels whose build restores SGPRs before a DMA (the fused-epilogue
+// variants) set it.  tests/test_dma_hazards.py walks every DMA of the built library back over
+// all its predecessor paths and fails if any can read a VALU-written base SGPR too early.
+template <bool NOP = false>
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+  if (NOP) asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+  else asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
+template <bool NOP = false>
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("global_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+  if (NOP) asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+  else asm volatile("global_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
@@ -329,15 +341,15 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
       const int jmax = ngroups - 1 - g0;
       const uint32_t* sx_s = p.sxp + (long)g0 * p.M;
       const uint32_t* sw_s = p.swp + (long)g0 * p.N;
-      dma4(sx_s, 4 * ((uint32_t)min(xj, jmax) * (uint32_t)p.M + xrowc), ldsX + 4 * ((buf * GPS + xjs) * XS + xbase));
-      dma4(sw_s, 4 * ((uint32_t)min(wj, jmax) * (uint32_t)p.N + wrowc), ldsW + 4 * ((buf * GPS + wjs) * WS + wbase));
+      dma4<EPI>(sx_s, 4 * ((uint32_t)min(xj, jmax) * (uint32_t)p.M + xrowc), ldsX + 4 * ((buf * GPS + xjs) * XS + xbase));
+      dma4<EPI>(sw_s, 4 * ((uint32_t)min(wj, jmax) * (uint32_t)p.N + wrowc), ldsW + 4 * ((buf * GPS + wjs) * WS + wbase));
     }
 #pragma unroll
     for (int i = 0; i < ADMA; ++i)
-      if ((i + 1) / 2 == q) dma16(qa_s, arow_o[i] + min(ac16[i], lim), ldsA + buf * ABUF + (ADMA * wave + i) * 1024);
+      if ((i + 1) / 2 == q) dma16<EPI>(qa_s, arow_o[i] + min(ac16[i], lim), ldsA + buf * ABUF + (ADMA * wave + i) * 1024);
 #pragma unroll
     for (int i = 0; i < BDMA; ++i)
-      if (q == 2 + i) dma16(qw_s, brow_o[i] + min(bc16[i], lim), ldsB + buf * BBUF + (BDMA * wave + i) * 1024);
+      if (q == 2 + i) dma16<EPI>(qw_s, brow_o[i] + min(bc16[i], lim), ldsB + buf * BBUF + (BDMA * wave + i) * 1024);
   };
 
   f32x16 acc[2][2];
@@ -585,23 +597,23 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
     const int kt = min(s * KT + (wave >> 1), nkt - 1);    // a k-step past K re-reads the last one
     const long pl = (long)(kt * 2 + (wave & 1));
     if (d < 4) {
-      dma16(p.qa + pl * Mp * 16, aq_o[d], ldsAQ + buf * AQ + (wave * TBM + 64 * d) * 16);
+      dma16<EPI>(p.qa + pl * Mp * 16, aq_o[d], ldsAQ + buf * AQ + (wave * TBM + 64 * d) * 16);
     } else if (d < 6) {
-      dma16(p.qa + aP0 + pl * Mp * 8, ap_o[d - 4], ldsAP + buf * AP + (wave * TBM + 128 * (d - 4)) * 8);
+      dma16<EPI>(p.qa + aP0 + pl * Mp * 8, ap_o[d - 4], ldsAP + buf * AP + (wave * TBM + 128 * (d - 4)) * 8);
     } else if (d < 8) {
-      dma16(p.qwe + pl * Np * 16, bq_o[d - 6], ldsBQ + buf * BQ + (wave * TBN + 64 * (d - 6)) * 16);
+      dma16<EPI>(p.qwe + pl * Np * 16, bq_o[d - 6], ldsBQ + buf * BQ + (wave * TBN + 64 * (d - 6)) * 16);
     } else if (d == 8) {
-      dma16(p.qwe + bP0 + pl * Np * 8, bp_o, ldsBP + buf * BP + wave * TBN * 8);
+      dma16<EPI>(p.qwe + bP0 + pl * Np * 8, bp_o, ldsBP + buf * BP + wave * TBN * 8);
     } else {
       const int g0 = s * GPS, jmax = ngroups - 1 - g0;
       if (d < 9 + SXD) {
         const int w0 = (512 * (d - 9) + 64 * wave) % (GPS * TBM), j = w0 / TBM, r0 = w0 % TBM;
         const uint32_t off = 4u * ((uint32_t)min(j, jmax) * (uint32_t)p.M + (uint32_t)min(m0 + r0 + lane, p.M - 1));
-        dma4(p.sxp + (long)g0 * p.M, off, ldsX + 4 * ((buf * GPS + j) * XS + r0));
+        dma4<EPI>(p.sxp + (long)g0 * p.M, off, ldsX + 4 * ((buf * GPS + j) * XS + r0));
       } else {
         const int w0 = (512 * (d - 9 - SXD) + 64 * wave) % (GPS * TBN), j = w0 / TBN, r0 = w0 % TBN;
         const uint32_t off = 4u * ((uint32_t)min(j, jmax) * (uint32_t)p.N + (uint32_t)min(n0 + r0 + lane, p.N - 1));
-        dma4(p.swp + (long)g0 * p.N, off, ldsW + 4 * ((buf * GPS + j) * WS + r0));
+        dma4<EPI>(p.swp + (long)g0 * p.N, off, ldsW + 4 * ((buf * GPS + j) * WS + r0));
       }
     }
   };
@@ -674,10 +686,10 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int idx = (4 * wave + c) * 64 + lane, r = idx >> 3, ch = (idx & 7) ^ ((r >> 1) & 7);
-      dma16(p.midp, (uint32_t)min(m0 + r, p.M - 1) * 128u + 16u * ch, ldsAQ + fbuf * AQ + (4 * wave + c) * 1024);
+      dma16<EPI>(p.midp, (uint32_t)min(m0 + r, p.M - 1) * 128u + 16u * ch, ldsAQ + fbuf * AQ + (4 * wave + c) * 1024);
     }
     const int idx = wave * 64 + lane, r = idx >> 2, ch = (idx & 3) ^ ((r >> 2) & 3);
-    dma16(p.l1cat, (uint32_t)min(n0 + r, p.N - 1) * 64u + 16u * ch, ldsBQ + fbuf * BQ + wave * 1024);
+    dma16<EPI>(p.l1cat, (uint32_t)min(n0 + r, p.N - 1) * 64u + 16u * ch, ldsBQ + fbuf * BQ + wave * 1024);
   };
   // This step's fragments in place and the previous step's rescale issued before the next reads
   // go out (keeps one register set live per step).
@@ -755,12 +767,12 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
       }
     };
     auto dma_next = [&](int nb, int d) {
-      if (d < 4) dma16(gAQ, aq_o[d], lAQ + nb * AQ + 64 * d * 16);
-      else if (d < 6) dma16(gAP, ap_o[d - 4], lAP + nb * AP + 128 * (d - 4) * 8);
-      else if (d < 8) dma16(gBQ, bq_o[d - 6], lBQ + nb * BQ + 64 * (d - 6) * 16);
-      else if (d == 8) dma16(gBP, bp_o, lBP + nb * BP);
-      else if (d < 9 + SXD) dma4(gX, sx_o[d - 9], lX[d - 9] + 4 * nb * GPS * XS);
-      else dma4(gW, sw_o[d - 9 - SXD], lW[d - 9 - SXD] + 4 * nb * GPS * WS);
+      if (d < 4) dma16<EPI>(gAQ, aq_o[d], lAQ + nb * AQ + 64 * d * 16);
+      else if (d < 6) dma16<EPI>(gAP, ap_o[d - 4], lAP + nb * AP + 128 * (d - 4) * 8);
+      else if (d < 8) dma16<EPI>(gBQ, bq_o[d - 6], lBQ + nb * BQ + 64 * (d - 6) * 16);
+      else if (d == 8) dma16<EPI>(gBP, bp_o, lBP + nb * BP);
+      else if (d < 9 + SXD) dma4<EPI>(gX, sx_o[d - 9], lX[d - 9] + 4 * nb * GPS * XS);
+      else dma4<EPI>(gW, sw_o[d - 9 - SXD], lW[d - 9 - SXD] + 4 * nb * GPS * WS);
     };
     auto stage = [&](auto buf_c, auto last_c) {
       constexpr int buf = decltype(buf_c)::value, nbuf = buf ^ 1;
