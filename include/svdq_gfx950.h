@@ -154,12 +154,9 @@ int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* 
 #define SVDQ_EPI_NONE 0           /* y                                                      */
 #define SVDQ_EPI_MUL_SIGMOID 1    /* bf16(a * bf16(sigmoid(o)))   gated attention output    */
 #define SVDQ_EPI_SILU_MUL 2       /* bf16(bf16(silu(a)) * o)      SwiGLU, a = the gate      */
-#define SVDQ_EPI_RESIDUAL_GATE 3  /* bf16(a + bf16(g * o))        gated residual, a = x     */
+#define SVDQ_EPI_RESIDUAL_GATE 3  /* bf16(a + g * o), one rounding (torch.addcmul): gated residual */
 
-/* svdq_w4a4_gemm / svdq_w4a16_gemm with an elementwise op fused into the store.  Switched off in
- * this build: a valid request with epi != SVDQ_EPI_NONE returns SVDQ_ERR_UNSUPPORTED (GPU runs of
- * the fused stand-in denoiser ended in GPU memory faults whose kernel was not identified); with
- * SVDQ_EPI_NONE they behave as the plain entry points.  No reference
+/* svdq_w4a4_gemm / svdq_w4a16_gemm with an elementwise op fused into the store.  No reference
  * counterpart inside the reference: they fold the elementwise torch ops that a DiT block applies
  * to a quantized linear's output (SwiGLU of ff.gate / ff.up, the sigmoid output gate of
  * attention, the gated residual of to_out.0 and ff.down) into the GEMM's one bf16 store, for

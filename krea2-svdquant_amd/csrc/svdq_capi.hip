@@ -188,11 +188,6 @@ int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int ope
                   "prepare_weight_operand");
 }
 
-// The fused ops are switched off: GPU commands that ran them inside the stand-in denoiser ended in
-// GPU memory faults whose kernel was not identified (the op tests themselves passed).  Their
-// arguments are still validated; a valid request is refused with SVDQ_ERR_UNSUPPORTED.
-static constexpr bool kEpiEnabled = false;
-
 static int epi_checks(const char* who, int epi, const void* aux, int64_t ldaux, const void* vec, int N,
                       int out_f32) {
   if (epi == SVDQ_EPI_NONE) return SVDQ_OK;
@@ -203,9 +198,6 @@ static int epi_checks(const char* who, int epi, const void* aux, int64_t ldaux, 
   if (ldaux < N) return fail(SVDQ_ERR_SHAPE, "%s: ldaux=%lld < N=%d", who, (long long)ldaux, N);
   if (reinterpret_cast<uintptr_t>(aux) % 2 || reinterpret_cast<uintptr_t>(vec) % 2)
     return fail(SVDQ_ERR_ALIGN, "%s: aux and vec must be 2-byte aligned (bf16)", who);
-  if (!kEpiEnabled)
-    return fail(SVDQ_ERR_UNSUPPORTED, "%s: fused epilogue ops are disabled in this build (unexplained GPU "
-                "faults in the fused stand-in denoiser)", who);
   return SVDQ_OK;
 }
 

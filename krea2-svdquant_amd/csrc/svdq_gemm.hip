@@ -34,11 +34,12 @@ __device__ __forceinline__ float ubyte_f32(uint32_t v) { return (float)((v >> (8
 // GemmParams::epi on one element: y = the bf16-rounded layer output, a = the aux element, g = the
 // column's evec element.  Each op rounds its result to bf16 as the unfused torch ops on bf16
 // tensors do (float math inside one op, bf16 out): sigmoid and silu as 1 / (1 + exp(-v)) and
-// v / (1 + exp(-v)) in float.  The caller rounds the returned value.
+// v / (1 + exp(-v)) in float, the gated residual in one step as torch.addcmul.  The caller rounds
+// the returned value.
 __device__ __forceinline__ float epi_op(int epi, float y, float a, float g) {
   if (epi == 1) return a * round_bf16(1.0f / (1.0f + expf(-y)));   // a * sigmoid(y)
   if (epi == 2) return round_bf16(a / (1.0f + expf(-a))) * y;      // silu(a) * y
-  return a + round_bf16(g * y);                                     // a + g * y
+  return __builtin_fmaf(g, y, a);                                   // addcmul(a, g, y)
 }
 
 // epi on a chunk of 8 bf16 outputs (row m, columns n..n+7; columns >= N are left as they are);

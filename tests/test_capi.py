@@ -121,14 +121,3 @@ def test_gemm_epilogue_ops_rejected_before_any_launch(fn, epi, out_f32, aux, lda
         lib.call(fn, *args, epi, aux_p, ldaux, vec_p, None)
     assert ei.value.status == status and needle in str(ei.value)
 
-
-@pytest.mark.parametrize("fn", ["svdq_w4a4_gemm_epi", "svdq_w4a16_gemm_epi"])
-def test_gemm_epilogue_ops_are_switched_off(fn):
-    fake = ctypes.c_void_p(0x1000)
-    if fn == "svdq_w4a4_gemm_epi":
-        args = (fake, 2, fake, fake, fake, fake, fake, 32, None, 128, 128, 128, 64, fake, 128, 0)
-    else:
-        args = (fake, 128, fake, fake, fake, fake, 32, None, 128, 128, 128, 64, fake, 128, 0)
-    with pytest.raises(lib.SVDQError) as ei:
-        lib.call(fn, *args, lib.SVDQ_EPI_SILU_MUL, fake, 128, None, None)
-    assert ei.value.status == -4 and "disabled" in str(ei.value)
