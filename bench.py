@@ -235,19 +235,24 @@ def denoise_line(args, dev) -> dict:
     steps, dt = 8, -1.0 / 8
     lat = model.denoise_step(text, latent, dt)      # warm-up: builds every layer's kernel operands
     lat = model.denoise_step(text, latent, dt, fused=True)
+    lat = model.denoise_step(text, latent, dt, siblings=True)
+    lat = model.denoise_step(text, latent, dt, fused=True, siblings=True)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    def run(fused: bool) -> tuple[float, "torch.Tensor"]:
+    def run(fused: bool, siblings: bool = False) -> tuple[float, "torch.Tensor"]:
         lat = latent
         a.record()
         for _ in range(steps):
-            lat = model.denoise_step(text, lat, dt, fused=fused)
+            lat = model.denoise_step(text, lat, dt, fused=fused, siblings=siblings)
         b.record()
         torch.cuda.synchronize()
         return a.elapsed_time(b) / steps, lat
     ms_fused, _ = run(True)
+    ms_sib, lat_sib = run(False, True)
+    ms_fused_sib, _ = run(True, True)
     ms, lat = run(False)
+    same_sib = bool(torch.equal(lat, lat_sib))
     # one more step with HIP events around every quantized linear: their share of the step
     pairs = []
 
@@ -268,13 +273,18 @@ def denoise_line(args, dev) -> dict:
     torch.cuda.empty_cache()
     return {"ms_per_denoise_step": round(ms, 3), "ms_8_steps": round(ms * steps, 2),
             "ms_per_denoise_step_fused_epilogues": round(ms_fused, 3),
+            "ms_per_denoise_step_concurrent_siblings": round(ms_sib, 3),
+            "ms_per_denoise_step_fused_epilogues_concurrent_siblings": round(ms_fused_sib, 3),
+            "concurrent_siblings_bit_identical": same_sib,
             "linears_ms_per_step": round(lin_ms, 3), "rest_ms_per_step": round(ms - lin_ms, 3),
             "tokens": 4352, "blocks": dims.layers, "peak_hbm_GB": round(hbm_gb, 1), "finite": finite,
             "note": "stand-in Krea-2 denoiser (diffusers is absent): 28 blocks, 8 W4A4 linears each on this "
                     "backend; attention (SDPA, 48 q / 12 kv heads), RMS norms, rotary embedding, gates and "
                     "residuals in PyTorch-ROCm (ms_per_denoise_step; with the sigmoid gate, SwiGLU product and "
                     "gated residuals fused into the stores of to_gate, ff.up, to_out.0 and ff.down instead: "
-                    "ms_per_denoise_step_fused_epilogues); random-init quantized weights, N(0,1) tokens; HIP "
+                    "ms_per_denoise_step_fused_epilogues; *_concurrent_siblings: the linears that read the same "
+                    "input (to_q, to_gate, to_k, to_v; ff.up, ff.gate) issued on side streams); random-init "
+                    "quantized weights, N(0,1) tokens; HIP "
                     "events around 8 Euler steps after one warm-up step of each; linears_ms_per_step: HIP events "
                     "around each linear of one forward"}
 

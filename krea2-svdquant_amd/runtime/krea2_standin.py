@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
+from functools import partial
 from typing import Callable, Optional
 
 import torch
@@ -38,6 +39,7 @@ from torch import Tensor, nn
 
 from ..quant.state import SVDQuantLinearState
 from .linear import SVDQuantLinear
+from .siblings import run_concurrent
 
 LINEAR_NAMES = ("attn.to_q", "attn.to_k", "attn.to_v", "attn.to_gate", "attn.to_out.0",
                 "ff.gate", "ff.up", "ff.down")
@@ -158,44 +160,54 @@ class Krea2StandInBlock(nn.Module):
                 "attn.to_out.0": a.to_out[0], "ff.gate": f.gate, "ff.up": f.up, "ff.down": f.down}
 
     def forward(self, x: Tensor, cos: Tensor, sin: Tensor, linear: LinearFn = _module_linear,
-                modulation: Optional[Tensor] = None, fused: bool = False) -> Tensor:
+                modulation: Optional[Tensor] = None, fused: bool = False, siblings: bool = False) -> Tensor:
         """x [T, hidden] -> [T, hidden].  ``linear(name, module, input)`` evaluates a quantized
         linear (default: the module itself); ``modulation`` overrides the block's buffer (a
         reference evaluation on another device passes its own copy).  ``fused=True`` runs the
         modules with the ops that follow to_gate, to_out.0, ff.up and ff.down fused into their
         kernels' stores (``SVDQuantLinear.forward_epilogue``: the same ops, the same bf16
-        rounding); ``linear`` is then not used."""
+        rounding); ``linear`` is then not used.  ``siblings=True`` issues the linears that read
+        the same input (to_q, to_k, to_v, to_gate; ff.gate, ff.up) concurrently on side streams
+        (``run_concurrent``: same kernels, bit-identical outputs)."""
         d = self.dims
         mod = self.modulation if modulation is None else modulation
         shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = (m.to(x.dtype) for m in mod)
         lin = self.linears()
         t = x.shape[0]
         if fused:
-            return self._forward_fused(x, cos, sin, lin, (shift_a, scale_a, gate_a, shift_f, scale_f, gate_f))
+            return self._forward_fused(x, cos, sin, lin, (shift_a, scale_a, gate_a, shift_f, scale_f, gate_f),
+                                       siblings)
+
+        def siblings_of(z: Tensor, *names: str) -> list[Tensor]:
+            fns = [partial(linear, n, lin[n]) for n in names]
+            return run_concurrent(z, fns) if siblings else [f(z) for f in fns]
 
         h = rms_norm(x, weight=1 + scale_a) + shift_a
-        q = linear("attn.to_q", lin["attn.to_q"], h).view(t, d.heads, d.head_dim)
-        k = linear("attn.to_k", lin["attn.to_k"], h).view(t, d.kv_heads, d.head_dim)
-        v = linear("attn.to_v", lin["attn.to_v"], h).view(t, d.kv_heads, d.head_dim)
+        q, g, k, v = siblings_of(h, "attn.to_q", "attn.to_gate", "attn.to_k", "attn.to_v")
+        q, k, v = (z.view(t, -1, d.head_dim) for z in (q, k, v))
         q = apply_rope(rms_norm(q), cos, sin)
         k = apply_rope(rms_norm(k), cos, sin)
         a = attention(q, k, v)                                   # [T, heads * head_dim]
-        a = a * torch.sigmoid(linear("attn.to_gate", lin["attn.to_gate"], h))
+        a = a * torch.sigmoid(g)
         x = torch.addcmul(x, gate_a, linear("attn.to_out.0", lin["attn.to_out.0"], a))
 
         h = rms_norm(x, weight=1 + scale_f) + shift_f
-        f = F.silu(linear("ff.gate", lin["ff.gate"], h)) * linear("ff.up", lin["ff.up"], h)
+        u, g = siblings_of(h, "ff.up", "ff.gate")
+        f = F.silu(g) * u
         return torch.addcmul(x, gate_f, linear("ff.down", lin["ff.down"], f))
 
-    def _forward_fused(self, x: Tensor, cos: Tensor, sin: Tensor, lin: dict, mods: tuple) -> Tensor:
-        """``forward`` with the gates, SwiGLU and residuals in the linears' epilogues."""
+    def _forward_fused(self, x: Tensor, cos: Tensor, sin: Tensor, lin: dict, mods: tuple,
+                       siblings: bool = False) -> Tensor:
+        """``forward`` with the gates, SwiGLU and residuals in the linears' epilogues (to_gate and
+        ff.up then need the attention output and ff.gate's output: only to_q, to_k and to_v
+        remain siblings)."""
         d = self.dims
         shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mods
         t = x.shape[0]
         h = rms_norm(x, weight=1 + scale_a) + shift_a
-        q = lin["attn.to_q"](h).view(t, d.heads, d.head_dim)
-        k = lin["attn.to_k"](h).view(t, d.kv_heads, d.head_dim)
-        v = lin["attn.to_v"](h).view(t, d.kv_heads, d.head_dim)
+        fns = [lin["attn.to_q"], lin["attn.to_k"], lin["attn.to_v"]]
+        q, k, v = run_concurrent(h, fns) if siblings else [f(h) for f in fns]
+        q, k, v = (z.view(t, -1, d.head_dim) for z in (q, k, v))
         q = apply_rope(rms_norm(q), cos, sin)
         k = apply_rope(rms_norm(k), cos, sin)
         a = attention(q, k, v)
@@ -251,17 +263,19 @@ class Krea2StandInTransformer(nn.Module):
             blocks.append(Krea2StandInBlock(dims, layers, mod.to(torch.bfloat16)))
         return cls(dims, blocks)
 
-    def forward(self, tokens: Tensor, linear: LinearFn = _module_linear, fused: bool = False) -> Tensor:
-        """tokens [T, hidden] -> [T, hidden] through every block (``linear``, ``fused`` as in the
-        block)."""
+    def forward(self, tokens: Tensor, linear: LinearFn = _module_linear, fused: bool = False,
+                siblings: bool = False) -> Tensor:
+        """tokens [T, hidden] -> [T, hidden] through every block (``linear``, ``fused``,
+        ``siblings`` as in the block)."""
         cos, sin = rope_tables(tokens.shape[0], self.dims.head_dim, tokens.device, tokens.dtype)
         x = tokens
         for blk in self.transformer_blocks:
-            x = blk(x, cos, sin, linear, fused=fused)
+            x = blk(x, cos, sin, linear, fused=fused, siblings=siblings)
         return x
 
-    def denoise_step(self, text: Tensor, latent: Tensor, dt: float, fused: bool = False) -> Tensor:
+    def denoise_step(self, text: Tensor, latent: Tensor, dt: float, fused: bool = False,
+                     siblings: bool = False) -> Tensor:
         """One Euler step of the flow: the denoiser over [text | latent], then
         ``latent + dt * velocity`` for the latent tokens."""
-        out = self.forward(torch.cat([text, latent], dim=0), fused=fused)
+        out = self.forward(torch.cat([text, latent], dim=0), fused=fused, siblings=siblings)
         return latent + dt * out[text.shape[0]:]

@@ -60,3 +60,42 @@ def test_block_rejects_wrong_linear_set():
     dims = ks.Krea2Dims(layers=1, hidden=256, heads=2, kv_heads=1, head_dim=128, mlp=512)
     with pytest.raises(ValueError):
         ks.Krea2StandInBlock(dims, {"attn.to_q": torch.nn.Identity()}, torch.zeros(6, 256))
+
+
+def test_run_concurrent_off_the_gpu_calls_in_order():
+    from krea2_svdquant_amd.runtime.siblings import run_concurrent
+    order = []
+
+    def f(i):
+        def g(z):
+            order.append(i)
+            return z + i
+        return g
+    x = torch.zeros(3)
+    outs = run_concurrent(x, [f(0), f(1), f(2)])
+    assert order == [0, 1, 2] and [float(o[0]) for o in outs] == [0.0, 1.0, 2.0]
+    assert run_concurrent(x, []) == []
+
+
+def test_block_siblings_flag_keeps_the_call_set_and_result():
+    # Off the GPU the siblings run in order; the flag must not change which linears see which input.
+    dims = ks.Krea2Dims(layers=1, hidden=256, heads=2, kv_heads=1, head_dim=128, mlp=512)
+    model = ks.Krea2StandInTransformer.random(dims, device="cpu", seed=2)
+    blk = model.transformer_blocks[0]
+    gen = torch.Generator().manual_seed(0)
+    w = {n: torch.randn(o, i, generator=gen) / math.sqrt(i) for n, (o, i) in dims.linear_shapes().items()}
+
+    def run(siblings):
+        seen = []
+
+        def lin(name, mod, x):
+            seen.append(name)
+            return x @ w[name].T
+        x = torch.randn(24, 256, generator=torch.Generator().manual_seed(1))
+        cos, sin = ks.rope_tables(24, 128, "cpu", torch.float32)
+        y = blk(x, cos, sin, lin, modulation=blk.modulation.float(), siblings=siblings)
+        return y, seen
+    y0, s0 = run(False)
+    y1, s1 = run(True)
+    assert sorted(s0) == sorted(ks.LINEAR_NAMES) and s0 == s1
+    assert torch.equal(y0, y1)
