@@ -154,48 +154,74 @@ def cpu_baseline(ds, x_dev, reps: int) -> dict:
             "act_quant_s": round(tq, 3)}
 
 
-def block_line(args, dev) -> dict:
-    """ms per block of the 8 W4A4 linears of config 1 at M=4096 (each timed alone, summed)."""
+BLOCK_ORDER = [("to_q", "to_gate", "to_k", "to_v"), ("to_out.0",), ("ff.up", "ff.gate"), ("ff.down",)]
+
+
+def block_layers(args, dev, m: int, mode: str, seed0: int) -> dict:
+    """The 8 block linears at M=m (``mode`` "w4a4" or "w4a16"): each timed alone, and the block
+    in dependency order (siblings that read the same input grouped, ``BLOCK_ORDER``), once with
+    the siblings issued one after another and once concurrently on side streams."""
     import torch
     from krea2_svdquant_amd.kernels.hip import backend
-    out, total, ops_total = {}, 0.0, 0.0
+    from krea2_svdquant_amd.runtime.siblings import run_concurrent
+    layers, per, ops_total = {}, {}, 0.0
     for i, (name, n, k) in enumerate(BLOCK_SHAPES):
-        x, _, prep = make_layer(n, k, args.m, args.rank, args.group, dev, seed=100 + 10 * i)
+        x, _, prep = make_layer(n, k, m, args.rank, args.group, dev, seed=seed0 + 10 * i)
+        layers[name] = (x, prep)
+        ops_total += 2.0 * m * n * k
+
+    def fwd(name):
+        prep = layers[name][1]
+        return lambda z: backend.forward_prepared(z, prep, mode=mode)
+    for name, (x, _) in layers.items():
+        f = fwd(name)
         for _ in range(3):
-            backend.forward_prepared(x, prep, mode="w4a4")
-        ms = time_avg(lambda: backend.forward_prepared(x, prep, mode="w4a4"), 20)
-        out[name] = round(ms, 4)
-        total += ms
-        ops_total += 2.0 * args.m * n * k
-        del x, prep
-        torch.cuda.empty_cache()
-    return {"ms_per_layer": out, "ms_per_block_linears": round(total, 4),
-            "eff_TOPS": round(ops_total / (total * 1e-3) / 1e12, 2),
+            f(x)
+        per[name] = round(time_avg(lambda: f(x), 20), 4)
+
+    def block(concurrent: bool):
+        for group in BLOCK_ORDER:
+            x, fns = layers[group[0]][0], [fwd(nm) for nm in group]
+            run_concurrent(x, fns) if concurrent else [f(x) for f in fns]
+    for c in (False, True):
+        block(c)
+    ms_seq = time_avg(lambda: block(False), 10)
+    ms_conc = time_avg(lambda: block(True), 10)
+    del layers
+    torch.cuda.empty_cache()
+    return {"per": per, "total": sum(per.values()), "ops": ops_total, "seq": ms_seq, "conc": ms_conc}
+
+
+def block_line(args, dev) -> dict:
+    """ms per block of the 8 W4A4 linears of config 1 at M=4096 (each timed alone, summed; and
+    the block in order, siblings sequential / concurrent)."""
+    b = block_layers(args, dev, args.m, "w4a4", 100)
+    total = b["total"]
+    return {"ms_per_layer": b["per"], "ms_per_block_linears": round(total, 4),
+            "eff_TOPS": round(b["ops"] / (total * 1e-3) / 1e12, 2),
             "linears_ms_per_denoise_step_28_blocks": round(28 * total, 3),
+            "ms_per_block_in_order": round(b["seq"], 4),
+            "ms_per_block_in_order_concurrent_siblings": round(b["conc"], 4),
             "note": "W4A4 linears only (M=4096, no text tokens, no attention / norms): the part of the "
-                    "denoise step this backend replaces"}
+                    "denoise step this backend replaces; ms_per_block_linears = each layer timed alone, "
+                    "summed; *_in_order: the 8 layers back to back in block order, the siblings that read "
+                    "the same input (to_q, to_gate, to_k, to_v; ff.up, ff.gate) one after another or "
+                    "concurrently on side streams"}
 
 
 def w4a16_line(args, dev) -> dict:
-    """the 8 block shapes, W4A16 at M=2304 (768x768 latent), each timed alone."""
-    import torch
-    from krea2_svdquant_amd.kernels.hip import backend
-    out, total, flops_total = {}, 0.0, 0.0
-    for i, (name, n, k) in enumerate(BLOCK_SHAPES):
-        x, _, prep = make_layer(n, k, 2304, args.rank, args.group, dev, seed=200 + 10 * i)
-        for _ in range(3):
-            backend.forward_prepared(x, prep, mode="w4a16")
-        ms = time_avg(lambda: backend.forward_prepared(x, prep, mode="w4a16"), 20)
-        out[name] = round(ms, 4)
-        total += ms
-        flops_total += 2.0 * 2304 * n * k
-        del x, prep
-        torch.cuda.empty_cache()
-    tflops = flops_total / (total * 1e-3) / 1e12
-    return {"ms_per_layer": out, "ms_per_block_linears": round(total, 4), "TFLOPs": round(tflops, 1),
+    """the 8 block shapes, W4A16 at M=2304 (768x768 latent), each timed alone
+    (and the block in order, siblings sequential / concurrent)."""
+    b = block_layers(args, dev, 2304, "w4a16", 200)
+    total = b["total"]
+    tflops = b["ops"] / (total * 1e-3) / 1e12
+    return {"ms_per_layer": b["per"], "ms_per_block_linears": round(total, 4), "TFLOPs": round(tflops, 1),
             "bf16_peak_frac": round(tflops / 2500.0, 4),
+            "ms_per_block_in_order": round(b["seq"], 4),
+            "ms_per_block_in_order_concurrent_siblings": round(b["conc"], 4),
             "note": "W4A16 (bf16 x_hat x in-register dequantized INT4 weights, bf16 MFMA), M=2304, layer = "
-                    "x_hat pass + GEMM with low-rank epilogue"}
+                    "x_hat pass + GEMM with low-rank epilogue; ms_per_block_linears = each layer timed alone, "
+                    "summed; *_in_order as in block_config1"}
 
 
 def lora_line(args, dev) -> dict:
