@@ -319,7 +319,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: every GPU box of this build has a single MI355X, and the "
-              "SVDQuantLinear path has no collective (the multi-GPU layout is described in DESIGN.md).",
+              "SVDQuantLinear path has no collective (sharded, each GPU would run the same kernels on its own rows or output columns).",
               file=sys.stderr)
         return 2
     import torch
