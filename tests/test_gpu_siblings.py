@@ -11,17 +11,22 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _layers(dev, shapes, seed):
+def _layers(dev, shapes, seed, backend):
     from krea2_svdquant_amd.runtime.krea2_standin import random_quantized_state
     from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
     gen = torch.Generator(device=dev).manual_seed(seed)
     return [SVDQuantLinear(random_quantized_state(n, k, rank=32, group_size=64, device=dev, generator=gen),
-                           backend="hip_gfx950") for n, k in shapes]
+                           backend=backend) for n, k in shapes]
 
 
-def test_run_concurrent_matches_sequential_bit_for_bit(dev):
+@pytest.mark.parametrize("backend", ["hip_gfx950", "hip_gfx950_w4a16"])
+def test_run_concurrent_matches_sequential_bit_for_bit(dev, backend):
     from krea2_svdquant_amd.runtime.siblings import run_concurrent
-    mods = _layers(dev, [(768, 512), (512, 512), (256, 512), (256, 512)], seed=21)
+    mods = _layers(dev, [(768, 512), (512, 512), (256, 512), (256, 512)], seed=21, backend=backend)
+    gen_l = torch.Generator(device=dev).manual_seed(5)
+    mods[2].add_lora_adapter((torch.randn(16, 512, device=dev, generator=gen_l) * 0.05).to(torch.bfloat16),
+                             (torch.randn(256, 16, device=dev, generator=gen_l) * 0.05).to(torch.bfloat16),
+                             scale=0.7)
     gen = torch.Generator(device=dev).manual_seed(2)
     kept = []
     for m in (300, 64, 517):                       # ragged row counts, smaller then larger
