@@ -219,23 +219,28 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
 // an operand, so the compiler owns that register.  Issued as inline asm so that the compiler
 // neither orders later LDS reads after it (it cannot tell the pipeline stages apart) nor
 // counts it in its own waits: the kernel waits explicitly.
-// The hazard: gfx9 requires 5 wait states between a VALU instruction that writes an SGPR and a
-// VMEM instruction that reads it.  The compiler inserts them for its own instructions but cannot
-// see the operands of inline asm; under SGPR pressure it restores a spilled base pointer with
-// v_readlane right before a DMA, which then reads a stale address (builds where that happened
-// faulted the GPU).  NOP = true starts the DMA with `s_nop 4` (5 wait states, about 2% of the
-// e3m2 GEMM's time); the kernels whose build restores SGPRs before a DMA (the fused-epilogue
-// variants) set it.  tests/test_dma_hazards.py walks every DMA of the built library back over
-// all its predecessor paths and fails if any can read a VALU-written base SGPR too early.
+// Two hazards the compiler cannot see, because it does not look inside inline asm:
+//  * gfx9 requires 1 wait state between an SALU instruction that writes M0 and an LDS DMA that
+//    reads it.  The compiler writes M0 (`s_mov_b32 m0, sN`) right before the asm block, so every
+//    DMA starts with `s_nop 0`.
+//  * gfx9 requires 5 wait states between a VALU instruction that writes an SGPR and a VMEM
+//    instruction that reads it.  Under SGPR pressure the compiler restores a spilled base pointer
+//    with v_readlane right before a DMA, which then reads a stale address (builds where that
+//    happened faulted the GPU).  NOP = true starts the DMA with `s_nop 4` instead (5 wait states,
+//    about 2% of the e3m2 GEMM's time); the kernels whose build restores SGPRs before a DMA (the
+//    fused-epilogue variants) set it.
+// tests/test_dma_hazards.py walks every DMA of the built library back over all its predecessor
+// paths and fails if one can read a VALU-written SGPR within 5 wait states or an SALU-written M0
+// within 1.
 template <bool NOP = false>
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
   if (NOP) asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
-  else asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+  else asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 template <bool NOP = false>
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
   if (NOP) asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
-  else asm volatile("global_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+  else asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);

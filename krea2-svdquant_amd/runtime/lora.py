@@ -1,41 +1,47 @@
-"""LoRA files onto a quantized transformer: each adapter pair attaches to its ``SVDQuantLinear``.
+"""Attaching the adapters of a LoRA file to the ``SVDQuantLinear`` modules of a transformer.
 
-Mirror of reference ``src/krea2_svdquant/runtime/lora.py``.  Diffusers/PEFT would inject
-adapters into ``nn.Linear`` modules that the SVDQuant checkpoint has already replaced, so the
-pairs are matched to ``SVDQuantLinear`` modules by name and attached with
-``add_lora_adapter``; in this package the adapter then runs fused inside the two kernels
-(down projection in the activation pass, up projection in the GEMM epilogue).
+Public behaviour follows reference ``src/krea2_svdquant/runtime/lora.py:135-187``
+(``load_svdquant_lora_adapters``): every complete down/up pair of the file is attached to the one
+quantized module its name designates, with ``add_lora_adapter`` (here the adapter then runs fused
+inside the two kernels: down projection in the activation pass, up projection in the GEMM
+epilogue), and a report ``{"lora_file", "loaded", "unmatched", "incomplete"}`` is returned.
 
-Behaviour kept from the reference:
+How it works:
 
-* file resolution (``lora.py:37-73``): a file path; a directory with ``weight_name`` or one of
-  the usual file names or exactly one ``*.safetensors``; else a Hub repo id;
-* key grammar (``lora.py:20-34,116-132``): a tensor is a down weight, an up weight or an alpha
-  by its suffix, and the rest of the key names the adapter; an alpha of more than one element
-  counts as absent (``network_alpha`` then defaults to the rank);
-* name matching (``lora.py:87-113``): leading ``transformer.``, ``unet.``,
-  ``base_model.model.``, ``model.``, ``module.``, ``diffusion_model.`` are stripped
-  repeatedly; the rest must equal the module name or end with ``.<module name>``, or, with
-  every ``.`` turned into ``_``, equal it or end with ``_<module name>`` (Kohya names such as
-  ``lora_unet_transformer_blocks_0_attn_to_q``);
-* outcome (``lora.py:152-187``): pairs missing a half are reported as incomplete, names that
-  match nothing as unmatched, a name that matches several modules raises ``ValueError``, and
-  with ``strict`` a file that attaches nothing raises ``ValueError``.
+* ``resolve_lora_file`` turns the argument into one file: the file itself; in a directory the
+  ``weight_name`` given, else the first of ``COMMON_WEIGHT_NAMES`` present, else the only
+  ``*.safetensors``; otherwise the argument is taken as a Hub repo id (reference ``:37-73``).
+* ``parse_key`` splits a tensor key into adapter name and role with one regular expression over
+  the suffix tables; the name is the shortest prefix, so the longest (most specific) suffix wins
+  (``a.lora.down.weight`` names adapter ``a``, not ``a.lora``).  An alpha tensor of more than one
+  element counts as absent, and ``network_alpha`` then defaults to the rank (reference ``:116-132``).
+* ``ModuleIndex`` indexes the model's quantized modules by dotted name and by the name with every
+  ``.`` turned into ``_``.  An adapter name, after the leading ``KNOWN_PREFIXES`` are stripped,
+  designates a module when one of its dotted suffixes (split at ``.``) is the module's name, or one
+  of its underscore suffixes is the module's flat name (Kohya keys such as
+  ``lora_unet_transformer_blocks_0_attn_to_q``; reference ``:87-113``).  Every candidate is one
+  dictionary lookup.
+* A name that designates two modules raises ``ValueError``; with ``strict``, a file that attaches
+  nothing raises ``ValueError``.
 
-One deliberate difference: ``.bin`` / ``.pt`` files are read with
-``torch.load(weights_only=True)``, which accepts tensors and plain containers only.
+``.bin`` / ``.pt`` files are read with ``torch.load(weights_only=True)`` (tensors and plain
+containers only), unwrapping a ``{"state_dict": ...}`` container.
 """
 from __future__ import annotations
 
+import re
 from collections import defaultdict
+from dataclasses import dataclass
 from pathlib import Path
-from typing import Any
+from typing import Any, Iterator, Mapping, Optional
 
 import torch
 from safetensors.torch import load_file
 
 from .linear import SVDQuantLinear
 
+# Format tables: the spellings LoRA files use for their weight files, tensor-key suffixes and
+# framework prefixes.
 COMMON_WEIGHT_NAMES = (
     "pytorch_lora_weights.safetensors",
     "adapter_model.safetensors",
@@ -43,8 +49,6 @@ COMMON_WEIGHT_NAMES = (
     "pytorch_lora_weights.bin",
     "adapter_model.bin",
 )
-# Suffix lists are tried in order; the more specific spellings come before ".down.weight" /
-# ".up.weight", which they also end with.
 DOWN_SUFFIXES = (".lora_A.weight", ".lora.down.weight", ".lora_linear_layer.down.weight",
                  ".lora_down.weight", ".down.weight")
 UP_SUFFIXES = (".lora_B.weight", ".lora.up.weight", ".lora_linear_layer.up.weight",
@@ -52,122 +56,167 @@ UP_SUFFIXES = (".lora_B.weight", ".lora.up.weight", ".lora_linear_layer.up.weigh
 ALPHA_SUFFIXES = (".alpha", ".network_alpha", ".lora_alpha")
 KNOWN_PREFIXES = ("transformer.", "unet.", "base_model.model.", "model.", "module.", "diffusion_model.")
 
+_ROLES = {**{s: "down" for s in DOWN_SUFFIXES}, **{s: "up" for s in UP_SUFFIXES},
+          **{s: "alpha" for s in ALPHA_SUFFIXES}}
+_KEY = re.compile(r"(?P<name>.+?)(?P<suffix>%s)" % "|".join(re.escape(s) for s in _ROLES))
+_PREFIXES = re.compile(r"(?:%s)+" % "|".join(re.escape(p) for p in KNOWN_PREFIXES))
 
-def _resolve_lora_file(lora_path_or_repo_id: str | Path, weight_name: str | None = None) -> Path:
-    path = Path(lora_path_or_repo_id).expanduser()
-    if path.is_file():
-        return path
-    if path.is_dir():
-        if weight_name is not None:
-            chosen = path / weight_name
-            if not chosen.exists():
-                raise FileNotFoundError(chosen)
-            return chosen
-        for name in COMMON_WEIGHT_NAMES:
-            if (path / name).exists():
-                return path / name
-        found = sorted(path.glob("*.safetensors"))
-        if len(found) == 1:
-            return found[0]
-        raise FileNotFoundError(f"could not infer LoRA weight file in {path}; pass weight_name")
-    repo_id = str(lora_path_or_repo_id)
-    if "/" not in repo_id or repo_id.startswith((".", "/", "~")):
-        raise FileNotFoundError(path)
+
+# ----------------------------------------------------------------------------- file
+def _file_in_directory(directory: Path, weight_name: Optional[str]) -> Path:
+    if weight_name is not None:
+        chosen = directory / weight_name
+        if not chosen.exists():
+            raise FileNotFoundError(chosen)
+        return chosen
+    usual = [directory / n for n in COMMON_WEIGHT_NAMES if (directory / n).exists()]
+    if usual:
+        return usual[0]
+    tensors = sorted(directory.glob("*.safetensors"))
+    if len(tensors) != 1:
+        raise FileNotFoundError(f"could not infer the LoRA file in {directory} ({len(tensors)} *.safetensors "
+                                "files, none of the usual names); pass weight_name")
+    return tensors[0]
+
+
+def _file_on_hub(repo_id: str, weight_name: Optional[str]) -> Path:
     try:
         from huggingface_hub import hf_hub_download
     except Exception as exc:  # environment without the Hub client
-        raise ImportError("huggingface_hub is required to load LoRA weights from the Hub") from exc
-    last_error: Exception | None = None
-    for name in ((weight_name,) if weight_name is not None else COMMON_WEIGHT_NAMES):
+        raise ImportError(f"loading LoRA {repo_id!r} from the Hub needs huggingface_hub") from exc
+    error: Optional[Exception] = None
+    for name in (weight_name,) if weight_name is not None else COMMON_WEIGHT_NAMES:
         try:
             return Path(hf_hub_download(repo_id=repo_id, filename=name, repo_type="model"))
-        except Exception as exc:  # try the next usual name
-            last_error = exc
-    raise FileNotFoundError(f"could not find a LoRA weight file in Hub repo {repo_id}") from last_error
+        except Exception as exc:  # the next usual name may exist
+            error = exc
+    raise FileNotFoundError(f"no LoRA weight file found in Hub repo {repo_id}") from error
 
 
-def _load_lora_state_dict(path: Path) -> dict[str, torch.Tensor]:
+def resolve_lora_file(source: str | Path, weight_name: Optional[str] = None) -> Path:
+    """The one LoRA weight file that ``source`` (file, directory or Hub repo id) designates."""
+    path = Path(source).expanduser()
+    if path.is_file():
+        return path
+    if path.is_dir():
+        return _file_in_directory(path, weight_name)
+    repo_id = str(source)
+    looks_local = repo_id.startswith((".", "/", "~")) or "/" not in repo_id
+    if looks_local:
+        raise FileNotFoundError(path)
+    return _file_on_hub(repo_id, weight_name)
+
+
+def read_lora_tensors(path: Path) -> dict[str, torch.Tensor]:
+    """The tensors of a LoRA file (safetensors, or a torch pickle read with weights_only=True)."""
     if path.suffix == ".safetensors":
         return load_file(str(path), device="cpu")
-    state = torch.load(path, map_location="cpu", weights_only=True)
-    if isinstance(state, dict) and isinstance(state.get("state_dict"), dict):
-        state = state["state_dict"]
-    if not isinstance(state, dict):
-        raise TypeError(f"unsupported LoRA checkpoint format: {path}")
-    return {str(k): v for k, v in state.items() if torch.is_tensor(v)}
+    obj = torch.load(path, map_location="cpu", weights_only=True)
+    if isinstance(obj, dict) and isinstance(obj.get("state_dict"), dict):
+        obj = obj["state_dict"]
+    if not isinstance(obj, dict):
+        raise TypeError(f"{path} holds a {type(obj).__name__}, not a dict of LoRA tensors")
+    return {str(k): v for k, v in obj.items() if torch.is_tensor(v)}
 
 
-def _strip_known_prefixes(name: str) -> str:
-    stripped = True
-    while stripped:
-        stripped = False
-        for prefix in KNOWN_PREFIXES:
-            if name.startswith(prefix):
-                name = name[len(prefix):]
-                stripped = True
-    return name
+# ----------------------------------------------------------------------------- keys
+def parse_key(key: str) -> Optional[tuple[str, str]]:
+    """``(adapter name, "down" | "up" | "alpha")`` of a LoRA tensor key, or None."""
+    m = _KEY.fullmatch(key)
+    return (m.group("name"), _ROLES[m.group("suffix")]) if m else None
 
 
-def _module_matches(prefix: str, module_name: str) -> bool:
-    prefix = _strip_known_prefixes(prefix)
-    if prefix == module_name or prefix.endswith("." + module_name):
-        return True
-    flat_prefix, flat_module = prefix.replace(".", "_"), module_name.replace(".", "_")
-    return flat_prefix == flat_module or flat_prefix.endswith("_" + flat_module)
+def canonical_name(name: str) -> str:
+    """``name`` without its leading framework prefixes (all of them, in any order)."""
+    m = _PREFIXES.match(name)
+    return name[m.end():] if m else name
 
 
-def _match_suffix(key: str, suffixes: tuple[str, ...]) -> str | None:
-    for suffix in suffixes:
-        if key.endswith(suffix):
-            return key[: -len(suffix)]
-    return None
+@dataclass
+class AdapterEntry:
+    """One adapter of a LoRA file: its name and the parts the file holds."""
+    name: str
+    down: Optional[torch.Tensor] = None
+    up: Optional[torch.Tensor] = None
+    alpha: Optional[float] = None
+
+    @property
+    def complete(self) -> bool:
+        return self.down is not None and self.up is not None
 
 
-def _split_lora_pairs(state_dict: dict[str, torch.Tensor]) -> dict[str, dict[str, Any]]:
-    """Group a LoRA state dict by adapter name: ``{name: {"down", "up", "alpha"}}`` (each part
-    present when the file has it), in the order the names first appear."""
-    pairs: dict[str, dict[str, Any]] = defaultdict(dict)
-    for key, tensor in state_dict.items():
-        name = _match_suffix(key, DOWN_SUFFIXES)
-        if name is not None:
-            pairs[name]["down"] = tensor
-        name = _match_suffix(key, UP_SUFFIXES)
-        if name is not None:
-            pairs[name]["up"] = tensor
-        name = _match_suffix(key, ALPHA_SUFFIXES)
-        if name is not None:
-            pairs[name]["alpha"] = tensor.item() if tensor.numel() == 1 else None
-    return pairs
+def group_adapters(tensors: Mapping[str, torch.Tensor]) -> dict[str, AdapterEntry]:
+    """The adapters of a LoRA state dict by name, in the order their names first appear."""
+    entries: dict[str, AdapterEntry] = {}
+    for key, tensor in tensors.items():
+        parsed = parse_key(key)
+        if parsed is None:
+            continue
+        name, role = parsed
+        entry = entries.setdefault(name, AdapterEntry(name))
+        if role == "alpha":
+            entry.alpha = float(tensor.item()) if tensor.numel() == 1 else None
+        else:
+            setattr(entry, role, tensor)
+    return entries
 
 
+def _suffixes(name: str, sep: str) -> Iterator[str]:
+    """``name`` and every tail of it that starts right after a ``sep``."""
+    yield name
+    pos = name.find(sep)
+    while pos >= 0:
+        yield name[pos + 1:]
+        pos = name.find(sep, pos + 1)
+
+
+class ModuleIndex:
+    """The ``SVDQuantLinear`` modules of a model, looked up by the names LoRA files give them."""
+
+    def __init__(self, root: torch.nn.Module):
+        self.modules = {n: m for n, m in root.named_modules() if isinstance(m, SVDQuantLinear)}
+        self._order = {n: i for i, n in enumerate(self.modules)}
+        self._dotted = {n: n for n in self.modules}
+        self._flat: dict[str, list[str]] = defaultdict(list)
+        for n in self.modules:
+            self._flat[n.replace(".", "_")].append(n)
+
+    def matches(self, adapter_name: str) -> list[str]:
+        """Module names the adapter name designates (module order)."""
+        key = canonical_name(adapter_name)
+        hits = {self._dotted[s] for s in _suffixes(key, ".") if s in self._dotted}
+        for s in _suffixes(key.replace(".", "_"), "_"):
+            hits.update(self._flat.get(s, ()))
+        return sorted(hits, key=self._order.__getitem__)
+
+
+# ----------------------------------------------------------------------------- loader
 def load_svdquant_lora_adapters(transformer: torch.nn.Module, lora_path_or_repo_id: str | Path, *,
-                                weight_name: str | None = None, scale: float = 1.0,
+                                weight_name: Optional[str] = None, scale: float = 1.0,
                                 strict: bool = True) -> dict[str, Any]:
-    """Attach every adapter pair of a LoRA file to the matching ``SVDQuantLinear`` of ``transformer``.
+    """Attach every adapter of a LoRA file to the ``SVDQuantLinear`` of ``transformer`` it names.
 
-    Returns ``{"lora_file", "loaded", "unmatched", "incomplete"}`` like the reference.
-    ``scale`` multiplies every adapter (``multiplier = scale * alpha / rank``).
+    ``scale`` multiplies every adapter (``multiplier = scale * alpha / rank``).  Returns
+    ``{"lora_file", "loaded", "unmatched", "incomplete"}``: the modules that received an adapter,
+    and the adapter names that designate no module or lack their down or up weight.
     """
-    lora_file = _resolve_lora_file(lora_path_or_repo_id, weight_name=weight_name)
-    pairs = _split_lora_pairs(_load_lora_state_dict(lora_file))
-    modules = {name: mod for name, mod in transformer.named_modules() if isinstance(mod, SVDQuantLinear)}
-    loaded: list[str] = []
-    unmatched: list[str] = []
-    incomplete: list[str] = []
-    for prefix, parts in pairs.items():
-        if "down" not in parts or "up" not in parts:
-            incomplete.append(prefix)
+    path = resolve_lora_file(lora_path_or_repo_id, weight_name=weight_name)
+    index = ModuleIndex(transformer)
+    report: dict[str, Any] = {"lora_file": str(path), "loaded": [], "unmatched": [], "incomplete": []}
+    for entry in group_adapters(read_lora_tensors(path)).values():
+        if not entry.complete:
+            report["incomplete"].append(entry.name)
             continue
-        hits = [name for name in modules if _module_matches(prefix, name)]
-        if not hits:
-            unmatched.append(prefix)
+        targets = index.matches(entry.name)
+        if len(targets) > 1:
+            raise ValueError(f"LoRA adapter {entry.name!r} matches multiple modules: {targets}")
+        if not targets:
+            report["unmatched"].append(entry.name)
             continue
-        if len(hits) > 1:
-            raise ValueError(f"LoRA prefix {prefix!r} matched multiple modules: {hits}")
-        modules[hits[0]].add_lora_adapter(parts["down"], parts["up"], scale=scale,
-                                          network_alpha=parts.get("alpha"))
-        loaded.append(hits[0])
-    if strict and not loaded:
-        raise ValueError(f"no LoRA tensors from {lora_file} matched SVDQuant transformer layers; "
-                         "check that this is a Krea2 transformer LoRA or pass the right weight_name")
-    return {"lora_file": str(lora_file), "loaded": loaded, "unmatched": unmatched, "incomplete": incomplete}
+        index.modules[targets[0]].add_lora_adapter(entry.down, entry.up, scale=scale, network_alpha=entry.alpha)
+        report["loaded"].append(targets[0])
+    if strict and not report["loaded"]:
+        raise ValueError(f"no LoRA tensors in {path} attach to an SVDQuantLinear of this model "
+                         f"({len(report['unmatched'])} unmatched, {len(report['incomplete'])} incomplete adapters); "
+                         "is it a LoRA for this transformer, and is weight_name right?")
+    return report

@@ -114,3 +114,29 @@ def e3m2_rows(buf: np.ndarray, r: int, k: int) -> np.ndarray:
     qp = buf[:t * 2 * rp * 16].reshape(t, 2, rp, 16)[:, :, :r]
     pp = buf[t * 2 * rp * 16:].reshape(t, 2, rp, 8)[:, :, :r]
     return np.concatenate([qp, pp], axis=-1)
+
+
+def e3m2_codes_of(buf: np.ndarray, r: int, k: int, rows=None) -> np.ndarray:
+    """Integer codes [R', K] decoded from a flat planar e3m2 operand (the inverse of e3m2_planar,
+    through the format's own decoding e3m2_value), for all rows or the listed ``rows``.  Each
+    3-byte run of a row's 24 bytes holds 4 little-endian 6-bit fields."""
+    v24 = e3m2_rows(buf, r, k)                       # [K/64, 2, R, 24]
+    if rows is not None:
+        v24 = v24[:, :, np.asarray(rows)]
+    b = v24.reshape(*v24.shape[:3], 8, 3).astype(np.uint32)
+    u = b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16)              # [K/64, 2, R', 8]
+    fields = np.stack([(u >> (6 * i)) & 63 for i in range(4)], axis=-1).reshape(*u.shape[:3], 32)
+    vals = e3m2_value(np.arange(64))
+    exact = (vals == np.rint(vals)) & (vals >= -8) & (vals <= 7)
+    table = np.where(exact, np.rint(vals), 99).astype(np.int8)    # 99: not an INT4 code
+    t = k // 64
+    return table[fields].transpose(2, 0, 1, 3).reshape(-1, t * 64)
+
+
+def sx_pairs_ok(sx_pairs: torch.Tensor, sx_ref: np.ndarray, rows=None) -> bool:
+    """sx pairs [K/G, M] (u32 bf16 | bf16 << 16) against the oracle's bf16 scales [M, K/G]."""
+    got = sx_pairs.cpu().numpy().view(np.uint32).T
+    if rows is not None:
+        got = got[np.asarray(rows)]
+    bits = nm.bf16_bits(sx_ref).astype(np.uint32)
+    return bool(np.array_equal(got, bits | (bits << 16)))

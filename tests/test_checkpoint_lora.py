@@ -139,21 +139,29 @@ def test_lora_key_styles(tmp_path, prefix, down_sfx, up_sfx):
 
 def test_lora_split_pairs_grammar():
     t = torch.zeros(1)
-    pairs = lr._split_lora_pairs({
+    entries = lr.group_adapters({
         "a.lora.down.weight": t, "a.lora.up.weight": t,        # ".lora.down" wins over ".down"
         "b.lora_A.weight": t,                                  # incomplete
         "c.alpha": torch.tensor([1.0, 2.0]),                   # multi-element alpha -> None
         "d.lora_alpha": torch.tensor(3.0),
         "unrelated.weight": t,
     })
-    assert list(pairs) == ["a", "b", "c", "d"]
-    assert set(pairs["a"]) == {"down", "up"} and set(pairs["b"]) == {"down"}
-    assert pairs["c"] == {"alpha": None} and pairs["d"] == {"alpha": 3.0}
-    assert lr._strip_known_prefixes("transformer.model.module.x.transformer.y") == "x.transformer.y"
-    assert lr._strip_known_prefixes("transformer_blocks.0") == "transformer_blocks.0"
-    assert lr._module_matches("lora_te_x_blocks_0_to_q", "blocks.0.to_q")
-    assert not lr._module_matches("blocks.10.to_q", "blocks.0.to_q")
-    assert not lr._module_matches("xblocks.0.to_q", "blocks.0.to_q")
+    assert list(entries) == ["a", "b", "c", "d"]
+    assert entries["a"].complete and entries["a"].alpha is None
+    assert entries["b"].down is not None and entries["b"].up is None and not entries["b"].complete
+    assert entries["c"].alpha is None and entries["c"].down is None and entries["d"].alpha == 3.0
+    assert lr.parse_key("x.lora_linear_layer.down.weight") == ("x", "down")
+    assert lr.parse_key("x.weight") is None
+    assert lr.canonical_name("transformer.model.module.x.transformer.y") == "x.transformer.y"
+    assert lr.canonical_name("transformer_blocks.0") == "transformer_blocks.0"
+    root = nn.Module()
+    root.blocks = nn.ModuleList([nn.Module() for _ in range(11)])
+    root.blocks[0].to_q = _svdq()
+    root.blocks[10].to_q = _svdq()
+    index = lr.ModuleIndex(root)
+    assert index.matches("lora_te_x_blocks_0_to_q") == ["blocks.0.to_q"]
+    assert index.matches("blocks.10.to_q") == ["blocks.10.to_q"]
+    assert index.matches("xblocks.0.to_q") == []
 
 
 def test_lora_report_unmatched_incomplete_and_errors(tmp_path):
@@ -196,17 +204,17 @@ def test_lora_file_resolution(tmp_path):
     d = tmp_path / "dir"
     d.mkdir()
     save_file(pair, d / "only_one.safetensors")
-    assert lr._resolve_lora_file(d) == d / "only_one.safetensors"
+    assert lr.resolve_lora_file(d) == d / "only_one.safetensors"
     save_file(pair, d / "second.safetensors")
     with pytest.raises(FileNotFoundError, match="could not infer"):
-        lr._resolve_lora_file(d)
+        lr.resolve_lora_file(d)
     save_file(pair, d / "adapter_model.safetensors")
-    assert lr._resolve_lora_file(d) == d / "adapter_model.safetensors"
-    assert lr._resolve_lora_file(d, weight_name="second.safetensors") == d / "second.safetensors"
+    assert lr.resolve_lora_file(d) == d / "adapter_model.safetensors"
+    assert lr.resolve_lora_file(d, weight_name="second.safetensors") == d / "second.safetensors"
     with pytest.raises(FileNotFoundError):
-        lr._resolve_lora_file(d, weight_name="absent.safetensors")
+        lr.resolve_lora_file(d, weight_name="absent.safetensors")
     with pytest.raises(FileNotFoundError):
-        lr._resolve_lora_file(tmp_path / "no_such_file.safetensors")
+        lr.resolve_lora_file(tmp_path / "no_such_file.safetensors")
     # .bin files are read with weights_only=True, including a {"state_dict": ...} wrapper
     b = tmp_path / "bin"
     b.mkdir()

@@ -1,15 +1,22 @@
-"""No global->LDS DMA of the built library can read a base SGPR that a VALU wrote too recently.
+"""No global->LDS DMA of the built library can read an SGPR or M0 that was written too recently.
 
-gfx9 requires 5 wait states between a VALU instruction that writes an SGPR and a VMEM instruction
-that reads it.  The GEMMs issue their global->LDS DMA (`global_load_lds_dword[x4]`) as inline asm,
-whose operands the compiler's hazard recognizer does not see; under SGPR pressure the compiler
-restores a spilled base pointer with `v_readlane` right before such a DMA, which then reads a
-stale address.  Builds in which that happened faulted the GPU.  Kernels whose builds do that start
-each DMA with `s_nop 4`.  This test disassembles the gfx950 code objects of the library built in
-this repository (llvm-objdump on our own build) and walks back from every LDS DMA over every
-predecessor path (fall-through and branches) for 5 wait states (`s_nop N` counts N + 1): no VALU
-instruction on any path may name one of the DMA's base SGPRs, and no path may reach the start of
-the function.  A planted hazard in a small hand-written listing must be caught.
+The GEMMs issue their global->LDS DMA (`global_load_lds_dword[x4]`) as inline asm, whose operands
+the compiler's hazard recognizer does not see.  Two gfx9 rules apply to it:
+
+* 5 wait states between a VALU instruction that writes an SGPR and a VMEM instruction that reads
+  it.  Under SGPR pressure the compiler restores a spilled base pointer with `v_readlane` right
+  before such a DMA, which then reads a stale address; builds in which that happened faulted the
+  GPU.  Kernels whose builds do that start each DMA with `s_nop 4`.
+* 1 wait state between an SALU instruction that writes M0 and an LDS DMA (which reads its LDS
+  address from M0).  The compiler sets M0 with `s_mov_b32 m0, ...` right before the asm block;
+  every DMA starts with at least `s_nop 0`.
+
+This test disassembles the gfx950 code objects of the library built in this repository
+(llvm-objdump on our own build) and walks back from every LDS DMA over every predecessor path
+(fall-through and branches): within 5 wait states (`s_nop N` counts N + 1) no VALU instruction may
+name one of the DMA's base SGPRs or M0, within 1 wait state no SALU instruction may write M0, and
+no path may reach the start of the function.  Planted hazards of both kinds in a small
+hand-written listing must be caught.
 """
 import re
 import struct
@@ -73,6 +80,13 @@ def _functions(lines: list[str]) -> list[dict]:
     return funcs
 
 
+def _writes_m0(text: str) -> bool:
+    """An SALU instruction whose destination is M0 (s_mov_b32 m0, ...; s_add_u32 m0, ...)."""
+    parts = text.replace(",", " ").split()
+    return (parts[0].startswith("s_") and not parts[0].startswith(("s_nop", "s_waitcnt", "s_barrier"))
+            and len(parts) > 1 and parts[1] == "m0")
+
+
 def dma_hazards(func: dict) -> tuple[int, list[str]]:
     """(number of LDS DMAs, descriptions of the hazardous ones) of one function."""
     ins = func["ins"]
@@ -92,7 +106,7 @@ def dma_hazards(func: dict) -> tuple[int, list[str]]:
         if not text.startswith("global_load_lds"):
             continue
         count += 1
-        base = _sregs(text.split()[-1].rstrip(","))
+        base = _sregs(text.split()[-1].rstrip(",")) | {"m0"}
         stack, seen, reason = [(p, 0) for p in preds[i]] or [(None, 0)], set(), None
         while stack and reason is None:
             j, waits = stack.pop()
@@ -108,8 +122,13 @@ def dma_hazards(func: dict) -> tuple[int, list[str]]:
                 w = int(t.split()[1], 0) + 1
             else:
                 w = 1
-                if op.startswith("v_") and any(_sregs(x.rstrip(",")) & base for x in t.split()[1:]):
+                if op.startswith("v_") and any(
+                        (_sregs(x.rstrip(",")) | ({"m0"} if x.rstrip(",") == "m0" else set())) & base
+                        for x in t.split()[1:]):
                     reason = f"{t!r} {waits} wait states before"
+                    break
+                if waits < 1 and _writes_m0(t):
+                    reason = f"{t!r} (SALU write of M0) {waits} wait states before"
                     break
             if waits + w < 5:
                 if not preds[j]:
@@ -130,22 +149,35 @@ PLANTED = """0000000000001000 <k>:
 \tglobal_load_lds_dwordx4 v2, s[4:5] // 000000001018: 0
 \ts_nop 4 // 00000000101C: 0
 \tglobal_load_lds_dwordx4 v3, s[4:5] // 000000001020: 0
-\ts_endpgm // 000000001024: 0
+\ts_mov_b32 m0, s9 // 000000001024: 0
+\tglobal_load_lds_dword v4, s[4:5] // 000000001028: 0
+\ts_add_u32 m0, s9, 0x400 // 00000000102C: 0
+\ts_nop 0 // 000000001030: 0
+\tglobal_load_lds_dword v5, s[4:5] // 000000001034: 0
+\ts_nop 3 // 000000001038: 0
+\tv_readfirstlane_b32 m0, v6 // 00000000103C: 0
+\ts_nop 3 // 000000001040: 0
+\tglobal_load_lds_dword v7, s[4:5] // 000000001044: 0
+\ts_endpgm // 000000001048: 0
 """
 
 
-def test_hazard_walk_catches_a_planted_hazard():
+def test_hazard_walk_catches_planted_hazards():
     (func,) = _functions(PLANTED.splitlines())
     count, bad = dma_hazards(func)
-    assert count == 2
-    # the first DMA: v_readlane wrote s5 three wait states earlier on the fall-through path; the
-    # second DMA is 5 wait states after it
-    assert len(bad) == 1 and "v2, s[4:5]" in bad[0]
+    assert count == 5
+    # v2: v_readlane wrote s5 three wait states earlier on the fall-through path; v3: 5 wait
+    # states after it, clean; v4: the SALU write of M0 right before it; v5: one s_nop 0 after the
+    # M0 write, clean; v7: a VALU write of M0 four wait states before
+    assert len(bad) == 3, bad
+    assert "v2, s[4:5]" in bad[0] and "v_readlane" in bad[0]
+    assert "v4, s[4:5]" in bad[1] and "SALU write of M0" in bad[1]
+    assert "v7, s[4:5]" in bad[2] and "v_readfirstlane_b32 m0" in bad[2]
 
 
 @pytest.mark.skipif(not LIB.exists() or not OBJDUMP.exists(),
                     reason="needs the built library and ROCm's llvm-objdump")
-def test_no_lds_dma_reads_a_valu_written_base_too_early():
+def test_no_lds_dma_reads_a_recently_written_sgpr_or_m0():
     code_objects = _gfx950_code_objects(LIB)
     assert code_objects, "no gfx950 code object in the library"
     dma, bad = 0, []
