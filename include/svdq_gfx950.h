@@ -105,6 +105,27 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
                    int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
                    float* mid, int splits, hipStream_t stream);
 
+/* Largest split-partial buffer of svdq_act_quant_noalloc, in floats (16 MiB): S * M * RTp must
+ * not exceed it (S from svdq_act_quant_workspace). */
+#define SVDQ_ACT_NOALLOC_MAX_FLOATS (4 << 20)
+
+/* svdq_act_quant without any allocation or caller workspace.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, flags, arithmetic and
+ * outputs as svdq_act_quant, except that `midp` is only the finalized GEMM operand (bf16
+ * [M, 2, RTp], i.e. the head of svdq_act_quant's workspace, M * RTp floats' worth of bytes);
+ * the S split partials live in a file-scope device array of SVDQ_ACT_NOALLOC_MAX_FLOATS floats
+ * that each GPU holds until the process ends.  Calls whose partials do not fit return
+ * SVDQ_ERR_SHAPE.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, or threads) race and must be serialized by the caller.  The array of the
+ * calling thread's current device is used, so that device must own `stream` and the buffers.
+ * The entry point calls no hipMalloc / hipFree; its first call on a device looks the array up
+ * (hipGetSymbolAddress). */
+int svdq_act_quant_noalloc(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
+                           const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
+                           int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
+                           float* midp, hipStream_t stream);
+
 /* Per-layer weight-scale operand of svdq_w4a4_gemm: swp[g][n] = bf16 hi | bf16 lo << 16 with
  * hi + lo == float(sw[n][g]) exactly (times 1/256 for SVDQ_OPERAND_I8), group-major.  No
  * reference counterpart: it splits the checkpoint's fp16 weight_scales (runtime/load.py:116)

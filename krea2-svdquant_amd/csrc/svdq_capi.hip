@@ -1,6 +1,7 @@
 // extern "C" entry points of libsvdq_gfx950.so: argument validation and kernel launch.
 #include <stdarg.h>
 #include <stdio.h>
+#include <mutex>
 #include <string>
 
 #include "../../include/svdq_gfx950.h"
@@ -68,10 +69,17 @@ int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int6
   return ok();
 }
 
-int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
-                   const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
-                   int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
-                   float* mid, int splits, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The activation pass behind svdq_act_quant and svdq_act_quant_noalloc: `head` receives the
+// finalized GEMM operand [M, 2, RTp] bf16, `part` holds the `splits` f32 partials [splits, M, RTp]
+// (every entry of rows < M written by the act kernel before the finalize kernel reads it).
+int act_quant_run(const void* x, int64_t ldx, const float* srs, const void* l2, int r, const void* lora_down,
+                  int rl, const float* lora_mult, int M, int K, int group, int RTp, unsigned flags, void* qa,
+                  void* sx, void* qx, void* xhat, int64_t ldxh, float* head, float* part, int splits,
+                  hipStream_t stream) {
   const unsigned known = SVDQ_ACT_PACKED | SVDQ_ACT_XHAT | SVDQ_ACT_EXACT_DIV | SVDQ_ACT_OPERAND_E4M3 |
                          SVDQ_ACT_OPERAND_I8 | SVDQ_ACT_SX_PAIRS | SVDQ_ACT_OPERAND_E3M2;
   if (flags & ~known) return fail(SVDQ_ERR_ARG, "act_quant: unknown flags 0x%x", flags);
@@ -91,20 +99,17 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
   if (RTp % 32 || RTp < r + rl) return fail(SVDQ_ERR_SHAPE, "act_quant: RTp=%d (r=%d rl=%d)", RTp, r, rl);
   const int nt = mid_tiles(r, rl);
   if (nt > 4) return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: ceil(r/32)+ceil(rl/32)=%d > 4", nt);
-  if (!x || !srs || !l2 || !mid || (rl > 0 && (!lora_down || !lora_mult)) || (quant && (!qa || !sx)) ||
+  if (!x || !srs || !l2 || !head || !part || (rl > 0 && (!lora_down || !lora_mult)) || (quant && (!qa || !sx)) ||
       (packed && !qx) || (want_xhat && !xhat))
     return fail(SVDQ_ERR_ARG, "act_quant: null pointer");
   if (ldx < K || ldx % 8 || (want_xhat && (ldxh < K || ldxh % 8)))
     return fail(SVDQ_ERR_ALIGN, "act_quant: ldx=%lld ldxh=%lld must be >= K and multiples of 8",
                 (long long)ldx, (long long)ldxh);
-  if (!aligned16(x) || !aligned16(srs) || !aligned16(l2) || !aligned16(mid) ||
+  if (!aligned16(x) || !aligned16(srs) || !aligned16(l2) || !aligned16(head) || !aligned16(part) ||
       (rl > 0 && !aligned16(lora_down)) || (quant && !aligned16(qa)) || (packed && !aligned16(qx)) ||
       (pairs && reinterpret_cast<uintptr_t>(sx) % 4) ||
       (want_xhat && !aligned16(xhat)))
     return fail(SVDQ_ERR_ALIGN, "act_quant: device pointers must be 16-byte aligned");
-  const int expect = svdq::act_splits(M, K, group);
-  if (splits != expect) return fail(SVDQ_ERR_ARG, "act_quant: splits=%d, workspace says %d", splits, expect);
-
   svdq::ActParams p{};
   p.x = static_cast<const uint16_t*>(x);
   p.ldx = ldx;
@@ -122,7 +127,7 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
   p.sx = static_cast<uint16_t*>(sx);
   p.xhat = static_cast<uint16_t*>(xhat);
   p.ldxh = ldxh;
-  p.mid = mid + (int64_t)M * RTp;   // split partials after the finalized operand
+  p.mid = part;
   const int ngroups = K / group;
   p.gps = (ngroups + splits - 1) / splits;
   p.exact = (flags & SVDQ_ACT_EXACT_DIV) ? 1 : 0;
@@ -130,8 +135,74 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
   if (int e = launched(svdq::launch_act(p, group, nt, e4m3 ? 1 : (i8 ? 2 : (e3m2 ? 3 : 0)), want_xhat, splits, stream),
                        "act_quant"))
     return e;
-  return launched(svdq::launch_mid_finalize(p.mid, splits, M, RTp, reinterpret_cast<uint16_t*>(mid), stream),
+  return launched(svdq::launch_mid_finalize(p.mid, splits, M, RTp, reinterpret_cast<uint16_t*>(head), stream),
                   "act_quant (mid)");
+}
+
+// Device scratch of svdq_act_quant_noalloc: the activation pass's split partials.  Each GPU holds
+// its own copy from code-object load until the process ends; the host side reaches it only
+// through the per-device address hipGetSymbolAddress returns (the array's name is a host-side
+// stand-in, not a device address).
+constexpr int64_t kScratchFloats = SVDQ_ACT_NOALLOC_MAX_FLOATS;   // 16 MiB
+__device__ __align__(256) float scratch[kScratchFloats];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch[kMaxDevices] = {};
+
+// The scratch address on the calling thread's current device, looked up once per device.
+int device_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(SVDQ_ERR_LAUNCH, "act_quant_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(SVDQ_ERR_UNSUPPORTED, "act_quant_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(SVDQ_ERR_LAUNCH, "act_quant_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return SVDQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
+                   const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
+                   int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
+                   float* mid, int splits, hipStream_t stream) {
+  if (M > 0 && group > 0 && K > 0 && K % group == 0) {
+    const int expect = svdq::act_splits(M, K, group);
+    if (splits != expect) return fail(SVDQ_ERR_ARG, "act_quant: splits=%d, workspace says %d", splits, expect);
+  }
+  float* part = mid ? mid + (int64_t)(M > 0 ? M : 0) * (RTp > 0 ? RTp : 0) : nullptr;   // partials after the head
+  return act_quant_run(x, ldx, srs, l2, r, lora_down, rl, lora_mult, M, K, group, RTp, flags, qa, sx, qx, xhat,
+                       ldxh, mid, part, splits, stream);
+}
+
+int svdq_act_quant_noalloc(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
+                           const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
+                           int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
+                           float* midp, hipStream_t stream) {
+  if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant_noalloc: M=%d", M);
+  if (int e = check_group(group, K)) return e;
+  if (RTp <= 0 || RTp % 32) return fail(SVDQ_ERR_SHAPE, "act_quant_noalloc: RTp=%d must be a positive multiple of 32", RTp);
+  const int splits = svdq::act_splits(M, K, group);
+  const int64_t need = (int64_t)splits * M * RTp;
+  if (need > kScratchFloats)
+    return fail(SVDQ_ERR_SHAPE,
+                "act_quant_noalloc: the split partials need %lld floats (%d splits x M=%d x RTp=%d), more than the "
+                "%lld-float device scratch; use svdq_act_quant with a workspace",
+                (long long)need, splits, M, RTp, (long long)kScratchFloats);
+  float* part = nullptr;
+  if (int e = device_scratch(&part)) return e;
+  return act_quant_run(x, ldx, srs, l2, r, lora_down, rl, lora_mult, M, K, group, RTp, flags, qa, sx, qx, xhat,
+                       ldxh, midp, part, splits, stream);
 }
 
 static int gemm_common_checks(const char* who, const void* qw, const void* sw, const void* mid,

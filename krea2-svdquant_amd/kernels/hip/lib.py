@@ -24,6 +24,9 @@ SVDQ_ACT_OPERAND_I8 = 16
 SVDQ_ACT_SX_PAIRS = 32
 SVDQ_ACT_OPERAND_E3M2 = 64
 
+# split-partial floats of the device scratch of svdq_act_quant_noalloc (SVDQ_ACT_NOALLOC_MAX_FLOATS)
+SVDQ_ACT_NOALLOC_MAX_FLOATS = 4 << 20
+
 # epilogue ops of the *_gemm_epi entry points
 SVDQ_EPI_NONE = 0
 SVDQ_EPI_MUL_SIGMOID = 1
@@ -47,6 +50,8 @@ SIGNATURES = {
     "svdq_act_quant_workspace": (_I, [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_L)]),
     "svdq_act_quant": (_I, [_P, _L, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _U, _P, _P, _P, _P, _L,
                             _P, _I, _P]),
+    "svdq_act_quant_noalloc": (_I, [_P, _L, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _U, _P, _P, _P, _P, _L,
+                                    _P, _P]),
     "svdq_prepare_weight_scales": (_I, [_P, _P, _I, _I, _I, _P]),
     "svdq_prepare_weight_operand": (_I, [_P, _P, _I, _I, _I, _P]),
     "svdq_w4a4_gemm": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),

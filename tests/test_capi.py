@@ -121,3 +121,23 @@ def test_gemm_epilogue_ops_rejected_before_any_launch(fn, epi, out_f32, aux, lda
         lib.call(fn, *args, epi, aux_p, ldaux, vec_p, None)
     assert ei.value.status == status and needle in str(ei.value)
 
+
+
+@pytest.mark.parametrize("m,k,g,rtp,status,needle", [
+    (40000, 6144, 64, 128, -2, "device scratch"),   # 1 split x 40000 x 128 floats > 4 Mi floats
+    (0, 6144, 64, 32, -1, "M=0"),
+    (4096, 6144, 64, 40, -2, "RTp=40"),
+    (4096, 6144, 48, 32, -4, "group size 48"),
+])
+def test_act_quant_noalloc_rejects_before_any_launch(m, k, g, rtp, status, needle):
+    """The no-allocation entry point refuses a split-partial buffer beyond its device scratch
+    (SVDQ_ACT_NOALLOC_MAX_FLOATS) and bad shapes on the host, before it touches the GPU."""
+    fake = ctypes.c_void_p(0x1000)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_act_quant_noalloc", fake, k, fake, fake, 32, None, 0, None, m, k, g, rtp,
+                 lib.SVDQ_ACT_OPERAND_E3M2 | lib.SVDQ_ACT_SX_PAIRS, fake, fake, None, None, k, fake, None)
+    assert ei.value.status == status and needle in str(ei.value)
+    splits = ctypes.c_int()
+    if m > 0 and rtp % 32 == 0 and g == 64:
+        lib.call("svdq_act_quant_workspace", m, k, g, rtp, ctypes.byref(splits), None)
+        assert splits.value * m * rtp > lib.SVDQ_ACT_NOALLOC_MAX_FLOATS
