@@ -71,8 +71,10 @@ def parse():
     ap.add_argument("--no-block", action="store_true", help="skip the config 1-4 extra lines")
     ap.add_argument("--lines", default="block,w4a16,lora,denoise",
                     help="extra lines to run (comma list of block, w4a16, lora, denoise)")
-    ap.add_argument("--pmc-pass", action="store_true",
-                    help="counter pass for rocprofv3: one copy kernel of known size, then GEMM launches")
+    ap.add_argument("--pmc-pass", nargs="?", const="w4a4", default=None, choices=["w4a4", "w4a16"],
+                    help="counter pass for rocprofv3: one copy kernel of known size, then 3 launches of the "
+                         "config 1 ff.up W4A4 GEMM and 3 activation passes (w4a4), or of the config 2 ff.up "
+                         "W4A16 GEMM at M=2304 (w4a16)")
     return ap.parse_args()
 
 
@@ -80,9 +82,10 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_avg(fn, iters: int, reps: int = 3) -> float:
-    """ms per call of ``fn``: HIP events around ``iters`` back-to-back calls on torch's current
-    stream (where the ops launch), so host dispatch overlaps the GPU work; median of ``reps``."""
+def time_reps(fn, iters: int, reps: int = 3) -> list[float]:
+    """ms per call of ``fn`` for each of ``reps`` repetitions: HIP events around ``iters``
+    back-to-back calls on torch's current stream (where the ops launch), so host dispatch
+    overlaps the GPU work."""
     import torch
     out = []
     for _ in range(reps):
@@ -94,7 +97,23 @@ def time_avg(fn, iters: int, reps: int = 3) -> float:
         b.record()
         torch.cuda.synchronize()
         out.append(a.elapsed_time(b) / iters)
-    return statistics.median(out)
+    return out
+
+
+def time_avg(fn, iters: int, reps: int = 3) -> float:
+    """Median over ``reps`` of ``time_reps``."""
+    return statistics.median(time_reps(fn, iters, reps))
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints), from /proc/cpuinfo."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def make_layer(n: int, k: int, m: int, r: int, g: int, dev, seed: int):
@@ -142,16 +161,28 @@ def cpu_baseline(ds, x_dev, reps: int) -> dict:
         sim.sim_forward_torch(x, st)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
+    # the A4 activation step the sim lacks: the reference's torch quantizer ops on all threads,
+    # and the numpy restatement on one thread
+    sim.quantize_activations_torch(x[:64], st)
+    tq_torch = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        sim.quantize_activations_torch(x, st)
+        tq_torch.append(time.perf_counter() - t0)
+    tqt = statistics.median(tq_torch)
     xq = x.float().numpy()
     t0 = time.perf_counter()
     sim.quantize_activations(xq, st)
     tq = time.perf_counter() - t0
-    return {"value": round(2.0 * m * n * k / t / 1e12, 4), "unit": "TOPS", "cores": torch.get_num_threads(),
-            "kind": "port",
+    threads = torch.get_num_threads()
+    return {"value": round(2.0 * m * n * k / t / 1e12, 4), "unit": "TOPS", "cores": threads,
+            "kind": "port", "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
             "sample": f"whole layer M={m} K={k} N={n}: oracle sim_forward_torch (restated reference pytorch_sim, "
-                      f"bf16 CPU torch), median of {reps} after warm-up = {t:.3f} s per forward; restated A4 "
-                      f"activation quantizer (numpy, 1 thread) {tq:.3f} s; os.cpu_count()={os.cpu_count()}",
-            "act_quant_s": round(tq, 3)}
+                      f"bf16 CPU torch, {threads} threads on {cpu_model()}), median of {reps} after warm-up = "
+                      f"{t:.3f} s per forward; A4 activation step (not part of the sim): the reference's torch "
+                      f"quantizer ops (quantize_activations_torch, {threads} threads) median of 3 = {tqt:.3f} s, "
+                      f"numpy restatement on 1 thread {tq:.3f} s",
+            "act_quant_s": round(tqt, 4), "act_quant_numpy_1thread_s": round(tq, 3)}
 
 
 BLOCK_ORDER = [("to_q", "to_gate", "to_k", "to_v"), ("to_out.0",), ("ff.up", "ff.gate"), ("ff.down",)]
@@ -315,6 +346,24 @@ def denoise_line(args, dev) -> dict:
                     "around each linear of one forward"}
 
 
+def pmc_pass_w4a16(args, dev) -> int:
+    """Counter pass of the config 2 ff.up W4A16 GEMM (M=2304): a copy of known size, then 3 GEMMs."""
+    import torch
+    from krea2_svdquant_amd.kernels.hip import ops
+    x, _, prep = make_layer(16384, 6144, 2304, args.rank, args.group, dev, seed=200)
+    _, _, _, xhat, mid = ops.act_quant(x, prep.srs, prep.l2, None, None, args.group, prep.rtp, ops.OPERAND_NONE,
+                                       False, True, False)
+    src = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    for _ in range(3):
+        ops.w4a16_gemm(xhat, prep.qweight, prep.weight_scales, mid, prep.l1cat, None, args.group, False)
+    torch.cuda.synchronize()
+    log("pmc pass done: 1 copy of 256 MiB, 3 W4A16 GEMM launches (ff.up, M=2304)")
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -327,6 +376,8 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     m, k, n, r, g = args.m, args.k, args.n, args.rank, args.group
+    if args.pmc_pass == "w4a16":
+        return pmc_pass_w4a16(args, dev)
     log(f"device {torch.cuda.get_device_name(dev)}; building state M={m} K={k} N={n} r={r} g={g}")
     x, ds, prep = make_layer(n, k, m, r, g, dev, seed=1)
     opc = ops.OPERAND_NAMES[args.operand]
@@ -337,7 +388,7 @@ def main() -> int:
     def gemm():
         return ops.w4a4_gemm(qa, sx, wop, wsp, mid, prep.l1cat, None, g, opc, False)
 
-    if args.pmc_pass:
+    if args.pmc_pass == "w4a4":
         # copy kernel of known size first (calibrates FETCH_SIZE / WRITE_SIZE), then the GEMM
         src = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -354,6 +405,20 @@ def main() -> int:
 
     def step():
         return backend.forward_prepared(x, prep, mode="w4a4", operand=args.operand)
+
+    def act():
+        return ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False, True)
+
+    # Per-kernel launch durations first, each kernel back to back on the stream it runs on (5
+    # repetitions of max(steps, 20) launches).  Running them before the timed steps also brings
+    # the GPU from idle to its sustained clock, which takes tens of milliseconds of work.
+    for _ in range(3):
+        act(), gemm()
+    it = max(args.steps, 20)
+    act_reps = time_reps(act, it, 5)
+    gemm_reps = time_reps(gemm, it, 5)
+    ms_act, ms_gemm = statistics.median(act_reps), statistics.median(gemm_reps)
+    log(f"act {ms_act:.4f} ms, gemm {ms_gemm:.4f} ms (medians of 5 x {it})")
 
     log(f"warmup {args.warmup}")
     for _ in range(args.warmup):
@@ -372,14 +437,6 @@ def main() -> int:
     ms = a.elapsed_time(b) / args.steps
     log(f"{ms:.4f} ms/step (HIP events; host wall {wall:.4f} ms/step)")
 
-    # per-kernel launch durations, each kernel launched back to back on the stream it runs on
-    def act():
-        return ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False, True)
-    for _ in range(3):
-        act(), gemm()
-    ms_act = time_avg(act, args.steps)
-    ms_gemm = time_avg(gemm, args.steps)
-    log(f"act {ms_act:.4f} ms, gemm {ms_gemm:.4f} ms")
     flops = 2.0 * m * n * k
     splits = mid.shape[0] - 1
     # x, srs, l2 read; codes, scales, split partials written; partials re-read and the final
@@ -406,6 +463,9 @@ def main() -> int:
                                "epilogue, bf16 out)",
                    "M": m, "K": k, "N": n, "rank": r, "group": g, "operand": args.operand},
         "kernels": {"act_quant_ms": round(ms_act, 4), "w4a4_gemm_ms": round(ms_gemm, 4),
+                    "act_quant_ms_min_max": [round(min(act_reps), 4), round(max(act_reps), 4)],
+                    "w4a4_gemm_ms_min_max": [round(min(gemm_reps), 4), round(max(gemm_reps), 4)],
+                    "step_minus_kernels_us": round((ms - ms_act - ms_gemm) * 1e3, 1),
                     "act_quant_GBps": round(act_bytes / (ms_act * 1e-3) / 1e9, 1),
                     "act_quant_hbm_frac": round(act_bytes / (ms_act * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "step_host_wall_ms": round(wall, 4)},

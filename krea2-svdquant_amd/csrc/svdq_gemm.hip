@@ -72,8 +72,10 @@ __device__ __forceinline__ u32x4 epi_chunk(const GemmParams& p, u32x4 v, int m, 
 template <bool OUT_F32, bool EPI = false>
 __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2], int m0, int n0,
                                          int lr, int h, uint8_t* stage, const uint8_t* lmid = nullptr,
-                                         const uint8_t* ll1 = nullptr, int wr = 0, int wc = 0) {
+                                         const uint8_t* ll1 = nullptr, int wr = 0, int wc = 0,
+                                         int mlim = 0x7FFFFFFF) {
   const int RTp = p.RTp;
+  const int mend = min(p.M, mlim);   // rows m >= mend are not stored (past M, or another wave's)
   if (lmid != nullptr) {
     // RTp == 32, operands prefetched into LDS by the GEMM's last stage: the tile's mid rows
     // (128 bytes: hi plane, lo plane; 16-byte chunk c of row r at c ^ ((r >> 1) & 7)) and l1cat
@@ -152,7 +154,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (m >= p.M) continue;
+          if (m >= mend) continue;
           float v = acc[i][j][r] + bv[j];
           if (OUT_F32) {
             reinterpret_cast<float*>(p.y)[(long)m * p.ldy + n] = v;
@@ -196,7 +198,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
       const int pos = c ^ ((row >> 2) & 1 ? CPR / 2 : 0);
       u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * (64 * ES) + pos * 16);
       const int m = m0 + 32 * i + rq + row, n = n0 + c * VPC;
-      if (m >= p.M) continue;
+      if (m >= mend) continue;
       if (!OUT_F32 && EPI) v = epi_chunk(p, v, m, n);
       uint8_t* out = reinterpret_cast<uint8_t*>(p.y) + ((long)m * p.ldy + n) * ES;
       if (vec && n + VPC <= p.N) {
@@ -1151,18 +1153,21 @@ __global__ void __launch_bounds__(WM * 128, 1) w4a16_kernel(GemmParams p) {
   epilogue<OUT_F32, EPI>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sA[0][0] + wave * 4096);
 }
 
-// W4A16 on large grids: one wave per SIMD with a 128 x 128 register tile (4 x 4 sub-tiles of
+// W4A16 on large grids: one wave per SIMD with a TM/2 x 128 register tile (TM/64 x 4 sub-tiles of
 // 32 x 32; the accumulators live in AGPRs, only MFMAs touch them before the epilogue), block tile
-// 256 x 256 on 4 waves.  (Two waves per SIMD with 128 x 64 tiles measured the same or slower.)  Per 64-column stage a wave issues 64 MFMAs (2048 cycles of the SIMD's
+// TM x 256 on 4 waves, TM = 256 or 192 (launch_w4a16 picks the height that needs the fewest
+// rounds of tiles over the CUs).  (Two waves per SIMD with 128 x 64 tiles measured the same or slower.)  Per 64-column stage a wave issues 64 MFMAs (2048 cycles of the SIMD's
 // MFMA pipe) and, spread between them, its share of the next stage: 8 x_hat chunks and one weight
 // row (64 codes dequantized as in w4a16_kernel) written to the other LDS buffer, so one instruction
 // stream keeps the MFMA pipe, the VALU and the LDS busy together.  Loads run two stages ahead with
 // the same exact-count asm waits; LDS rows have the 144-byte pitch of w4a16_kernel.
-template <int G, bool OUT_F32, bool EPI = false>
+template <int G, bool OUT_F32, bool EPI = false, int TM = 256>
 __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
-  constexpr int NT = 256, TBM = 256, TBN = 256, KB = 64;
+  constexpr int NT = 256, TBM = TM, TBN = 256, KB = 64;
+  constexpr int RI = TBM / 64;                // 32-row sub-tiles per wave (the wave tile is TBM / 2 rows)
+  static_assert(TBM == 256 || TBM == 192, "tile height");
   constexpr int PITCH = 2 * KB + 16;
-  constexpr int ALD = TBM * 8 / NT;           // 8 x_hat chunks per thread and stage
+  constexpr int ALD = TBM * 8 / NT;           // x_hat chunks per thread and stage (8 or 6)
   constexpr int LPS = ALD + 3;                // + two 16-byte weight loads + one scale
   constexpr int D = 2;                        // register sets (stages in flight)
   __shared__ __attribute__((aligned(16))) uint8_t sA[2][TBM * PITCH];
@@ -1216,18 +1221,24 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
     constexpr int q = decltype(q_c)::value;
     wait_regs(ra[q], rb[q], rs[q]);
   };
-  // part `pt` (0..3) of a set's move to LDS buffer buf: x_hat chunks 2 pt, 2 pt + 1 and the weight
-  // row's 16 codes of k 16 pt .. 16 pt + 15 (bf16(q * bf16(s)), one exact FMA per code)
+  // part `pt` (0..3) of a set's move to LDS buffer buf: the x_hat chunks i with i % 4 == pt (two
+  // of 8, or one or two of 6) and the weight row's 16 codes of k 16 pt .. 16 pt + 15
+  // (bf16(q * bf16(s)), one exact FMA per code)
   auto lstore_part = [&](int buf, auto q_c, int pt) {
     constexpr int q = decltype(q_c)::value;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&sA[buf][aoff[2 * pt + i]]) = ra[q][2 * pt + i];
+    for (int i = 0; i < ALD; ++i)
+      if (i % 4 == pt) *reinterpret_cast<u32x4*>(&sA[buf][aoff[i]]) = ra[q][i];
     const float sc = round_bf16(half_bits_to_float((uint16_t)rs[q])), ns8 = -8.0f * sc;
     const u32x4 w = rb[q][pt >> 1];
     uint32_t o[8];
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
-      const uint32_t v = w[2 * (pt & 1) + d], lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+      const uint32_t v = w[2 * (pt & 1) + d];
+      uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+      // opaque to the combiner, which would otherwise fold the masks into one bit-field
+      // extract per code: each byte then converts with a single v_cvt_f32_ubyteN
+      asm("" : "+v"(lo), "+v"(hi));
       o[4 * d + 0] = pack_bf16x2(__builtin_fmaf(ubyte_f32<0>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<0>(hi), sc, ns8));
       o[4 * d + 1] = pack_bf16x2(__builtin_fmaf(ubyte_f32<1>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<1>(hi), sc, ns8));
       o[4 * d + 2] = pack_bf16x2(__builtin_fmaf(ubyte_f32<2>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<2>(hi), sc, ns8));
@@ -1237,13 +1248,13 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
     *reinterpret_cast<u32x4*>(&sB[buf][boff + 32 * pt + 16]) = u32x4{o[4], o[5], o[6], o[7]};
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[RI][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < RI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  const int ra0 = (128 * wm + lr) * PITCH + 16 * h, rb0 = (128 * wn + lr) * PITCH + 16 * h;
+  const int ra0 = ((TBM / 2) * wm + lr) * PITCH + 16 * h, rb0 = (128 * wn + lr) * PITCH + 16 * h;
   using Q0 = std::integral_constant<int, 0>;
   using Q1 = std::integral_constant<int, 1>;
   gload(0, Q0{});
@@ -1262,13 +1273,13 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
     wait_set(QN{});                      // set q + 1 landed; the D - 1 newer sets may be in flight
 #pragma unroll
     for (int ks = 0; ks < KB / 16; ++ks) {
-      u32x4 a[4], b[4];
+      u32x4 a[RI], b[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const u32x4*>(&sA[buf][ra0 + 32 * i * PITCH + 32 * ks]);
+      for (int i = 0; i < RI; ++i) a[i] = *reinterpret_cast<const u32x4*>(&sA[buf][ra0 + 32 * i * PITCH + 32 * ks]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4*>(&sB[buf][rb0 + 32 * j * PITCH + 32 * ks]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < RI; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16_32x32x16(a[i], b[j], acc[i][j]);
       lstore_part(buf ^ 1, QN{}, ks);
@@ -1289,14 +1300,19 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
     for (int i = 0; i < ALD; ++i) asm volatile("" ::"v"(ra[q][i]));
     asm volatile("" ::"v"(rb[q][0]), "v"(rb[q][1]), "v"(rs[q]));
   }
-  // epilogue per 64 x 64 quadrant of the wave tile (the A buffers stage the output)
+  // epilogue per 64 x 64 quadrant of the wave tile (the A buffers stage the output); with three
+  // row sub-tiles (TM = 192) the last quadrant holds one, and its other 32 rows (the next wave's)
+  // are not stored
+  const int wrow = m0 + (TBM / 2) * wm, wend = wrow + TBM / 2;
   if constexpr (EPI) {
     // written out per quadrant: with the fused op the unrolled loop below is too large for the
     // unroller, and a rolled loop would index the accumulators at run time (scratch)
     auto quadrant = [&](auto qi_c, auto qj_c) {
       constexpr int qi = decltype(qi_c)::value, qj = decltype(qj_c)::value;
-      f32x16 part[2][2] = {{acc[2 * qi][2 * qj], acc[2 * qi][2 * qj + 1]}, {acc[2 * qi + 1][2 * qj], acc[2 * qi + 1][2 * qj + 1]}};
-      epilogue<OUT_F32, EPI>(p, part, m0 + 128 * wm + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096);
+      constexpr int i1 = 2 * qi + 1 < RI ? 2 * qi + 1 : 2 * qi;
+      f32x16 part[2][2] = {{acc[2 * qi][2 * qj], acc[2 * qi][2 * qj + 1]}, {acc[i1][2 * qj], acc[i1][2 * qj + 1]}};
+      epilogue<OUT_F32, EPI>(p, part, wrow + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096,
+                             nullptr, nullptr, 0, 0, wend);
     };
     quadrant(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
     quadrant(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
@@ -1304,11 +1320,13 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
     quadrant(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
   } else {
 #pragma unroll
-    for (int qi = 0; qi < 2; ++qi)
+    for (int qi = 0; qi < (RI + 1) / 2; ++qi)
 #pragma unroll
       for (int qj = 0; qj < 2; ++qj) {
-        f32x16 part[2][2] = {{acc[2 * qi][2 * qj], acc[2 * qi][2 * qj + 1]}, {acc[2 * qi + 1][2 * qj], acc[2 * qi + 1][2 * qj + 1]}};
-        epilogue<OUT_F32>(p, part, m0 + 128 * wm + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096);
+        const int i1 = 2 * qi + 1 < RI ? 2 * qi + 1 : 2 * qi;   // the half quadrant repeats its sub-tile
+        f32x16 part[2][2] = {{acc[2 * qi][2 * qj], acc[2 * qi][2 * qj + 1]}, {acc[i1][2 * qj], acc[i1][2 * qj + 1]}};
+        epilogue<OUT_F32>(p, part, wrow + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096,
+                          nullptr, nullptr, 0, 0, wend);
       }
   }
 }
@@ -1376,18 +1394,29 @@ hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, 
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st) {
   // 256 x 256 tiles (one wave per SIMD) when they cover the chip at least half, else 128 x 128
   // tiles (two workgroups of 4 waves per CU)
-  const long tiles_wide = (long)((p.M + 255) / 256) * ((p.N + 255) / 256);
+  const long nbn = (p.N + 255) / 256;
+  const long tiles_wide = (long)((p.M + 255) / 256) * nbn;
   if (tiles_wide >= 128) {
-    const dim3 grid((unsigned)tiles_wide);
-#define SVDQ_W4A16W(GG)                                                                    \
-  if (G == GG) {                                                                          \
-    if (out_f32) w4a16_wide_kernel<GG, true><<<grid, 256, 0, st>>>(p);                    \
-    else if (p.epi) w4a16_wide_kernel<GG, false, true><<<grid, 256, 0, st>>>(p);          \
-    else w4a16_wide_kernel<GG, false><<<grid, 256, 0, st>>>(p);                           \
-    return hipGetLastError();                                                             \
+    // tile height 256 or 192: the one with the least work per CU, rounds of tiles x tile rows (a
+    // round = one tile on each of the 256 CUs); e.g. M = 2304, N = 16384: 576 tiles of 256 rows
+    // need 3 rounds (the last a quarter full), 768 tiles of 192 rows 3 full rounds
+    const long tiles192 = (long)((p.M + 191) / 192) * nbn;
+    const bool t192 = ((tiles192 + 255) / 256) * 192 < ((tiles_wide + 255) / 256) * 256;
+#define SVDQ_W4A16W(GG, TT)                                                                 \
+  if (G == GG) {                                                                            \
+    const dim3 grid((unsigned)(TT == 192 ? tiles192 : tiles_wide));                         \
+    if (out_f32) w4a16_wide_kernel<GG, true, false, TT><<<grid, 256, 0, st>>>(p);           \
+    else if (p.epi) w4a16_wide_kernel<GG, false, true, TT><<<grid, 256, 0, st>>>(p);        \
+    else w4a16_wide_kernel<GG, false, false, TT><<<grid, 256, 0, st>>>(p);                  \
+    return hipGetLastError();                                                               \
   }
-    SVDQ_W4A16W(64)
-    SVDQ_W4A16W(128)
+    if (t192) {
+      SVDQ_W4A16W(64, 192)
+      SVDQ_W4A16W(128, 192)
+    } else {
+      SVDQ_W4A16W(64, 256)
+      SVDQ_W4A16W(128, 256)
+    }
 #undef SVDQ_W4A16W
     return hipErrorInvalidValue;
   }

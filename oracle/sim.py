@@ -162,6 +162,31 @@ def sim_forward_torch(x, st: LayerState, *, num_threads: int | None = None):
     return y
 
 
+def quantize_activations_torch(x, st: LayerState, *, num_threads: int | None = None):
+    """The A4 step on CPU torch, with the reference's own ops: ``x / smooth`` in x's dtype
+    (``quant/svd.py:121-122``), then ``quantize_symmetric_int4(x_hat, G)`` (``quant/pack.py:6-23``:
+    group ``amax``, ``clamp_min(1e-8) / 7`` in the input dtype, ``round(x_hat.float() / scales)``,
+    clamp to [-8, 7]) and ``pack_int4`` (``pack.py:47-56``).  ``x`` is a bf16 torch tensor
+    [M, K]; returns ``(packed uint8 [M, Kp/2], scales bf16 [M, Kp/G])`` as torch tensors.  The
+    multithreaded CPU baseline of the activation pass; bit-identical to ``quantize_activations``.
+    """
+    import torch
+
+    if num_threads is not None:
+        torch.set_num_threads(num_threads)
+    smooth = torch.from_numpy(np.ascontiguousarray(st.smooth, dtype=np.float32)).to(x.dtype)
+    x_hat = x / smooth
+    kp, g = st.padded_in, st.group_size
+    if x_hat.shape[-1] != kp:
+        x_hat = torch.cat([x_hat, x_hat.new_zeros(x_hat.shape[0], kp - x_hat.shape[-1])], dim=-1)
+    grouped = x_hat.reshape(x_hat.shape[0], kp // g, g)
+    scales = grouped.abs().amax(dim=-1, keepdim=True).clamp_min(1e-8) / 7.0
+    q = torch.round(grouped.float() / scales).clamp(-8, 7).to(torch.int8).reshape(x_hat.shape[0], kp)
+    u = (q.to(torch.int16) + 8).to(torch.uint8)
+    packed = u[:, 0::2] | (u[:, 1::2] << 4)
+    return packed, scales.squeeze(-1)
+
+
 def rel_l2(a, b) -> float:
     """||a - b||_2 / ||b||_2 in float64."""
     a = np.asarray(a, dtype=np.float64)
@@ -170,5 +195,5 @@ def rel_l2(a, b) -> float:
     return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))
 
 
-__all__ = ["Adapter", "LayerState", "quantize_activations", "w4a4_eval", "w4a16_eval",
+__all__ = ["Adapter", "LayerState", "quantize_activations", "quantize_activations_torch", "w4a4_eval", "w4a16_eval",
            "sim_weight", "sim_forward_torch", "rel_l2", "bf16_bits", "from_bf16_bits"]

@@ -61,7 +61,8 @@ def _check(op, fused, ref):
     ("w4a4", "e4m3", 72, 136, 256),
     ("w4a4", "i8", 40, 200, 192),
     ("w4a16", "e3m2", 64, 136, 256),     # 128 x 128 tiles
-    ("w4a16", "e3m2", 512, 16384, 128),  # 256 x 256 tiles (128 of them)
+    ("w4a16", "e3m2", 512, 16384, 128),  # 192 x 256 tiles (192 of them; the last row of tiles partial)
+    ("w4a16", "e3m2", 1024, 16384, 128), # 256 x 256 tiles (256 of them: 192-row tiles would need 2 rounds)
 ])
 @pytest.mark.parametrize("op", OPS)
 def test_fused_epilogue_matches_torch_op(dev, mode, operand, m, n, k, op):

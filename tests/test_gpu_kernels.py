@@ -215,9 +215,13 @@ def test_layer_random_shapes(dev, m, n, k, g, r, rl, bias, mode):
 
 
 @pytest.mark.parametrize("m,n,k,g,bias", [
-    (2304, 4096, 512, 64, False),    # 144 tiles of 256 x 256: the one-wave-per-SIMD W4A16 kernel
-    (2100, 4300, 576, 64, True),     # partial last tiles in M and N; 9 stages (odd: the tail stage)
-    (2048, 4352, 640, 128, False),   # group 128
+    # the one-wave-per-SIMD W4A16 kernel; tile height 192 where it needs no more rounds of tiles
+    # over the 256 CUs than 256 does, else 256
+    (2304, 4096, 512, 64, False),    # 192 tiles of 192 x 256
+    (2100, 4300, 576, 64, True),     # 192-row tiles, partial last tiles in M and N; 9 stages (odd: the tail stage)
+    (2048, 4352, 640, 128, False),   # group 128, 192-row tiles
+    (4096, 4096, 512, 64, True),     # 256 tiles of 256 x 256 (192-row tiles would need 2 rounds)
+    (2304, 16384, 384, 64, False),   # config 2 ff.up's tiling at short K: 768 tiles of 192 x 256
 ])
 def test_w4a16_wide_tiles(dev, m, n, k, g, bias):
     x = synth.make_activation(m, k, seed=17)

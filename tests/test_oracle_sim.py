@@ -116,3 +116,17 @@ def test_edge_activation_fixture_regression():
     assert np.array_equal(nm.bf16_bits(xh), fx["xhat"])
     assert np.array_equal(packed, fx["qx_packed"]) and np.array_equal(nm.bf16_bits(sx), fx["sx"])
     assert q[1, :8].tolist() == [7, 2, 4, -2, 0, 2, -7, 0]
+
+
+@pytest.mark.parametrize("m,k,g", [(37, 448, 64), (16, 1024, 128), (64, 6144, 64)])
+def test_torch_a4_quantizer_matches_numpy_restatement(m, k, g):
+    """The torch restatement (the multithreaded CPU baseline) gives the numpy oracle's bits."""
+    import torch
+    from oracle import numerics as nm
+    x = synth.make_activation(m, k, seed=m)
+    st = synth.make_layer(32, k, x, rank=8, group_size=g, seed=2)
+    xt = torch.from_numpy(nm.bf16_bits(x).view(np.int16)).view(torch.bfloat16)
+    packed, scales = sim.quantize_activations_torch(xt, st)
+    _, packed_ref, sx_ref, _ = sim.quantize_activations(x, st)
+    assert np.array_equal(packed.numpy(), packed_ref)
+    assert np.array_equal(scales.view(torch.int16).numpy().view(np.uint16), nm.bf16_bits(sx_ref))
