@@ -98,7 +98,8 @@ int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int6
  *              bf16 [M, 2, RTp], per row the hi plane then the lo plane of the f32 low-rank
  *              activations (hi + lo within 2^-18 relative), whose columns are [0, r) = x_hat @ l2^T,
  *              [r, r+rl) = mult * (x @ A^T), [r+rl, RTp) = 0; the split partials behind it are
- *              summed in split order.  RTp % 32 == 0, RTp >= r + rl, ceil(r/32) + ceil(rl/32) <= 4;
+ *              summed in split order.  RTp % 32 == 0, RTp >= r + rl (any rank: the down
+ *              projections run in launches of 4 MFMA column tiles, 32 columns each);
  *              S (`splits`) from svdq_act_quant_workspace. */
 int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2, int r,
                    const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,

@@ -92,11 +92,15 @@ __device__ __forceinline__ void smooth64_exact(const u32x4 (&xr)[8], cfloat_ptr 
 // whole planes.
 // QX: the canonical packed codes may be requested (p.qx checked at run time); without it the
 // kernel carries no nibble-packing code at all.
-template <int G, int NT, int OPER, bool XHAT, bool QX>
+// NT: the MFMA column tiles of the down projections this launch computes, global tiles
+// p.t0 .. p.t0 + NT - 1 of [L2 (ceil(r/32) tiles) | LoRA (ceil(rl/32) tiles)].  LX: some of them
+// may be LoRA tiles (the raw x is then kept as an MFMA operand too).  Ranks beyond 4 tiles take
+// further launches with OPER 0 and no XHAT (down projections only), each writing its own columns
+// of the split partials.
+template <int G, int NT, int OPER, bool XHAT, bool QX, bool LX>
 __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
   constexpr int HB = G / 64;             // 64-column blocks per group
   constexpr bool QUANT = OPER != 0;
-  constexpr int TR_MIN = 1;                // at least one low-rank tile; more tiles may be LoRA
   __shared__ __attribute__((aligned(16))) float red[4 * 64 * 32];
 
   const int tid = threadIdx.x;
@@ -124,7 +128,7 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
   // is dead (after the smoothing and its exact fallback): the loads overlap the quantization, the
   // stores and the low-rank MFMAs with no extra registers.  With LoRA the raw x feeds the LoRA
   // down projection, so each group is loaded when it starts.
-  constexpr bool LORA = NT > TR_MIN;
+  constexpr bool LORA = LX;
   u32x4 xr[HB][8];
   auto load_x = [&](int g) {
 #pragma unroll
@@ -265,7 +269,7 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
           permlane32_swap(v0, v1);
           fa[0][c][d] = v0;
           fa[1][c][d] = v1;
-          if (NT > TR_MIN) {
+          if (LX) {
             uint32_t w0 = xr[b][2 * c][d], w1 = xr[b][2 * c + 1][d];
             permlane32_swap(w0, w1);
             fx[0][c][d] = w0;
@@ -276,8 +280,9 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
       const int kb = g * G + 64 * b;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const bool is_l2 = t < TR;
-        const int n = is_l2 ? 32 * t + lr : 32 * (t - TR) + lr;
+        const int T = p.t0 + t;   // global tile
+        const bool is_l2 = T < TR;
+        const int n = is_l2 ? 32 * T + lr : 32 * (T - TR) + lr;
         const int nmax = is_l2 ? p.r : p.rl;
         const uint16_t* bsrc = (is_l2 ? p.l2 : p.lora) + (long)min(n, nmax - 1) * K + kb + 8 * h;
         const bool nok = n < nmax;
@@ -305,13 +310,14 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
       for (int i = 0; i < 16; ++i)
         red[wave * 2048 + (32 * a + 8 * (i >> 2) + 4 * h + (i & 3)) * 32 + lr] = acc[a][t][i];
     __syncthreads();
-    const bool is_l2 = t < TR;
+    const int T = p.t0 + t;
+    const bool is_l2 = T < TR;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int idx = tid + 256 * i;
       const int rr = idx >> 5, cc = idx & 31;
       const int grow = m0 + rr;
-      const int j = is_l2 ? 32 * t + cc : 32 * (t - TR) + cc;
+      const int j = is_l2 ? 32 * T + cc : 32 * (T - TR) + cc;
       const bool ok = is_l2 ? j < p.r : j < p.rl;
       if (grow < p.M && ok) {
         float v = ((red[idx] + red[2048 + idx]) + red[4096 + idx]) + red[6144 + idx];
@@ -364,13 +370,15 @@ __global__ void prepare_smooth_kernel(const uint16_t* __restrict__ s, float* __r
   }
 }
 
-template <int G, int OPER, bool XHAT, bool QX>
+template <int G, int OPER, bool XHAT, bool QX, bool MIDONLY = false>
 hipError_t launch_act_nt(const ActParams& p, int nt, dim3 grid, hipStream_t st) {
+  // the first launch (t0 = 0) may hold LoRA tiles only when it has two or more tiles (tile 0 is
+  // L2); a down-projection-only launch may hold any mix
   switch (nt) {
-    case 1: act_kernel<G, 1, OPER, XHAT, QX><<<grid, 256, 0, st>>>(p); break;
-    case 2: act_kernel<G, 2, OPER, XHAT, QX><<<grid, 256, 0, st>>>(p); break;
-    case 3: act_kernel<G, 3, OPER, XHAT, QX><<<grid, 256, 0, st>>>(p); break;
-    case 4: act_kernel<G, 4, OPER, XHAT, QX><<<grid, 256, 0, st>>>(p); break;
+    case 1: act_kernel<G, 1, OPER, XHAT, QX, MIDONLY><<<grid, 256, 0, st>>>(p); break;
+    case 2: act_kernel<G, 2, OPER, XHAT, QX, true><<<grid, 256, 0, st>>>(p); break;
+    case 3: act_kernel<G, 3, OPER, XHAT, QX, true><<<grid, 256, 0, st>>>(p); break;
+    case 4: act_kernel<G, 4, OPER, XHAT, QX, true><<<grid, 256, 0, st>>>(p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -378,6 +386,10 @@ hipError_t launch_act_nt(const ActParams& p, int nt, dim3 grid, hipStream_t st) 
 
 template <int G>
 hipError_t launch_act_g(const ActParams& p, int nt, int oper, bool xhat, dim3 grid, hipStream_t st) {
+  if (p.t0 > 0) {   // down projections only
+    if (oper != 0 || xhat) return hipErrorInvalidValue;
+    return launch_act_nt<G, 0, false, false, true>(p, nt, grid, st);
+  }
   if (oper == 3 && !xhat && !p.qx) return launch_act_nt<G, 3, false, false>(p, nt, grid, st);
   if (oper == 3 && !xhat) return launch_act_nt<G, 3, false, true>(p, nt, grid, st);
   if (oper == 1 && !xhat) return launch_act_nt<G, 1, false, true>(p, nt, grid, st);

@@ -97,8 +97,7 @@ int act_quant_run(const void* x, int64_t ldx, const float* srs, const void* l2, 
   if (int e = check_group(group, K)) return e;
   if (r < 1 || rl < 0) return fail(SVDQ_ERR_SHAPE, "act_quant: rank r=%d rl=%d", r, rl);
   if (RTp % 32 || RTp < r + rl) return fail(SVDQ_ERR_SHAPE, "act_quant: RTp=%d (r=%d rl=%d)", RTp, r, rl);
-  const int nt = mid_tiles(r, rl);
-  if (nt > 4) return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: ceil(r/32)+ceil(rl/32)=%d > 4", nt);
+  const int nt = mid_tiles(r, rl);   // MFMA column tiles of the down projections (any number)
   if (!x || !srs || !l2 || !head || !part || (rl > 0 && (!lora_down || !lora_mult)) || (quant && (!qa || !sx)) ||
       (packed && !qx) || (want_xhat && !xhat))
     return fail(SVDQ_ERR_ARG, "act_quant: null pointer");
@@ -132,9 +131,25 @@ int act_quant_run(const void* x, int64_t ldx, const float* srs, const void* l2, 
   p.gps = (ngroups + splits - 1) / splits;
   p.exact = (flags & SVDQ_ACT_EXACT_DIV) ? 1 : 0;
   p.sx_pairs = pairs ? 1 : 0;
-  if (int e = launched(svdq::launch_act(p, group, nt, e4m3 ? 1 : (i8 ? 2 : (e3m2 ? 3 : 0)), want_xhat, splits, stream),
+  // The first launch quantizes and computes the first 4 column tiles; each further launch adds 4
+  // more tiles of the down projections (rank + LoRA rank beyond 128), into their own columns of
+  // the split partials.
+  p.t0 = 0;
+  if (int e = launched(svdq::launch_act(p, group, nt < 4 ? nt : 4, e4m3 ? 1 : (i8 ? 2 : (e3m2 ? 3 : 0)), want_xhat,
+                                        splits, stream),
                        "act_quant"))
     return e;
+  for (int t0 = 4; t0 < nt; t0 += 4) {
+    svdq::ActParams q = p;
+    q.t0 = t0;
+    q.qa = nullptr;
+    q.sx = nullptr;
+    q.qx = nullptr;
+    q.xhat = nullptr;
+    if (int e = launched(svdq::launch_act(q, group, nt - t0 < 4 ? nt - t0 : 4, 0, false, splits, stream),
+                         "act_quant (down projections)"))
+      return e;
+  }
   return launched(svdq::launch_mid_finalize(p.mid, splits, M, RTp, reinterpret_cast<uint16_t*>(head), stream),
                   "act_quant (mid)");
 }

@@ -14,6 +14,7 @@ struct ActParams {
   const float* lora_mult;   // [rl]
   int r, rl;
   int M, K, RTp;            // RTp: row stride of mid (>= r + rl, multiple of 32)
+  int t0;                   // first MFMA column tile of the down projections in this launch
   uint8_t* qx;              // [M, K/2] canonical packed codes (optional)
   uint8_t* qa;              // [M, K] 8-bit GEMM operand codes (quantizing modes)
   uint16_t* sx;             // [M, K/G] bf16, or [K/G, M] u32 (sx, sx) pairs when sx_pairs
@@ -51,7 +52,9 @@ struct GemmParams {
 };
 
 int act_splits(int M, int K, int G);
-// oper: 0 = no codes (x_hat only), 1 = e4m3 operand codes, 2 = int8 16*q operand codes
+// oper: 0 = no codes (x_hat only), 1 = e4m3 operand codes, 2 = int8 16*q operand codes, 3 = e3m2;
+// nt: column tiles of the down projections from p.t0 (at most 4); with p.t0 > 0 the launch computes
+// down projections only (oper 0, no x_hat)
 hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, int splits, hipStream_t st);
 // Sums the S split partials `part` [S, M, RTp] in split order and writes the GEMM epilogue's
 // operand midp [M, 2, RTp] (bf16 hi plane, then bf16 lo plane, hi + lo within 2^-18 of the f32 sum, relative).

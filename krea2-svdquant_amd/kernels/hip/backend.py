@@ -73,11 +73,14 @@ def _pad_cols(t: Tensor, kp: int, value: float = 0.0) -> Tensor:
 
 
 def prepare_layer(state: SVDQuantLinearState, adapters: Sequence = (),
-                  device: torch.device | str | None = None) -> PreparedLayer:
+                  device: torch.device | str | None = None, *, base: Optional[PreparedLayer] = None) -> PreparedLayer:
     """Validate a packed state and build the kernels' per-layer operands on ``device``.
 
     ``adapters`` are objects with ``down_weight`` [rl, K], ``up_weight`` [N, rl] and
-    ``multiplier`` (``SVDQuantLoRAAdapter``).
+    ``multiplier`` (``SVDQuantLoRAAdapter``).  ``base``: the same layer prepared without
+    adapters; its smoothing constants, weight buffers and (lazily built) weight operands are
+    shared instead of rebuilt, so a layer holds one expanded weight operand however many adapter
+    sets it is prepared with.
     """
     if not state.qweight_packed:
         raise RuntimeError("HIP gfx950 backend expects packed uint8 qweight (qweight_packed=True)")
@@ -119,16 +122,17 @@ def prepare_layer(state: SVDQuantLinearState, adapters: Sequence = (),
         l1cat[:, col: col + up.shape[1]] = up
         col += up.shape[1]
     bias = None if state.bias is None else state.bias.to(dev, torch.bfloat16).contiguous()
+    shared = base is not None and base.device == dev and base.kp == kp and base.n == n
     return PreparedLayer(
-        srs=ops.prepare_smooth(smooth.contiguous()),
+        srs=base.srs if shared else ops.prepare_smooth(smooth.contiguous()),
         l2=l2.contiguous(),
         l1cat=l1cat,
         lora_down=torch.cat(downs, 0).contiguous() if downs else None,
         lora_mult=torch.cat(mults, 0).contiguous() if mults else None,
-        qweight=qweight,
-        weight_scales=scales.contiguous(),
-        scale_pairs={},
-        operands={},
+        qweight=base.qweight if shared else qweight,
+        weight_scales=base.weight_scales if shared else scales.contiguous(),
+        scale_pairs=base.scale_pairs if shared else {},
+        operands=base.operands if shared else {},
         bias=bias,
         group_size=g, n=n, k=k, kp=kp, rtp=rtp,
     )

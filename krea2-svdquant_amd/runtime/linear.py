@@ -150,16 +150,35 @@ class SVDQuantLinear(nn.Module):
     def _mode(self, device: torch.device) -> str:
         return _HIP_MODES[self.resolved_backend(device)]
 
+    def _buffers_key(self, device: torch.device) -> tuple:
+        # storage and version counter of every buffer: in-place edits bump the version
+        bufs = (self.qweight, self.smooth_scale, self.weight_scales, self.l1, self.l2, self.bias)
+        return (str(device),) + tuple((b.data_ptr(), b._version) if b is not None else None for b in bufs)
+
+    def _adapters_key(self) -> tuple:
+        # each adapter's identity, multiplier (read on every forward, as the reference does) and
+        # weights (storage and version)
+        return tuple((id(a), a.multiplier, a.down_weight.data_ptr(), a.down_weight._version, a.up_weight.data_ptr(),
+                      a.up_weight._version) for a in self.lora_adapters)
+
     def _prepare(self, device: torch.device, with_adapters: bool) -> PreparedLayer:
-        key = (str(device), self.qweight.data_ptr(), self.smooth_scale.data_ptr(), self.l1.data_ptr(),
-               len(self.lora_adapters) if with_adapters else 0)
-        hit = self._prepared.get(with_adapters)
-        if hit is not None and hit[0] == key:
-            return hit[1]
+        """The kernels' operands of this layer, cached per (buffers, adapters).  The adapter entry
+        shares the base entry's weight operands (prepare_layer's ``base``)."""
         self.resolved_backend(device)
-        prep = prepare_layer(self.state, list(self.lora_adapters) if with_adapters else (), device)
-        self._prepared[with_adapters] = (key, prep)
-        return prep
+        base_key = self._buffers_key(device)
+        hit = self._prepared.get(False)
+        if hit is None or hit[0] != base_key:
+            self._prepared.clear()
+            hit = (base_key, prepare_layer(self.state, (), device))
+            self._prepared[False] = hit
+        if not with_adapters:
+            return hit[1]
+        key = base_key + self._adapters_key()
+        ahit = self._prepared.get(True)
+        if ahit is None or ahit[0] != key:
+            ahit = (key, prepare_layer(self.state, list(self.lora_adapters), device, base=hit[1]))
+            self._prepared[True] = ahit
+        return ahit[1]
 
     def invalidate_prepared(self) -> None:
         """Drop the cached per-layer kernel operands (call after editing buffers in place)."""

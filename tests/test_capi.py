@@ -63,9 +63,9 @@ def test_gemm_rejects_null_and_misaligned_pointers_before_any_launch():
         lib.call("svdq_w4a16_gemm", fake, 100, fake, fake, fake, fake, 32, nul, 128, 128, 128, 64, fake, 128, 0, nul)
     assert ei.value.status == -3
     with pytest.raises(lib.SVDQError) as ei:
-        lib.call("svdq_act_quant", fake, 128, fake, fake, 200, nul, 0, nul, 64, 128, 64, 224, lib.SVDQ_ACT_OPERAND_E4M3,
+        lib.call("svdq_act_quant", fake, 128, fake, fake, 200, nul, 0, nul, 64, 128, 64, 192, lib.SVDQ_ACT_OPERAND_E4M3,
                  fake, fake, nul, nul, 0, fake, 1, nul)
-    assert ei.value.status == -4  # ceil(200/32) = 7 MFMA column tiles > 4
+    assert ei.value.status == -2 and "RTp=192" in str(ei.value)   # RTp < r + rl
     with pytest.raises(lib.SVDQError) as ei:
         lib.call("svdq_act_quant", fake, 128, fake, fake, 32, nul, 0, nul, 64, 128, 64, 32,
                  lib.SVDQ_ACT_OPERAND_E4M3 | lib.SVDQ_ACT_OPERAND_I8, fake, fake, nul, nul, 0, fake, 1, nul)
