@@ -60,7 +60,13 @@ const char* svdq_version(void);
 /* Message for the most recent failing call on this host thread ("" if none). */
 const char* svdq_last_error(void);
 
-/* Group sizes with kernels in this build; returns 1 if `group` is supported. */
+/* Group sizes with kernels in this build; returns 1 if `group` is supported: any positive
+ * multiple of 16 (the reference quantizer takes any group, quant/pack.py:6-23; its own test uses
+ * 16, tests/test_svd_linear_cpu.py:10).  64 and 128 have the tuned kernels and every operand
+ * format.  Every other group size takes the generic kernels: K % 64 == 0, the int8 operand only
+ * (SVDQ_ACT_OPERAND_I8 / SVDQ_OPERAND_I8), quantized from x_hat (svdq_act_quant needs
+ * SVDQ_ACT_XHAT and an xhat buffer with it), no fused epilogue op on svdq_w4a4_gemm_epi, and no
+ * 2^31 limit on M*K or N*K. */
 int svdq_group_supported(int group);
 
 /* Per-layer constant of the activation pass: srs[0:K] = float(smooth), srs[K:2K] =
@@ -92,8 +98,9 @@ int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int6
  *          bytes 0-15 at Q[t][h][Mp][16] (offset 0), bytes 16-23 at P[t][h][Mp][8] (offset
  *          Mp * K / 2); rows of the padding are not written
  *     qx : u8 [M, K/2] canonical packed codes (pack.py:47-56), if SVDQ_ACT_PACKED
- *   xhat     : bf16 [M, ldxh] (SVDQ_ACT_XHAT; with a quantizing flag only for e4m3)
- *   E3M2 needs K % 64 == 0 (always true: group 64 or 128) and a 16-byte aligned qa.
+ *   xhat     : bf16 [M, ldxh] (SVDQ_ACT_XHAT; with a quantizing flag: e4m3 at group 64 / 128, and
+ *              required with I8 at any other group size, whose codes are quantized from it)
+ *   E3M2 needs K % 64 == 0 (always true at group 64 or 128) and a 16-byte aligned qa.
  *   mid      : workspace of svdq_act_quant_workspace's mid_floats floats.  Output at its head:
  *              bf16 [M, 2, RTp], per row the hi plane then the lo plane of the f32 low-rank
  *              activations (hi + lo within 2^-18 relative), whose columns are [0, r) = x_hat @ l2^T,
@@ -154,7 +161,9 @@ int svdq_prepare_weight_operand(const void* qw, void* qwe, int N, int K, int ope
  *   sxp: u32 [K/group, M] bf16 pairs (svdq_act_quant with SVDQ_ACT_SX_PAIRS)
  *   qwe: u8 [N, K] from svdq_prepare_weight_operand (same format; planar for E3M2)
  *   swp: u32 [K/group, N] from svdq_prepare_weight_scales (same operand format)
- *   E4M3 / I8: M*K and N*K below 2^31 (larger problems are split over rows by the caller)
+ *   E4M3 / I8 at group 64 / 128: M*K and N*K below 2^31 (larger problems are split over rows
+ *   by the caller).  Other group sizes (see svdq_group_supported): SVDQ_OPERAND_I8 and
+ *   SVDQ_EPI_NONE only.
  *   mid: bf16 [M, 2, RTp] (hi, lo planes) = the head of svdq_act_quant's mid workspace
  *   l1cat : bf16 [N, RTp] = [l1 | up_1 | ... | 0]
  *   bias: bf16 [N] or NULL     y : [M, ldy], bf16 (out_f32 = 0) or f32 (out_f32 = 1) */

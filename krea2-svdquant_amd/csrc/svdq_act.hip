@@ -360,6 +360,63 @@ __global__ void mid_finalize_kernel(const float* __restrict__ part, int S, int M
   *reinterpret_cast<u32x4*>(dst + RTp) = lo;
 }
 
+// A4 quantizer for any group size G (a multiple of 16 dividing K), from x_hat (written by the act
+// kernel in x_hat mode): the generic path behind group sizes other than 64 and 128.  One thread per
+// (row, group), adjacent threads on adjacent groups of a row (contiguous x_hat reads):
+//   sx = bf16(max(amax, bf16(1e-8)) / 7), q = clamp(rne(x_hat / sx), -8, 7)   (pack.py:17-21)
+// with IEEE float32 division, written as the int8 GEMM operand (16 q, within each chunk of 8
+// columns in the order k0 k2 k4 k6 k1 k3 k5 k7), the scales as bf16 [M, K/G] or u32 pairs
+// [K/G, M], and optionally the canonical packed codes.
+__global__ void quant_any_group_kernel(const uint16_t* __restrict__ xhat, long ldxh, int M, int K, int G,
+                                       uint8_t* __restrict__ qa, uint16_t* __restrict__ sx, int sx_pairs,
+                                       uint8_t* __restrict__ qx) {
+  const int ngroups = K / G;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)M * ngroups) return;
+  const long m = idx / ngroups;
+  const int g = (int)(idx % ngroups);
+  const uint16_t* src = xhat + m * ldxh + (long)g * G;
+  uint32_t amb = 0;
+  for (int c = 0; c < G; c += 8) {
+    const u32x4 v = ld16(src + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      amb = max(amb, v[e] & 0x7FFFu);
+      amb = max(amb, (v[e] >> 16) & 0x7FFFu);
+    }
+  }
+  // inf / NaN bit patterns compare largest and propagate through the division as in the reference
+  const float sc = round_bf16(fmaxf(bf16f((uint16_t)amb), kBf16OneEMinus8) / 7.0f);
+  const uint32_t sb = __float_as_uint(sc) >> 16;
+  if (sx_pairs) reinterpret_cast<uint32_t*>(sx)[(long)g * M + m] = sb * 0x10001u;
+  else sx[m * ngroups + g] = (uint16_t)sb;
+  uint8_t* dst = qa + m * K + (long)g * G;
+  uint8_t* pk = qx ? qx + m * (K / 2) + (long)g * G / 2 : nullptr;
+  for (int c = 0; c < G; c += 8) {
+    const u32x4 v = ld16(src + c);
+    int q[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      q[2 * e] = (int)fminf(fmaxf(__builtin_rintf(bf16lo(v[e]) / sc), -8.0f), 7.0f);
+      q[2 * e + 1] = (int)fminf(fmaxf(__builtin_rintf(bf16hi(v[e]) / sc), -8.0f), 7.0f);
+    }
+    // operand bytes: even columns first, then odd (the layout of the fast kernels' int8 operand)
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lo |= (uint32_t)(uint8_t)(int8_t)(16 * q[2 * e]) << (8 * e);
+      hi |= (uint32_t)(uint8_t)(int8_t)(16 * q[2 * e + 1]) << (8 * e);
+    }
+    *reinterpret_cast<u32x2*>(dst + c) = u32x2{lo, hi};
+    if (pk) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w |= (uint32_t)(q[e] + 8) << (4 * e);
+      *reinterpret_cast<uint32_t*>(pk + c / 2) = w;
+    }
+  }
+}
+
 // (s, RN(1/s)) in float32 for a bf16 smoothing vector: computed once per layer.
 __global__ void prepare_smooth_kernel(const uint16_t* __restrict__ s, float* __restrict__ srs, int K) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -421,6 +478,13 @@ hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, in
 hipError_t launch_mid_finalize(const float* part, int S, int M, int RTp, uint16_t* midp, hipStream_t st) {
   const long n = (long)M * (RTp / 8);
   mid_finalize_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(part, S, M, RTp, midp);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_any_group(const uint16_t* xhat, long ldxh, int M, int K, int G, uint8_t* qa, uint16_t* sx,
+                                  int sx_pairs, uint8_t* qx, hipStream_t st) {
+  const long n = (long)M * (K / G);
+  quant_any_group_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(xhat, ldxh, M, K, G, qa, sx, sx_pairs, qx);
   return hipGetLastError();
 }
 

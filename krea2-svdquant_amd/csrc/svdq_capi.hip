@@ -34,9 +34,19 @@ int launched(hipError_t e, const char* what) {
   return ok();
 }
 
+bool fast_group(int group) { return group == 64 || group == 128; }
+
+// The group size the activation kernel runs with: the layer's own for 64 / 128; 64 for the generic
+// path (the kernel then writes x_hat and the down projections only, which do not depend on the
+// group, and the generic quantizer reads x_hat).
+int kernel_group(int group) { return fast_group(group) ? group : 64; }
+
 int check_group(int group, int K) {
-  if (!svdq_group_supported(group)) return fail(SVDQ_ERR_UNSUPPORTED, "group size %d has no kernel (64 or 128)", group);
+  if (!svdq_group_supported(group))
+    return fail(SVDQ_ERR_UNSUPPORTED, "group size %d has no kernel (64, 128, or a multiple of 16)", group);
   if (K <= 0 || K % group != 0) return fail(SVDQ_ERR_SHAPE, "K=%d must be a positive multiple of group=%d", K, group);
+  if (!fast_group(group) && K % 64 != 0)
+    return fail(SVDQ_ERR_SHAPE, "K=%d: group size %d needs K %% 64 == 0", K, group);
   return SVDQ_OK;
 }
 
@@ -50,7 +60,7 @@ const char* svdq_version(void) { return "svdq_gfx950 0.1.0"; }
 
 const char* svdq_last_error(void) { return g_last_error.c_str(); }
 
-int svdq_group_supported(int group) { return group == 64 || group == 128; }
+int svdq_group_supported(int group) { return group > 0 && group % 16 == 0; }
 
 int svdq_prepare_smooth(const void* smooth, float* srs, int K, hipStream_t stream) {
   if (!smooth || !srs) return fail(SVDQ_ERR_ARG, "prepare_smooth: null pointer");
@@ -63,7 +73,7 @@ int svdq_act_quant_workspace(int M, int K, int group, int RTp, int* splits, int6
   if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant_workspace: M=%d", M);
   if (int e = check_group(group, K)) return e;
   if (RTp <= 0 || RTp % 32) return fail(SVDQ_ERR_SHAPE, "RTp=%d must be a positive multiple of 32", RTp);
-  const int s = svdq::act_splits(M, K, group);
+  const int s = svdq::act_splits(M, K, kernel_group(group));
   if (splits) *splits = s;
   if (mid_floats) *mid_floats = (int64_t)(s + 1) * M * RTp;
   return ok();
@@ -91,10 +101,19 @@ int act_quant_run(const void* x, int64_t ldx, const float* srs, const void* l2, 
   if (packed && !quant) return fail(SVDQ_ERR_ARG, "act_quant: PACKED needs an operand format");
   const bool pairs = flags & SVDQ_ACT_SX_PAIRS;
   if (pairs && !quant) return fail(SVDQ_ERR_ARG, "act_quant: SX_PAIRS needs an operand format");
-  if ((i8 || e3m2) && want_xhat)
-    return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: XHAT with int8 or e3m2 operands has no kernel");
   if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant: M=%d", M);
   if (int e = check_group(group, K)) return e;
+  const bool generic = !fast_group(group);
+  if (generic) {
+    // the generic path: int8 operand codes, quantized from the x_hat the caller's buffer receives
+    if (e4m3 || e3m2)
+      return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: group size %d has int8 operands only (SVDQ_ACT_OPERAND_I8)", group);
+    if (i8 && !want_xhat)
+      return fail(SVDQ_ERR_ARG, "act_quant: group size %d quantizes from x_hat: add SVDQ_ACT_XHAT and an xhat buffer",
+                  group);
+  } else if ((i8 || e3m2) && want_xhat) {
+    return fail(SVDQ_ERR_UNSUPPORTED, "act_quant: XHAT with int8 or e3m2 operands has no kernel");
+  }
   if (r < 1 || rl < 0) return fail(SVDQ_ERR_SHAPE, "act_quant: rank r=%d rl=%d", r, rl);
   if (RTp % 32 || RTp < r + rl) return fail(SVDQ_ERR_SHAPE, "act_quant: RTp=%d (r=%d rl=%d)", RTp, r, rl);
   const int nt = mid_tiles(r, rl);   // MFMA column tiles of the down projections (any number)
@@ -127,7 +146,7 @@ int act_quant_run(const void* x, int64_t ldx, const float* srs, const void* l2, 
   p.xhat = static_cast<uint16_t*>(xhat);
   p.ldxh = ldxh;
   p.mid = part;
-  const int ngroups = K / group;
+  const int ngroups = K / kernel_group(group);   // the act kernel's groups
   p.gps = (ngroups + splits - 1) / splits;
   p.exact = (flags & SVDQ_ACT_EXACT_DIV) ? 1 : 0;
   p.sx_pairs = pairs ? 1 : 0;
@@ -135,10 +154,25 @@ int act_quant_run(const void* x, int64_t ldx, const float* srs, const void* l2, 
   // more tiles of the down projections (rank + LoRA rank beyond 128), into their own columns of
   // the split partials.
   p.t0 = 0;
-  if (int e = launched(svdq::launch_act(p, group, nt < 4 ? nt : 4, e4m3 ? 1 : (i8 ? 2 : (e3m2 ? 3 : 0)), want_xhat,
-                                        splits, stream),
-                       "act_quant"))
+  if (generic) {   // x_hat and the first tiles, then the group-size-generic quantizer from x_hat
+    svdq::ActParams q = p;
+    q.qa = nullptr;
+    q.sx = nullptr;
+    q.qx = nullptr;
+    if (int e = launched(svdq::launch_act(q, kernel_group(group), nt < 4 ? nt : 4, 0, true, splits, stream),
+                         "act_quant"))
+      return e;
+    if (i8) {
+      if (int e = launched(svdq::launch_quant_any_group(p.xhat, ldxh, M, K, group, p.qa, p.sx, pairs ? 1 : 0, p.qx,
+                                                        stream),
+                           "act_quant (any-group quantizer)"))
+        return e;
+    }
+  } else if (int e = launched(svdq::launch_act(p, group, nt < 4 ? nt : 4, e4m3 ? 1 : (i8 ? 2 : (e3m2 ? 3 : 0)),
+                                               want_xhat, splits, stream),
+                              "act_quant")) {
     return e;
+  }
   for (int t0 = 4; t0 < nt; t0 += 4) {
     svdq::ActParams q = p;
     q.t0 = t0;
@@ -146,7 +180,7 @@ int act_quant_run(const void* x, int64_t ldx, const float* srs, const void* l2, 
     q.sx = nullptr;
     q.qx = nullptr;
     q.xhat = nullptr;
-    if (int e = launched(svdq::launch_act(q, group, nt - t0 < 4 ? nt - t0 : 4, 0, false, splits, stream),
+    if (int e = launched(svdq::launch_act(q, kernel_group(group), nt - t0 < 4 ? nt - t0 : 4, 0, false, splits, stream),
                          "act_quant (down projections)"))
       return e;
   }
@@ -192,7 +226,7 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
                    int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
                    float* mid, int splits, hipStream_t stream) {
   if (M > 0 && group > 0 && K > 0 && K % group == 0) {
-    const int expect = svdq::act_splits(M, K, group);
+    const int expect = svdq::act_splits(M, K, kernel_group(group));
     if (splits != expect) return fail(SVDQ_ERR_ARG, "act_quant: splits=%d, workspace says %d", splits, expect);
   }
   float* part = mid ? mid + (int64_t)(M > 0 ? M : 0) * (RTp > 0 ? RTp : 0) : nullptr;   // partials after the head
@@ -207,7 +241,7 @@ int svdq_act_quant_noalloc(const void* x, int64_t ldx, const float* srs, const v
   if (M <= 0) return fail(SVDQ_ERR_ARG, "act_quant_noalloc: M=%d", M);
   if (int e = check_group(group, K)) return e;
   if (RTp <= 0 || RTp % 32) return fail(SVDQ_ERR_SHAPE, "act_quant_noalloc: RTp=%d must be a positive multiple of 32", RTp);
-  const int splits = svdq::act_splits(M, K, group);
+  const int splits = svdq::act_splits(M, K, kernel_group(group));
   const int64_t need = (int64_t)splits * M * RTp;
   if (need > kScratchFloats)
     return fail(SVDQ_ERR_SHAPE,
@@ -317,7 +351,7 @@ int svdq_w4a4_gemm_epi(const void* qa, int operand, const void* sxp, const void*
     return fail(SVDQ_ERR_ALIGN, "w4a4_gemm: qa, qwe must be 16-byte aligned, sxp, swp 4-byte aligned");
   // The 8-bit kernels address qa and qwe with 32-bit byte offsets (the e3m2 kernel with 64-bit
   // plane bases and 32-bit row offsets).
-  if (operand != SVDQ_OPERAND_E3M2 &&
+  if (operand != SVDQ_OPERAND_E3M2 && fast_group(group) &&
       ((int64_t)M * K > INT32_MAX || (int64_t)N * K > INT32_MAX || (int64_t)M * (K / group) * 4 > INT32_MAX ||
        (int64_t)N * (K / group) * 4 > INT32_MAX))
     return fail(SVDQ_ERR_SHAPE, "w4a4_gemm: M*K=%lld or N*K=%lld exceeds 2^31-1 bytes; split the call",
@@ -328,6 +362,13 @@ int svdq_w4a4_gemm_epi(const void* qa, int operand, const void* sxp, const void*
   p.sxp = static_cast<const uint32_t*>(sxp);
   p.swp = static_cast<const uint32_t*>(swp);
   set_epi(p, epi, aux, ldaux, vec);
+  if (!fast_group(group)) {
+    if (operand != SVDQ_OPERAND_I8)
+      return fail(SVDQ_ERR_UNSUPPORTED, "w4a4_gemm: group size %d has int8 operands only (SVDQ_OPERAND_I8)", group);
+    if (epi != SVDQ_EPI_NONE)
+      return fail(SVDQ_ERR_UNSUPPORTED, "w4a4_gemm: group size %d has no fused epilogue ops", group);
+    return launched(svdq::launch_w4a4_any_group(p, group, out_f32 == 1, stream), "w4a4_gemm (any group)");
+  }
   return launched(svdq::launch_w4a4(p, group, operand, out_f32 == 1, stream), "w4a4_gemm");
 }
 

@@ -984,6 +984,8 @@ __global__ void weight_scale_pairs_kernel(const uint16_t* __restrict__ sw, uint3
 // RNE pack) -- with one barrier per stage.  LDS rows are 64 bf16 plus 16 bytes of padding (144-byte
 // pitch): the fragment reads (16 lanes on 16 consecutive rows) and the staging writes hit
 // distinct bank groups.
+// G = 0: the group size comes at run time (p.group; any multiple of 16): a thread's 16 codes of a
+// stage always lie in one group, so each still needs one scale per stage.
 template <int G, int WM, bool OUT_F32, bool EPI = false>
 __global__ void __launch_bounds__(WM * 128, 1) w4a16_kernel(GemmParams p) {
   constexpr int NT = WM * 128;                // threads
@@ -1003,7 +1005,8 @@ __global__ void __launch_bounds__(WM * 128, 1) w4a16_kernel(GemmParams p) {
   int bm, bn;
   tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
   const int m0 = bm * TBM, n0 = bn * TBN;
-  const int K = p.K, ngroups = K / G, kp = K / 2, nst = K / KB;
+  const int GS = G > 0 ? G : p.group;         // group size
+  const int K = p.K, ngroups = K / GS, kp = K / 2, nst = K / KB;
 
   // staging assignments: A chunk (row, 16-byte chunk) = (idx / 8, idx % 8), idx = tid + NT * i;
   // weights: row tid / 4 (+ BROWS per pass), 16 codes = chunks 2 (tid % 4) and 2 (tid % 4) + 1
@@ -1046,7 +1049,7 @@ __global__ void __launch_bounds__(WM * 128, 1) w4a16_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < BLD; ++i) {
       asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(db[i]) : "v"(brow[i] + k0 / 2) : "memory");
-      asm volatile("global_load_ushort %0, %1, off" : "=v"(ds[i]) : "v"(bsc[i] + k0 / G) : "memory");
+      asm volatile("global_load_ushort %0, %1, off" : "=v"(ds[i]) : "v"(bsc[i] + (k0 + 16 * bq) / GS) : "memory");
     }
   };
   auto gload = [&](int st, auto q_c) {
@@ -1331,7 +1334,107 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
   }
 }
 
+// W4A4 GEMM for group sizes other than 64 / 128 (any multiple of 16 dividing K): the generic path.
+// Operands are the int8 codes 16 q (SVDQ_OPERAND_I8 layout: within each chunk of 8 columns the even
+// columns, then the odd ones, identically for activations and weights, so the order cancels).  K
+// advances 16 columns per v_mfma_i32_32x32x16_i8 (lanes 0-31 supply one 8-column chunk of a row,
+// lanes 32-63 the next), accumulating the exact group sum P in int32; at every group boundary
+// acc += f32(P) * S with S = sx (x) sw on a bf16 MFMA (K = 2: (sx, sx) against (hi, lo) of sw, the
+// 1/256 of the int8 operands folded into the weight pair as in the fast kernels) and P is reset.
+// Block tile 128 x 128 on 4 waves (wave tile 64 x 64), 64-column stages through LDS (rows padded
+// to 80 bytes), one stage at a time.
+template <bool OUT_F32>
+__global__ void __launch_bounds__(256, 2) w4a4_any_group_kernel(GemmParams p, int G) {
+  constexpr int TBM = 128, TBN = 128, KB = 64, PITCH = KB + 16;
+  // one buffer: the two operand tiles during the main loop (20 KB), then 4 KB of output staging
+  // per wave (16 KB) in the epilogue
+  constexpr int LDS_BYTES = (TBM + TBN) * PITCH;
+  static_assert(LDS_BYTES >= 4 * 4096, "epilogue staging");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+  uint8_t* sA = lds;
+  uint8_t* sB = lds + TBM * PITCH;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
+  int bm, bn;
+  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
+  const int m0 = bm * TBM, n0 = bn * TBN;
+  const int K = p.K;
+  f32x16 acc[2][2];
+  i32x16 P[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      acc[i][j] = f32x16{};
+      P[i][j] = i32x16{};
+    }
+  for (int k0 = 0; k0 < K; k0 += KB) {
+    // stage: 128 rows x 64 bytes of each operand, 16 bytes per thread and operand, twice
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int idx = tid + 256 * it, r = idx >> 2, c = idx & 3;
+      *reinterpret_cast<u32x4*>(&sA[r * PITCH + 16 * c]) =
+          ld16(p.qa + (long)min(m0 + r, p.M - 1) * K + k0 + 16 * c);
+      *reinterpret_cast<u32x4*>(&sB[r * PITCH + 16 * c]) =
+          ld16(p.qwe + (long)min(n0 + r, p.N - 1) * K + k0 + 16 * c);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < KB / 16; ++kk) {
+      long a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a[i] = *reinterpret_cast<const long*>(&sA[(64 * wm + 32 * i + lr) * PITCH + 16 * kk + 8 * h]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        b[j] = *reinterpret_cast<const long*>(&sB[(64 * wn + 32 * j + lr) * PITCH + 16 * kk + 8 * h]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) P[i][j] = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[i], b[j], P[i][j], 0, 0, 0);
+      const int kend = k0 + 16 * kk + 16;
+      if (kend % G == 0) {   // group boundary: rescale the exact group sums into acc
+        const int g = kend / G - 1;
+        u32x4 xop[2], wop[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int m = min(m0 + 64 * wm + 32 * i + lr, p.M - 1);
+          xop[i] = u32x4{h ? 0u : p.sxp[(long)g * p.M + m], 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = min(n0 + 64 * wn + 32 * j + lr, p.N - 1);
+          wop[j] = u32x4{h ? 0u : p.swp[(long)g * p.N + n], 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const f32x16 S = mfma_bf16_32x32x16(xop[i], wop[j], f32x16{});
+            const f32x16 pf = __builtin_convertvector(P[i][j], f32x16);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(pf[r], S[r], acc[i][j][r]);
+            P[i][j] = i32x16{};
+          }
+      }
+    }
+    __syncthreads();
+  }
+  // the operand buffers stage the output (4 KB per wave; the last barrier above ended their use)
+  epilogue<OUT_F32>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, lds + wave * 4096);
+}
+
 }  // namespace
+
+hipError_t launch_w4a4_any_group(const GemmParams& p, int G, bool out_f32, hipStream_t st) {
+  if (G <= 0 || G % 16 || p.K % G || p.K % 64) return hipErrorInvalidValue;
+  const dim3 grid(((p.M + 127) / 128) * ((p.N + 127) / 128));
+  if (out_f32) w4a4_any_group_kernel<true><<<grid, 256, 0, st>>>(p, G);
+  else w4a4_any_group_kernel<false><<<grid, 256, 0, st>>>(p, G);
+  return hipGetLastError();
+}
 
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st) {
   const dim3 grid(((p.M + 255) / 256) * ((p.N + 127) / 128));
@@ -1392,6 +1495,17 @@ hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, 
 }
 
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st) {
+  if (G != 64 && G != 128) {
+    // other group sizes (multiples of 16 dividing K): the 128 x 128 kernel with a run-time group
+    if (G <= 0 || G % 16 || p.K % G || p.K % 64) return hipErrorInvalidValue;
+    GemmParams q = p;
+    q.group = G;
+    const dim3 grid(((p.M + 127) / 128) * ((p.N + 127) / 128));
+    if (out_f32) w4a16_kernel<0, 2, true><<<grid, 256, 0, st>>>(q);
+    else if (p.epi) w4a16_kernel<0, 2, false, true><<<grid, 256, 0, st>>>(q);
+    else w4a16_kernel<0, 2, false><<<grid, 256, 0, st>>>(q);
+    return hipGetLastError();
+  }
   // 256 x 256 tiles (one wave per SIMD) when they cover the chip at least half, else 128 x 128
   // tiles (two workgroups of 4 waves per CU)
   const long nbn = (p.N + 255) / 256;

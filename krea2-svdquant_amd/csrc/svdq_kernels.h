@@ -42,6 +42,7 @@ struct GemmParams {
   void* y;                  // [M, ldy] bf16 or f32
   long ldy;
   int M, N, K;
+  int group;                // run-time group size (the kernels templated on G = 0)
   // Elementwise op on the bf16-rounded output (bf16 output only): 0 none, 1 aux * sigmoid(y),
   // 2 silu(aux) * y, 3 aux + evec[n] * y, each intermediate rounded to bf16 as torch does.
   int epi;
@@ -60,6 +61,10 @@ hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, in
 // operand midp [M, 2, RTp] (bf16 hi plane, then bf16 lo plane, hi + lo within 2^-18 of the f32 sum, relative).
 hipError_t launch_mid_finalize(const float* part, int S, int M, int RTp, uint16_t* midp, hipStream_t st);
 hipError_t launch_prepare_smooth(const uint16_t* s, float* srs, int K, hipStream_t st);
+// A4 codes and scales for any group size G (multiple of 16 dividing K) from x_hat: int8 operand
+// (16 q) [M, K], scales bf16 [M, K/G] or u32 pairs [K/G, M], packed codes [M, K/2] if qx
+hipError_t launch_quant_any_group(const uint16_t* xhat, long ldxh, int M, int K, int G, uint8_t* qa, uint16_t* sx,
+                                  int sx_pairs, uint8_t* qx, hipStream_t st);
 // mode: 0 = e4m3 operands on the FP8 MFMA, 1 = int8 operands on the INT8 MFMA, 2 = e3m2 planar
 // operands on the FP6 MFMA
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st);
@@ -68,5 +73,7 @@ hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, int n, i
 // bytes per row)
 hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, int mode, hipStream_t st);
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st);
+// W4A4 GEMM for any group size G (multiple of 16 dividing K): int8 operands (SVDQ_OPERAND_I8 layout)
+hipError_t launch_w4a4_any_group(const GemmParams& p, int G, bool out_f32, hipStream_t st);
 
 }  // namespace svdq

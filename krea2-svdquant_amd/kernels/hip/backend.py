@@ -28,6 +28,11 @@ from ...quant.state import SVDQuantLinearState
 from . import ops
 
 
+FAST_GROUPS = (64, 128)
+"""Group sizes with the tuned kernels; any other multiple of 16 dividing K takes the generic
+kernels (int8 operands, K in steps of 16, a rescale at every group boundary)."""
+
+
 @dataclass
 class PreparedLayer:
     """Device-resident per-layer operands of the two kernels."""
@@ -180,6 +185,7 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
 
     ``operand`` picks the W4A4 MFMA: ``"e3m2"`` (FP6 MFMA, default: twice the FP8 rate),
     ``"e4m3"`` (FP8 MFMA) or ``"i8"`` (INT8 MFMA); all compute the same exact integer group sums.
+    Layers whose group size is not 64 or 128 always take the generic int8 kernels.
     ``epilogue`` fuses an elementwise op into the GEMM's bf16 store (o = the layer output, bf16
     rounding after every op as with the unfused torch ops): ``"mul_sigmoid"`` gives
     ``aux * sigmoid(o)``, ``"silu_mul"`` gives ``silu(aux) * o`` and ``"residual_gate"`` gives
@@ -202,8 +208,12 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
         if operand not in ops.OPERAND_NAMES:
             raise ValueError(f"operand must be 'e4m3', 'e3m2' or 'i8', got {operand!r}")
         opc = ops.OPERAND_NAMES[operand]
+        generic = prep.group_size not in FAST_GROUPS
+        if generic:
+            # group sizes other than 64 / 128: the generic kernels, int8 operands quantized from x_hat
+            opc = ops.OPERAND_I8
         qa, sx, _, _, mid = ops.act_quant(x2, prep.srs, prep.l2, prep.lora_down, prep.lora_mult,
-                                          prep.group_size, prep.rtp, opc, False, False, exact_div, True)
+                                          prep.group_size, prep.rtp, opc, False, generic, exact_div, True)
         y = ops.w4a4_gemm(qa, sx, prep.weight_operand(opc), prep.weight_scale_pairs(opc), mid, prep.l1cat,
                           prep.bias, prep.group_size, opc, out_f32, epi, aux2, vec2)
     elif mode == "w4a16":

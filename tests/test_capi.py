@@ -28,7 +28,9 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_group_support_and_workspace_sizing():
     h = lib.load()
     assert h.svdq_group_supported(64) == 1 and h.svdq_group_supported(128) == 1
-    assert h.svdq_group_supported(32) == 0
+    # any other multiple of 16 takes the generic kernels
+    assert h.svdq_group_supported(32) == 1 and h.svdq_group_supported(16) == 1 and h.svdq_group_supported(192) == 1
+    assert h.svdq_group_supported(24) == 0 and h.svdq_group_supported(0) == 0
     s, mp = ctypes.c_int(), ctypes.c_int64()
     lib.call("svdq_act_quant_workspace", 4096, 6144, 64, 32, ctypes.byref(s), ctypes.byref(mp))
     assert s.value >= 1 and mp.value == (s.value + 1) * 4096 * 32   # finalized head + one partial per split
@@ -37,7 +39,8 @@ def test_group_support_and_workspace_sizing():
 
 
 @pytest.mark.parametrize("args,status,needle", [
-    ((4096, 6144, 32, 32), -4, "group size 32"),
+    ((4096, 6144, 24, 32), -4, "group size 24"),
+    ((4096, 6160, 16, 32), -2, "K % 64"),            # generic group sizes need K % 64 == 0
     ((4096, 6100, 64, 32), -2, "multiple of group"),
     ((4096, 6144, 64, 48), -2, "RTp=48"),
     ((0, 6144, 64, 32), -1, "M=0"),
@@ -127,7 +130,7 @@ def test_gemm_epilogue_ops_rejected_before_any_launch(fn, epi, out_f32, aux, lda
     (40000, 6144, 64, 128, -2, "device scratch"),   # 1 split x 40000 x 128 floats > 4 Mi floats
     (0, 6144, 64, 32, -1, "M=0"),
     (4096, 6144, 64, 40, -2, "RTp=40"),
-    (4096, 6144, 48, 32, -4, "group size 48"),
+    (4096, 6144, 40, 32, -4, "group size 40"),
 ])
 def test_act_quant_noalloc_rejects_before_any_launch(m, k, g, rtp, status, needle):
     """The no-allocation entry point refuses a split-partial buffer beyond its device scratch
@@ -141,3 +144,24 @@ def test_act_quant_noalloc_rejects_before_any_launch(m, k, g, rtp, status, needl
     if m > 0 and rtp % 32 == 0 and g == 64:
         lib.call("svdq_act_quant_workspace", m, k, g, rtp, ctypes.byref(splits), None)
         assert splits.value * m * rtp > lib.SVDQ_ACT_NOALLOC_MAX_FLOATS
+
+
+def test_generic_group_rejects_fast_only_formats_before_any_launch():
+    """Group sizes other than 64 / 128 run the generic kernels: int8 operands only, quantized from
+    x_hat (the caller passes SVDQ_ACT_XHAT), and no fused epilogue ops."""
+    fake, nul = ctypes.c_void_p(0x1000), None
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_act_quant", fake, 128, fake, fake, 32, nul, 0, nul, 64, 128, 32, 32,
+                 lib.SVDQ_ACT_OPERAND_E3M2 | lib.SVDQ_ACT_SX_PAIRS, fake, fake, nul, nul, 0, fake, 1, nul)
+    assert ei.value.status == -4 and "int8 operands only" in str(ei.value)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_act_quant", fake, 128, fake, fake, 32, nul, 0, nul, 64, 128, 32, 32,
+                 lib.SVDQ_ACT_OPERAND_I8 | lib.SVDQ_ACT_SX_PAIRS, fake, fake, nul, nul, 0, fake, 1, nul)
+    assert ei.value.status == -1 and "SVDQ_ACT_XHAT" in str(ei.value)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a4_gemm", fake, 2, fake, fake, fake, fake, fake, 32, nul, 128, 128, 128, 32, fake, 128, 0, nul)
+    assert ei.value.status == -4 and "int8 operands only" in str(ei.value)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a4_gemm_epi", fake, 1, fake, fake, fake, fake, fake, 32, nul, 128, 128, 128, 32, fake, 128,
+                 0, lib.SVDQ_EPI_SILU_MUL, fake, 128, nul, nul)
+    assert ei.value.status == -4 and "epilogue" in str(ei.value)
