@@ -31,41 +31,102 @@ __device__ __forceinline__ float ubyte_f32(uint32_t v) { return (float)((v >> (8
 
 
 
+// a / d for d >= 1 where it rounds to the same bf16 as the IEEE float quotient RN(a / d); *exact
+// is cleared where that is not shown and the caller must divide.  The product f = a * v_rcp_f32(d)
+// lies within 2 ulps of a / d (1 ulp for the reciprocal, 1/2 for the product) and so within 3 of
+// RN(a / d); bf16 rounding is monotone and changes only where the low 16 bits cross 0x8000, so
+// when f's low 16 bits are more than 8 away from 0x8000 both round to the same bf16.  Not shown:
+// d >= 2^100, |a| >= 2^100, inf / NaN, and results below 2^-100 (the reciprocal may leave the
+// normal range).
+__device__ __forceinline__ float div_bf16_fast(float a, float d, bool& exact) {
+  const float f = a * __builtin_amdgcn_rcpf(d);
+  const uint32_t lo = __float_as_uint(f) & 0xFFFFu;
+  // bitwise & / |: the conditions evaluate branch-free
+  exact = (d < 0x1p100f) & (fabsf(a) < 0x1p100f) & ((fabsf(f) >= 0x1p-100f) | (a == 0.0f)) & (lo - 0x7FF8u > 16u);
+  return f;
+}
+
 // GemmParams::epi on one element: y = the bf16-rounded layer output, a = the aux element, g = the
 // column's evec element.  Each op rounds its result to bf16 as the unfused torch ops on bf16
 // tensors do (float math inside one op, bf16 out): sigmoid and silu as 1 / (1 + exp(-v)) and
 // v / (1 + exp(-v)) in float, the gated residual in one step as torch.addcmul.  The caller rounds
 // the returned value.
+// epi 1 and 2 are evaluated for a chunk of 8 elements at a time by epi_apply_op.
 __device__ __forceinline__ float epi_op(int epi, float y, float a, float g) {
   if (epi == 1) return a * round_bf16(1.0f / (1.0f + expf(-y)));   // a * sigmoid(y)
   if (epi == 2) return round_bf16(a / (1.0f + expf(-a))) * y;      // silu(a) * y
   return __builtin_fmaf(g, y, a);                                   // addcmul(a, g, y)
 }
 
-// epi on a chunk of 8 bf16 outputs (row m, columns n..n+7; columns >= N are left as they are);
-// aux and evec by 16-byte loads when their layout allows, else element by element.
-__device__ __forceinline__ u32x4 epi_chunk(const GemmParams& p, u32x4 v, int m, int n) {
-  const uint16_t* ar = p.aux + (long)m * p.ldaux + n;
-  u32x4 a, g = u32x4{};
-  if (p.aux_vec && n + 8 <= p.N) {
-    a = ld16(ar);
-    if (p.epi == 3) g = ld16(p.evec + n);
+// epi on a chunk of 8 bf16 outputs v with their aux elements a and evec elements g.  The op is
+// chosen once per chunk, so each op's code appears once per call site.
+// For the sigmoid and silu quotients the 8 reciprocal products come first, branch-free; only
+// when one of the lane's 8 is not shown exact does the lane divide (all 8, keeping the
+// reciprocal products that were exact).
+template <int E>
+__device__ __forceinline__ u32x4 epi_apply_op(u32x4 v, u32x4 a, u32x4 g) {
+  float y[8], x[8];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    y[2 * d] = bf16lo(v[d]);
+    y[2 * d + 1] = bf16hi(v[d]);
+    x[2 * d] = bf16lo(a[d]);
+    x[2 * d + 1] = bf16hi(a[d]);
+  }
+  float o[8];
+  if constexpr (E == 3) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = epi_op(3, y[e], x[e], e % 2 ? bf16hi(g[e / 2]) : bf16lo(g[e / 2]));
   } else {
-    a = u32x4{};
-    for (int e = 0; e < min(8, p.N - n); ++e) {
-      a[e / 2] |= (uint32_t)ar[e] << (16 * (e % 2));
-      if (p.epi == 3) g[e / 2] |= (uint32_t)p.evec[n + e] << (16 * (e % 2));
+    // sigmoid(y) = 1 / (1 + exp(-y)); silu(x) = x / (1 + exp(-x))
+    float num[8], den[8], q[8];
+    bool all = true;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      num[e] = E == 1 ? 1.0f : x[e];
+      den[e] = 1.0f + expf(-(E == 1 ? y[e] : x[e]));
+      bool ok;
+      q[e] = div_bf16_fast(num[e], den[e], ok);
+      all = all & ok;
     }
+    if (!all) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bool ok;
+        div_bf16_fast(num[e], den[e], ok);
+        if (!ok) q[e] = num[e] / den[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = E == 1 ? x[e] * round_bf16(q[e]) : round_bf16(q[e]) * y[e];
   }
 #pragma unroll
-  for (int d = 0; d < 4; ++d)
-    v[d] = pack_bf16x2(epi_op(p.epi, bf16lo(v[d]), bf16lo(a[d]), bf16lo(g[d])),
-                       epi_op(p.epi, bf16hi(v[d]), bf16hi(a[d]), bf16hi(g[d])));
+  for (int d = 0; d < 4; ++d) v[d] = pack_bf16x2(o[2 * d], o[2 * d + 1]);
   return v;
 }
+__device__ __forceinline__ u32x4 epi_apply(const GemmParams& p, u32x4 v, u32x4 a, u32x4 g) {
+  if (p.epi == 1) return epi_apply_op<1>(v, a, g);
+  if (p.epi == 2) return epi_apply_op<2>(v, a, g);
+  return epi_apply_op<3>(v, a, g);
+}
 
-// acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store (directly, or through the
-// wave's 4 KB LDS region `stage` when it is given).  mid is the activation
+// Whether the chunk of 8 outputs at columns n..n+7 takes its aux / evec by 16-byte loads.
+__device__ __forceinline__ bool epi_vec(const GemmParams& p, int n) { return p.aux_vec && n + 8 <= p.N; }
+
+// aux and evec elements of the chunk at (m, n..n+7) loaded element by element (the chunks
+// epi_vec rejects; columns >= N read as 0 and are not stored).
+__device__ __forceinline__ void epi_load_elems(const GemmParams& p, int m, int n, u32x4& a, u32x4& g) {
+  const uint16_t* ar = p.aux + (long)m * p.ldaux + n;
+  a = u32x4{};
+  g = u32x4{};
+  for (int e = 0; e < min(8, p.N - n); ++e) {
+    a[e / 2] |= (uint32_t)ar[e] << (16 * (e % 2));
+    if (p.epi == 3) g[e / 2] |= (uint32_t)p.evec[n + e] << (16 * (e % 2));
+  }
+}
+
+// acc (2x2 sub-tiles of the wave) += mid @ l1cat^T, + bias, then store through the wave's 4 KB
+// LDS region `stage` (coalesced 16-byte row chunks).  mid is the activation
 // pass's finalized operand, bf16 hi and lo planes per row ([M, 2, RTp]); both planes go through
 // the bf16 MFMA, so the low-rank term carries the f32 mid to 2^-18.  Two 16-column steps per
 // iteration, their twelve loads issued together (one memory latency per 32 columns of RTp).
@@ -76,6 +137,24 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
                                          int mlim = 0x7FFFFFFF) {
   const int RTp = p.RTp;
   const int mend = min(p.M, mlim);   // rows m >= mend are not stored (past M, or another wave's)
+  // Staged bf16 stores with an elementwise op: the aux chunks of the lane's 8 output chunks (and
+  // its evec chunk) are loaded here, ahead of the low-rank MFMAs, so that one memory latency
+  // covers them all.  Left to the store loop, each load would wait behind the previous chunk's
+  // store (the compiler must assume aux and y may overlap) and the tile would pay 8 latencies.
+  // Lane (h, lr) stores chunk c = lr % 8 of rows 8 it + 4 h + lr / 8 in each 32-row pass.
+  constexpr bool PRE = EPI && !OUT_F32;
+  u32x4 apre[PRE ? 8 : 1], gpre = u32x4{};
+  if constexpr (PRE) {
+    const int n = n0 + 8 * (lr & 7);
+    if (epi_vec(p, n)) {
+      if (p.epi == 3) gpre = ld16(p.evec + n);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int m = m0 + 32 * (u >> 2) + 8 * (u & 3) + 4 * h + (lr >> 3);
+        apre[u] = m < mend ? ld16(p.aux + (long)m * p.ldaux + n) : u32x4{};
+      }
+    }
+  }
   if (lmid != nullptr) {
     // RTp == 32, operands prefetched into LDS by the GEMM's last stage: the tile's mid rows
     // (128 bytes: hi plane, lo plane; 16-byte chunk c of row r at c ^ ((r >> 1) & 7)) and l1cat
@@ -144,30 +223,6 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
     const int n = n0 + 32 * j + lr;
     bv[j] = p.bias && n < p.N ? bf16f(p.bias[n]) : 0.0f;
   }
-  if (stage == nullptr) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + 32 * j + lr;
-      if (n >= p.N) continue;
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (m >= mend) continue;
-          float v = acc[i][j][r] + bv[j];
-          if (OUT_F32) {
-            reinterpret_cast<float*>(p.y)[(long)m * p.ldy + n] = v;
-          } else {
-            if (EPI)
-              v = epi_op(p.epi, round_bf16(v), bf16f(p.aux[(long)m * p.ldaux + n]),
-                         p.epi == 3 ? bf16f(p.evec[n]) : 0.0f);
-            reinterpret_cast<uint16_t*>(p.y)[(long)m * p.ldy + n] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
-          }
-        }
-    }
-    return;
-  }
   // Staged: in passes of 4 KB (32 rows of bf16, 16 rows of f32 out of the wave's 64), the values
   // go to the wave's LDS region (rows of 64 values; 16-byte chunk c of row r at c ^ (CPR / 2) when
   // (r >> 2) is odd, so the two half-waves, 4 rows apart, write disjoint banks) and come back as
@@ -192,14 +247,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
         if (OUT_F32) *reinterpret_cast<float*>(dst) = v;
         else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
       }
-#pragma unroll
-    for (int it = 0; it < RP * CPR / 64; ++it) {
-      const int idx = 64 * it + (h << 5 | lr), row = idx / CPR, c = idx % CPR;
-      const int pos = c ^ ((row >> 2) & 1 ? CPR / 2 : 0);
-      u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * (64 * ES) + pos * 16);
-      const int m = m0 + 32 * i + rq + row, n = n0 + c * VPC;
-      if (m >= mend) continue;
-      if (!OUT_F32 && EPI) v = epi_chunk(p, v, m, n);
+    auto put = [&](u32x4 v, int m, int n) {
       uint8_t* out = reinterpret_cast<uint8_t*>(p.y) + ((long)m * p.ldy + n) * ES;
       if (vec && n + VPC <= p.N) {
         st16(out, v);
@@ -210,6 +258,37 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, f32x16 (&acc)[2][2
           if (OUT_F32) reinterpret_cast<uint32_t*>(out)[e] = v[e];
           else reinterpret_cast<uint16_t*>(out)[e] = (uint16_t)(v[e / 2] >> (16 * (e % 2)));
         }
+      }
+    };
+    if constexpr (PRE) {
+      // A loop kept rolled over the pass's 4 chunks, so that the op's code appears once per pass
+      // (unrolled, the epilogue's code outgrew the instruction cache); the prefetched aux
+      // chunks move down one register per chunk.
+      static_assert(CPR == 8 && VPC == 8 && RP == 32, "bf16 passes");
+      u32x4 a0 = apre[4 * q], a1 = apre[4 * q + 1], a2 = apre[4 * q + 2], a3 = apre[4 * q + 3];
+#pragma unroll 1
+      for (int it = 0; it < 4; ++it) {
+        const int row = 8 * it + 4 * h + (lr >> 3), c = lr & 7;
+        const int pos = c ^ ((row >> 2) & 1 ? CPR / 2 : 0);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * (64 * ES) + pos * 16);
+        const int m = m0 + 32 * i + rq + row, n = n0 + c * VPC;
+        if (m < mend) {
+          u32x4 a = a0, g = gpre;
+          if (!epi_vec(p, n)) epi_load_elems(p, m, n, a, g);
+          put(epi_apply(p, v, a, g), m, n);
+        }
+        a0 = a1;
+        a1 = a2;
+        a2 = a3;
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < RP * CPR / 64; ++it) {
+        const int idx = 64 * it + (h << 5 | lr), row = idx / CPR, c = idx % CPR;
+        const int pos = c ^ ((row >> 2) & 1 ? CPR / 2 : 0);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * (64 * ES) + pos * 16);
+        const int m = m0 + 32 * i + rq + row, n = n0 + c * VPC;
+        if (m < mend) put(v, m, n);
       }
     }
   }

@@ -122,3 +122,30 @@ def test_fused_standin_block_matches_unfused(dev):
     same = float((fused == unfused).float().mean())
     print(f"  fused vs unfused blocks: rel_l2 {err:.3e}, bit-equal {same:.4f}")
     assert err < 5e-3 and same > 0.9
+
+
+def test_fused_sigmoid_and_silu_bit_equal_to_torch_everywhere(dev):
+    """The store's sigmoid / silu quotients take a reciprocal product where it rounds to the same
+    bf16 as the IEEE quotient and the IEEE division elsewhere: bit-equal to torch's ops.
+    silu_mul over every finite bf16 aux value (a 256 x 256 grid of all bit patterns); mul_sigmoid
+    over 8M GEMM outputs of spread magnitude."""
+    from krea2_svdquant_amd.kernels.hip import backend
+    prep, gen = _layer(256, 128, dev, seed=21)
+    bits = torch.arange(65536, dtype=torch.int32, device=dev)
+    finite = (bits & 0x7F80) != 0x7F80
+    aux = torch.where(finite, bits, torch.zeros_like(bits)).to(torch.int16).view(torch.bfloat16).view(256, 256)
+    x = torch.randn(256, 128, device=dev, generator=gen).to(torch.bfloat16)
+    y = backend.forward_prepared(x, prep)
+    fused = backend.forward_prepared(x, prep, epilogue="silu_mul", aux=aux)
+    ref = F.silu(aux) * y
+    torch.cuda.synchronize()
+    assert torch.equal(fused, ref), f"silu_mul: {int((fused != ref).sum())} elements differ from torch"
+
+    prep, gen = _layer(16384, 128, dev, seed=22)
+    x = (torch.randn(512, 128, device=dev, generator=gen) * 40).to(torch.bfloat16)
+    aux = torch.randn(512, 16384, device=dev, generator=gen).to(torch.bfloat16)
+    y = backend.forward_prepared(x, prep)
+    fused = backend.forward_prepared(x, prep, epilogue="mul_sigmoid", aux=aux)
+    ref = aux * torch.sigmoid(y)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, ref), f"mul_sigmoid: {int((fused != ref).sum())} elements differ from torch"
