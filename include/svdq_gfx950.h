@@ -206,6 +206,24 @@ int svdq_w4a16_gemm_epi(const void* xhat, int64_t ldxh, const void* qw, const vo
                         int64_t ldy, int out_f32, int epi, const void* aux, int64_t ldaux, const void* vec,
                         hipStream_t stream);
 
+/* Normalizations of the stand-in Krea-2 block around its quantized linears.  No counterpart in
+ * the reference: its blocks run in diffusers (reference src/krea2_svdquant/transformer.py:46-59),
+ * whose internals it does not contain.  bf16 in and out, float32 math, one pass over the rows.
+ *
+ * Adaptive RMS norm, per row of H (H % 8 == 0; x, w, shift, y 16-byte aligned, ldx, ldy
+ * multiples of 8, y may not overlap x):
+ *   y = bf16(bf16(x * rsqrt(mean(x^2) + eps) * w) + shift)     w = 1 + scale, shift: bf16 [H] */
+int svdq_rms_norm_modulate(const void* x, int64_t ldx, const void* w, const void* shift, int T, int H, float eps,
+                           void* y, int64_t ldy, hipStream_t stream);
+
+/* Per-head RMS norm and rotate-half rotary embedding of t, contiguous bf16 [T, heads, 128] (q or
+ * k), into out (same layout, may not overlap t).  cos / sin: bf16 [T, ldcs] position tables, of
+ * which columns 0..63 are read (the rotate-half tables repeat their first half).  Per head:
+ *   n = bf16(t * rsqrt(mean(t^2) + eps));  for j < 64, (n1, n2) = (n[j], n[j + 64]):
+ *   out[j] = bf16(fma(-n2, sin, bf16(n1 * cos))),  out[j + 64] = bf16(fma(n1, sin, bf16(n2 * cos))) */
+int svdq_head_rms_rope(const void* t, int T, int heads, const void* cos, const void* sin, int64_t ldcs, float eps,
+                       void* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -372,6 +372,35 @@ int svdq_w4a4_gemm_epi(const void* qa, int operand, const void* sxp, const void*
   return launched(svdq::launch_w4a4(p, group, operand, out_f32 == 1, stream), "w4a4_gemm");
 }
 
+int svdq_rms_norm_modulate(const void* x, int64_t ldx, const void* w, const void* shift, int T, int H, float eps,
+                           void* y, int64_t ldy, hipStream_t stream) {
+  if (!x || !w || !shift || !y) return fail(SVDQ_ERR_ARG, "rms_norm_modulate: null pointer");
+  if (T <= 0 || H <= 0 || H % 8) return fail(SVDQ_ERR_SHAPE, "rms_norm_modulate: T=%d, H=%d (H %% 8 == 0)", T, H);
+  if (!(eps >= 0.0f)) return fail(SVDQ_ERR_ARG, "rms_norm_modulate: eps must be >= 0");
+  if (ldx < H || ldy < H || ldx % 8 || ldy % 8 || !aligned16(x) || !aligned16(w) || !aligned16(shift) ||
+      !aligned16(y))
+    return fail(SVDQ_ERR_ALIGN, "rms_norm_modulate: 16-byte aligned pointers, ldx, ldy >= H and multiples of 8");
+  return launched(svdq::launch_rms_norm_modulate(static_cast<const uint16_t*>(x), ldx, static_cast<const uint16_t*>(w),
+                                                 static_cast<const uint16_t*>(shift), T, H, eps,
+                                                 static_cast<uint16_t*>(y), ldy, stream),
+                  "rms_norm_modulate");
+}
+
+int svdq_head_rms_rope(const void* t, int T, int heads, const void* cos, const void* sin, int64_t ldcs, float eps,
+                       void* out, hipStream_t stream) {
+  if (!t || !cos || !sin || !out) return fail(SVDQ_ERR_ARG, "head_rms_rope: null pointer");
+  if (T <= 0 || heads <= 0 || ldcs < 64) return fail(SVDQ_ERR_SHAPE, "head_rms_rope: T=%d heads=%d ldcs=%lld",
+                                                     T, heads, (long long)ldcs);
+  if (!(eps >= 0.0f)) return fail(SVDQ_ERR_ARG, "head_rms_rope: eps must be >= 0");
+  if (reinterpret_cast<uintptr_t>(t) % 2 || reinterpret_cast<uintptr_t>(out) % 2 ||
+      reinterpret_cast<uintptr_t>(cos) % 2 || reinterpret_cast<uintptr_t>(sin) % 2)
+    return fail(SVDQ_ERR_ALIGN, "head_rms_rope: bf16 pointers must be 2-byte aligned");
+  return launched(svdq::launch_head_rms_rope(static_cast<const uint16_t*>(t), T, heads,
+                                             static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
+                                             ldcs, eps, static_cast<uint16_t*>(out), stream),
+                  "head_rms_rope");
+}
+
 int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const void* mid,
                     const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group, void* y,
                     int64_t ldy, int out_f32, hipStream_t stream) {

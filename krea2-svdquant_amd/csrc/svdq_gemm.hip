@@ -42,7 +42,8 @@ __device__ __forceinline__ float div_bf16_fast(float a, float d, bool& exact) {
   const float f = a * __builtin_amdgcn_rcpf(d);
   const uint32_t lo = __float_as_uint(f) & 0xFFFFu;
   // bitwise & / |: the conditions evaluate branch-free
-  exact = (d < 0x1p100f) & (fabsf(a) < 0x1p100f) & ((fabsf(f) >= 0x1p-100f) | (a == 0.0f)) & (lo - 0x7FF8u > 16u);
+  exact = (int)(d < 0x1p100f) & (int)(fabsf(a) < 0x1p100f) & ((int)(fabsf(f) >= 0x1p-100f) | (int)(a == 0.0f)) &
+          (int)(lo - 0x7FF8u > 16u);
   return f;
 }
 

@@ -75,5 +75,11 @@ hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, 
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st);
 // W4A4 GEMM for any group size G (multiple of 16 dividing K): int8 operands (SVDQ_OPERAND_I8 layout)
 hipError_t launch_w4a4_any_group(const GemmParams& p, int G, bool out_f32, hipStream_t st);
+// Stand-in block normalizations (svdq_block.hip): adaptive RMS norm of rows [T, H] (H % 8 == 0),
+// per-head RMS norm + rotary embedding of contiguous [T, heads, 128]
+hipError_t launch_rms_norm_modulate(const uint16_t* x, long ldx, const uint16_t* w, const uint16_t* shift, int T,
+                                    int H, float eps, uint16_t* y, long ldy, hipStream_t st);
+hipError_t launch_head_rms_rope(const uint16_t* t, int T, int heads, const uint16_t* cs, const uint16_t* sn,
+                                long ldcs, float eps, uint16_t* out, hipStream_t st);
 
 }  // namespace svdq

@@ -329,3 +329,55 @@ def w4a16_gemm(xhat: Tensor, qweight: Tensor, weight_scales: Tensor, mid: Tensor
 @w4a16_gemm.register_fake
 def _(xhat, qweight, weight_scales, mid, l1cat, bias, group_size, out_f32, epi=0, aux=None, vec=None):
     return xhat.new_empty((xhat.shape[0], qweight.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)
+
+
+# ---- stand-in block normalizations -------------------------------------------------------------
+@torch.library.custom_op("svdq::rms_norm_modulate", mutates_args=())
+def rms_norm_modulate(x: Tensor, weight: Tensor, shift: Tensor, eps: float) -> Tensor:
+    """``bf16(bf16(x * rsqrt(mean(x^2) + eps) * weight) + shift)`` over the last dimension of a
+    bf16 ``x`` [..., H] (H % 8 == 0): the stand-in block's adaptive RMS norm (weight = 1 + scale)."""
+    _need(x.is_cuda, RuntimeError, "svdq::rms_norm_modulate needs GPU tensors")
+    dev = x.device
+    h = x.shape[-1]
+    for name, t in (("weight", weight), ("shift", shift)):
+        _check_dev(name, t, dev, torch.bfloat16)
+        _need(t.numel() == h, ValueError, f"{name} must have {h} elements, got {t.numel()}")
+    _need(x.dtype == torch.bfloat16, TypeError, f"x must be bf16, got {x.dtype}")
+    x2 = x.reshape(-1, h)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    y = torch.empty((x2.shape[0], h), dtype=torch.bfloat16, device=dev)
+    lib.call("svdq_rms_norm_modulate", _vp(x2), x2.stride(0), _vp(weight), _vp(shift),
+             x2.shape[0], h, ctypes.c_float(eps), _vp(y), h, _stream(dev))
+    return y.view(x.shape)
+
+
+@rms_norm_modulate.register_fake
+def _(x, weight, shift, eps):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("svdq::head_rms_rope", mutates_args=())
+def head_rms_rope(t: Tensor, cos: Tensor, sin: Tensor, eps: float) -> Tensor:
+    """Per-head RMS norm of ``t`` [T, heads, 128] (bf16) followed by the rotate-half rotary
+    embedding with the position tables ``cos`` / ``sin`` [T, >= 64] (bf16; columns 0..63 read)."""
+    _need(t.is_cuda, RuntimeError, "svdq::head_rms_rope needs GPU tensors")
+    dev = t.device
+    _need(t.dim() == 3 and t.shape[-1] == 128, ValueError, f"t must be [T, heads, 128], got {tuple(t.shape)}")
+    _need(t.dtype == torch.bfloat16, TypeError, f"t must be bf16, got {t.dtype}")
+    tok, heads = t.shape[0], t.shape[1]
+    for name, tab in (("cos", cos), ("sin", sin)):
+        _check_dev(name, tab, dev, torch.bfloat16)
+        _need(tab.dim() == 2 and tab.shape[0] == tok and tab.shape[1] >= 64 and tab.stride(-1) == 1, ValueError,
+              f"{name} must be [{tok}, >= 64] with unit column stride, got {tuple(tab.shape)}")
+    _need(cos.stride(0) == sin.stride(0), ValueError, "cos and sin must share a row stride")
+    t = t.contiguous()
+    out = torch.empty_like(t)
+    lib.call("svdq_head_rms_rope", _vp(t), tok, heads, _vp(cos), _vp(sin), cos.stride(0), ctypes.c_float(eps),
+             _vp(out), _stream(dev))
+    return out
+
+
+@head_rms_rope.register_fake
+def _(t, cos, sin, eps):
+    return torch.empty_like(t)

@@ -21,8 +21,10 @@ the concatenated text and latent tokens, modulation vectors fixed per block):
 (the modulation's ``1 + scale`` runs as the norm's weight, the gated residuals as ``addcmul``
 and the rotary embedding half by half: one bf16 rounding per fused op, fewer passes over x).
 A denoise step is the 28 blocks over [text | latent] tokens followed by the Euler update of the
-latent tokens, ``latent += dt * velocity``.  Attention, norms and elementwise work run in
-PyTorch-ROCm; every quantized linear runs on the gfx950 kernels (``SVDQuantLinear``).  With
+latent tokens, ``latent += dt * velocity``.  On the GPU every quantized linear runs on the gfx950
+kernels (``SVDQuantLinear``), and so do the adaptive RMS norms and the per-head norm + rotary
+embedding (``svdq::rms_norm_modulate``, ``svdq::head_rms_rope``: one pass each); attention and
+the remaining elementwise work run in PyTorch-ROCm (on the CPU everything is torch).  With
 ``fused=True`` the sigmoid gate, the SwiGLU product and the two gated residual adds run inside
 the stores of to_gate, ff.up, to_out.0 and ff.down instead.
 """
@@ -37,6 +39,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
+from ..kernels.hip import ops as hip_ops
 from ..quant.state import SVDQuantLinearState
 from .linear import SVDQuantLinear
 from .siblings import run_concurrent
@@ -93,6 +96,23 @@ def rms_norm(x: Tensor, eps: float = 1e-6, weight: Optional[Tensor] = None) -> T
     """RMS norm over the last dimension, in x's dtype with an fp32 reduction; ``weight`` (the
     modulation's ``1 + scale``) is applied inside the same kernel."""
     return F.rms_norm(x, (x.shape[-1],), weight=weight, eps=eps)
+
+
+def norm_modulate(x: Tensor, scale: Tensor, shift: Tensor, eps: float = 1e-6) -> Tensor:
+    """The block's adaptive RMS norm ``rms_norm(x) * (1 + scale) + shift``: one gfx950 kernel on
+    the GPU (``svdq::rms_norm_modulate``), the torch ops elsewhere."""
+    w = 1 + scale
+    if x.is_cuda:
+        return hip_ops.rms_norm_modulate(x, w, shift, eps)
+    return rms_norm(x, eps, weight=w) + shift
+
+
+def head_norm_rope(t: Tensor, cos: Tensor, sin: Tensor, eps: float = 1e-6) -> Tensor:
+    """Per-head RMS norm of q or k [T, heads, head_dim] and the rotary embedding: one gfx950
+    kernel on the GPU for head_dim 128 (``svdq::head_rms_rope``), the torch ops elsewhere."""
+    if t.is_cuda:
+        return hip_ops.head_rms_rope(t, cos, sin, eps)
+    return apply_rope(rms_norm(t, eps), cos, sin)
 
 
 def rope_tables(tokens: int, head_dim: int, device, dtype, theta: float = 10000.0) -> tuple[Tensor, Tensor]:
@@ -182,16 +202,16 @@ class Krea2StandInBlock(nn.Module):
             fns = [partial(linear, n, lin[n]) for n in names]
             return run_concurrent(z, fns) if siblings else [f(z) for f in fns]
 
-        h = rms_norm(x, weight=1 + scale_a) + shift_a
+        h = norm_modulate(x, scale_a, shift_a)
         q, g, k, v = siblings_of(h, "attn.to_q", "attn.to_gate", "attn.to_k", "attn.to_v")
         q, k, v = (z.view(t, -1, d.head_dim) for z in (q, k, v))
-        q = apply_rope(rms_norm(q), cos, sin)
-        k = apply_rope(rms_norm(k), cos, sin)
+        q = head_norm_rope(q, cos, sin)
+        k = head_norm_rope(k, cos, sin)
         a = attention(q, k, v)                                   # [T, heads * head_dim]
         a = a * torch.sigmoid(g)
         x = torch.addcmul(x, gate_a, linear("attn.to_out.0", lin["attn.to_out.0"], a))
 
-        h = rms_norm(x, weight=1 + scale_f) + shift_f
+        h = norm_modulate(x, scale_f, shift_f)
         u, g = siblings_of(h, "ff.up", "ff.gate")
         f = F.silu(g) * u
         return torch.addcmul(x, gate_f, linear("ff.down", lin["ff.down"], f))
@@ -204,16 +224,16 @@ class Krea2StandInBlock(nn.Module):
         d = self.dims
         shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mods
         t = x.shape[0]
-        h = rms_norm(x, weight=1 + scale_a) + shift_a
+        h = norm_modulate(x, scale_a, shift_a)
         fns = [lin["attn.to_q"], lin["attn.to_k"], lin["attn.to_v"]]
         q, k, v = run_concurrent(h, fns) if siblings else [f(h) for f in fns]
         q, k, v = (z.view(t, -1, d.head_dim) for z in (q, k, v))
-        q = apply_rope(rms_norm(q), cos, sin)
-        k = apply_rope(rms_norm(k), cos, sin)
+        q = head_norm_rope(q, cos, sin)
+        k = head_norm_rope(k, cos, sin)
         a = attention(q, k, v)
         a = lin["attn.to_gate"].forward_epilogue(h, "mul_sigmoid", aux=a)
         x = lin["attn.to_out.0"].forward_epilogue(a, "residual_gate", aux=x, vec=gate_a)
-        h = rms_norm(x, weight=1 + scale_f) + shift_f
+        h = norm_modulate(x, scale_f, shift_f)
         g = lin["ff.gate"](h)
         f = lin["ff.up"].forward_epilogue(h, "silu_mul", aux=g)
         return lin["ff.down"].forward_epilogue(f, "residual_gate", aux=x, vec=gate_f)
