@@ -100,6 +100,33 @@ def time_reps(fn, iters: int, reps: int = 3) -> list[float]:
     return out
 
 
+def time_graph(fn, calls: int = 20, reps: int = 5):
+    """Device ms per call of ``fn``: ``calls`` calls captured in one HIP graph, replayed ``reps``
+    times with HIP events around each replay (no host dispatch between the kernels, which a
+    short kernel sequence launched from Python would otherwise wait for).  Returns the median,
+    the per-replay values and the outputs of the graph's last call."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [fn() for _ in range(calls)]
+    graph.replay()
+    torch.cuda.synchronize()
+    vals = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        vals.append(a.elapsed_time(b) / calls)
+    return statistics.median(vals), vals, outs[-1], graph
+
+
 def time_avg(fn, iters: int, reps: int = 3) -> float:
     """Median over ``reps`` of ``time_reps``."""
     return statistics.median(time_reps(fn, iters, reps))
@@ -409,16 +436,17 @@ def main() -> int:
     def act():
         return ops.act_quant(x, prep.srs, prep.l2, None, None, g, prep.rtp, opc, False, False, False, True)
 
-    # Per-kernel launch durations first, each kernel back to back on the stream it runs on (5
-    # repetitions of max(steps, 20) launches).  Running them before the timed steps also brings
-    # the GPU from idle to its sustained clock, which takes tens of milliseconds of work.
-    for _ in range(3):
-        act(), gemm()
-    it = max(args.steps, 20)
-    act_reps = time_reps(act, it, 5)
-    gemm_reps = time_reps(gemm, it, 5)
-    ms_act, ms_gemm = statistics.median(act_reps), statistics.median(gemm_reps)
-    log(f"act {ms_act:.4f} ms, gemm {ms_gemm:.4f} ms (medians of 5 x {it})")
+    # The GPU ramps from idle to its sustained clock over tens of milliseconds of work: run steps
+    # for at least 150 ms first, so that the warmup and the timed steps see the sustained clock.
+    torch.cuda.synchronize()
+    t_settle = time.perf_counter()
+    settle = 0
+    while time.perf_counter() - t_settle < 0.15 or settle < 20:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        settle += 10
+    log(f"clock settle: {settle} steps")
 
     log(f"warmup {args.warmup}")
     for _ in range(args.warmup):
@@ -436,6 +464,33 @@ def main() -> int:
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
     ms = a.elapsed_time(b) / args.steps
     log(f"{ms:.4f} ms/step (HIP events; host wall {wall:.4f} ms/step)")
+
+    # Right after the timed steps (same clock): 20 more steps, each split by HIP events between
+    # its activation pass and its GEMM (the host runs ahead of the GPU, so each interval is the
+    # device time of its kernels).  The GEMM's launch duration for the roofline comes from here.
+    def split_steps(count):
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(count)]
+        for e in evs:
+            e[0].record()
+            qa_s, sx_s, _, _, mid_s = act()
+            e[1].record()
+            ops.w4a4_gemm(qa_s, sx_s, wop, wsp, mid_s, prep.l1cat, None, g, opc, False)
+            e[2].record()
+        torch.cuda.synchronize()
+        return [e[0].elapsed_time(e[1]) for e in evs], [e[1].elapsed_time(e[2]) for e in evs]
+    act_in_step, gemm_reps = split_steps(20)
+    ms_act_step, ms_gemm = statistics.median(act_in_step), statistics.median(gemm_reps)
+    # The activation pass alone: from Python back to back it is bounded by the host dispatch of the
+    # op, so its device time comes from a HIP graph of 20 calls, whose last outputs are checked
+    # bit for bit against an eager call.
+    ms_act, act_reps, g_out, act_graph = time_graph(act, 20, 5)
+    e_out = act()
+    torch.cuda.synchronize()
+    act_graph_exact = all(torch.equal(u, v) for u, v in zip(g_out[:2], e_out[:2])) and torch.equal(g_out[4][0], e_out[4][0])
+    del act_graph, g_out, e_out
+    ms_gemm_b2b = time_avg(gemm, max(args.steps, 20), 3)
+    log(f"in the steps: act {ms_act_step:.4f} ms, gemm {ms_gemm:.4f} ms; act alone (graph) {ms_act:.4f} ms; "
+        f"gemm back to back {ms_gemm_b2b:.4f} ms")
 
     flops = 2.0 * m * n * k
     splits = mid.shape[0] - 1
@@ -464,8 +519,13 @@ def main() -> int:
                    "M": m, "K": k, "N": n, "rank": r, "group": g, "operand": args.operand},
         "kernels": {"act_quant_ms": round(ms_act, 4), "w4a4_gemm_ms": round(ms_gemm, 4),
                     "act_quant_ms_min_max": [round(min(act_reps), 4), round(max(act_reps), 4)],
+                    "act_quant_timing": "HIP graph of 20 calls (device time of the two kernels); outputs "
+                                        f"bit-equal to an eager call: {act_graph_exact}",
+                    "act_quant_ms_in_step": round(ms_act_step, 4),
                     "w4a4_gemm_ms_min_max": [round(min(gemm_reps), 4), round(max(gemm_reps), 4)],
-                    "step_minus_kernels_us": round((ms - ms_act - ms_gemm) * 1e3, 1),
+                    "w4a4_gemm_timing": "HIP events between the kernels of 20 steps right after the timed steps",
+                    "w4a4_gemm_ms_back_to_back": round(ms_gemm_b2b, 4),
+                    "step_minus_kernels_us": round((ms - ms_act_step - ms_gemm) * 1e3, 1),
                     "act_quant_GBps": round(act_bytes / (ms_act * 1e-3) / 1e9, 1),
                     "act_quant_hbm_frac": round(act_bytes / (ms_act * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     "step_host_wall_ms": round(wall, 4)},
