@@ -106,6 +106,49 @@ __global__ void __launch_bounds__(256) head_rms_rope_kernel(const uint16_t* __re
   orow[j + 64] = (uint16_t)(pk >> 16);
 }
 
+// The same with 16-byte accesses: 8 lanes per row (32 rows per workgroup), lane j holding
+// channels 8 j .. 8 j + 7 and their rotary partners 64 + 8 j ..; the mean of squares reduces over
+// the 8 lanes.  Needs t, out, cos, sin 16-byte aligned and ldcs % 8 == 0.
+__global__ void __launch_bounds__(256) head_rms_rope_vec_kernel(const uint16_t* __restrict__ t, long rows,
+                                                                int heads, const uint16_t* __restrict__ cs,
+                                                                const uint16_t* __restrict__ sn, long ldcs,
+                                                                float eps, uint16_t* __restrict__ out) {
+  const long row = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
+  if (row >= rows) return;   // a row's 8 lanes leave together: the shuffles stay within live lanes
+  const int j = threadIdx.x & 7;
+  const long tok = row / heads;
+  const u32x4 a = ld16(t + row * 128 + 8 * j), b = ld16(t + row * 128 + 64 + 8 * j);
+  float ss = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    ss = __builtin_fmaf(bf16lo(a[d]), bf16lo(a[d]), ss);
+    ss = __builtin_fmaf(bf16hi(a[d]), bf16hi(a[d]), ss);
+    ss = __builtin_fmaf(bf16lo(b[d]), bf16lo(b[d]), ss);
+    ss = __builtin_fmaf(bf16hi(b[d]), bf16hi(b[d]), ss);
+  }
+#pragma unroll
+  for (int off = 4; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  const float r = rsqrtf(ss / 128.0f + eps);
+  const u32x4 c = ld16(cs + tok * ldcs + 8 * j), sv = ld16(sn + tok * ldcs + 8 * j);
+  u32x4 o1, o2;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    float p1[2], p2[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float x1 = e ? bf16hi(a[d]) : bf16lo(a[d]), x2 = e ? bf16hi(b[d]) : bf16lo(b[d]);
+      const float cc = e ? bf16hi(c[d]) : bf16lo(c[d]), ssn = e ? bf16hi(sv[d]) : bf16lo(sv[d]);
+      const float n1 = round_bf16(x1 * r), n2 = round_bf16(x2 * r);
+      p1[e] = __builtin_fmaf(-n2, ssn, round_bf16(n1 * cc));
+      p2[e] = __builtin_fmaf(n1, ssn, round_bf16(n2 * cc));
+    }
+    o1[d] = pack_bf16x2(p1[0], p1[1]);
+    o2[d] = pack_bf16x2(p2[0], p2[1]);
+  }
+  *reinterpret_cast<u32x4*>(out + row * 128 + 8 * j) = o1;
+  *reinterpret_cast<u32x4*>(out + row * 128 + 64 + 8 * j) = o2;
+}
+
 }  // namespace
 
 hipError_t launch_rms_norm_modulate(const uint16_t* x, long ldx, const uint16_t* w, const uint16_t* shift, int T,
@@ -118,7 +161,12 @@ hipError_t launch_rms_norm_modulate(const uint16_t* x, long ldx, const uint16_t*
 hipError_t launch_head_rms_rope(const uint16_t* t, int T, int heads, const uint16_t* cs, const uint16_t* sn,
                                 long ldcs, float eps, uint16_t* out, hipStream_t st) {
   const long rows = (long)T * heads;
-  head_rms_rope_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(t, rows, heads, cs, sn, ldcs, eps, out);
+  const bool vec = ((reinterpret_cast<uintptr_t>(t) | reinterpret_cast<uintptr_t>(out) |
+                     reinterpret_cast<uintptr_t>(cs) | reinterpret_cast<uintptr_t>(sn)) & 15) == 0 && ldcs % 8 == 0;
+  if (vec)
+    head_rms_rope_vec_kernel<<<(unsigned)((rows + 31) / 32), 256, 0, st>>>(t, rows, heads, cs, sn, ldcs, eps, out);
+  else
+    head_rms_rope_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(t, rows, heads, cs, sn, ldcs, eps, out);
   return hipGetLastError();
 }
 

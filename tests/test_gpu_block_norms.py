@@ -50,12 +50,17 @@ def test_rms_norm_modulate_matches_torch(dev, t, h, ld):
     _check(got, ref, norm, f"rms_norm_modulate T={t} H={h}")
 
 
-@pytest.mark.parametrize("t,heads", [(4352, 48), (4352, 12), (77, 3), (1, 1)])
-def test_head_rms_rope_matches_torch(dev, t, heads):
+@pytest.mark.parametrize("t,heads,aligned", [(4352, 48, True), (4352, 12, True), (77, 3, True), (1, 1, True),
+                                             (77, 3, False)])
+def test_head_rms_rope_matches_torch(dev, t, heads, aligned):
+    """16-byte kernel for aligned rows (the stand-in's case); the element-wise kernel for a view at
+    an odd element offset."""
     from krea2_svdquant_amd.kernels.hip import ops
     from krea2_svdquant_amd.runtime.krea2_standin import apply_rope, rms_norm, rope_tables
     gen = torch.Generator(device=dev).manual_seed(t * heads)
-    q = (torch.randn(t, heads * 128, device=dev, generator=gen) * 2).to(torch.bfloat16).view(t, heads, 128)
+    src = (torch.randn(t * heads * 128 + 1, device=dev, generator=gen) * 2).to(torch.bfloat16)
+    q = (src[:-1] if aligned else src[1:]).view(t, heads, 128)
+    assert (q.data_ptr() % 16 == 0) == aligned
     cos, sin = rope_tables(t, 128, dev, torch.bfloat16)
     got = ops.head_rms_rope(q, cos, sin, 1e-6)
     norm = rms_norm(q, 1e-6)
