@@ -18,6 +18,7 @@ Nothing falls back to another implementation.
 """
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
@@ -227,11 +228,35 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
     return y.reshape(*lead, prep.n)
 
 
+# Prepared operands of the stateless entry, per state object: id(state) -> (key, PreparedLayer).  An
+# entry is dropped when its state is garbage-collected and replaced when any buffer of the state
+# or of an adapter is swapped or edited in place (storage and version counter in the key) or an
+# adapter's multiplier changes.
+_SEAM_CACHE: dict[int, tuple[tuple, PreparedLayer]] = {}
+
+
+def _seam_key(state: SVDQuantLinearState, adapters: Sequence, device: torch.device) -> tuple:
+    bufs = (state.qweight, state.smooth_scale, state.weight_scales, state.l1, state.l2, state.bias)
+    return ((str(device), state.group_size)
+            + tuple((b.data_ptr(), b._version) if b is not None else None for b in bufs)
+            + tuple((id(a), a.multiplier, a.down_weight.data_ptr(), a.down_weight._version,
+                     a.up_weight.data_ptr(), a.up_weight._version) for a in adapters))
+
+
 def svdquant_linear_hip_gfx950(x: Tensor, state: SVDQuantLinearState, *, adapters: Sequence = (),
                                mode: str = "w4a4", out_f32: bool = False, operand: str = "e3m2") -> Tensor:
-    """Stateless backend entry (prepares the layer on every call; modules cache it)."""
-    return forward_prepared(x, prepare_layer(state, adapters, x.device), mode=mode, out_f32=out_f32,
-                            operand=operand)
+    """Stateless backend entry, the reference's backend-function seam
+    (``kernels/triton/generic_int4.py:227``: ``fn(x, state)``).  The layer's kernel operands
+    (including the expanded weight operand) are prepared on the first call for a state and kept
+    while the state lives and its buffers are unchanged."""
+    key = _seam_key(state, adapters, x.device)
+    hit = _SEAM_CACHE.get(id(state))
+    if hit is None or hit[0] != key:
+        if hit is None:
+            weakref.finalize(state, _SEAM_CACHE.pop, id(state), None)
+        hit = (key, prepare_layer(state, adapters, x.device))
+        _SEAM_CACHE[id(state)] = hit
+    return forward_prepared(x, hit[1], mode=mode, out_f32=out_f32, operand=operand)
 
 
 def svdquant_linear_hip_gfx950_w4a16(x: Tensor, state: SVDQuantLinearState, *, adapters: Sequence = (),

@@ -31,6 +31,23 @@ def test_module_forward_with_lora_matches_oracle(dev):
     assert torch.equal(yb, y0.reshape(96, 384))
 
 
+def test_backend_function_matches_module_and_reuses_operands(dev):
+    """The stateless backend function (reference seam ``fn(x, state)``) gives the module's output
+    bit for bit and prepares the state once."""
+    from krea2_svdquant_amd.kernels.hip import backend
+    from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
+    x = synth.make_activation(80, 512, seed=35)
+    st = synth.make_layer(192, 512, x, rank=32, group_size=64, seed=36, bias=True)
+    ds = to_device_state(st, dev)
+    xd = bf16_tensor(x, dev)
+    y_mod = SVDQuantLinear(ds, backend="hip_gfx950")(xd)
+    y1 = backend.svdquant_linear_hip_gfx950(xd, ds)
+    prep = backend._SEAM_CACHE[id(ds)][1]
+    y2 = backend.svdquant_linear_hip_gfx950(xd, ds)
+    assert backend._SEAM_CACHE[id(ds)][1] is prep and prep.operands
+    assert torch.equal(y1, y_mod) and torch.equal(y2, y_mod)
+
+
 def test_w4a16_module_matches_sim_math(dev):
     from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
     x = synth.make_activation(64, 512, seed=41)

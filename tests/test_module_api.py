@@ -118,3 +118,36 @@ def test_epilogue_operand_validation_on_the_host():
         backend._epilogue_operands("mul_sigmoid", aux, torch.zeros(8, dtype=torch.bfloat16), 4, 8, cpu)
     epi, a2, v2 = backend._epilogue_operands("residual_gate", aux.view(2, 2, 8), torch.ones(8), 4, 8, cpu)
     assert epi == 3 and tuple(a2.shape) == (4, 8) and v2.dtype == torch.bfloat16
+
+
+def test_backend_function_caches_prepared_operands_per_state(monkeypatch):
+    """The stateless backend function (the reference's ``fn(x, state)`` seam) prepares a state's
+    kernel operands once and reuses them; an in-place edit of a buffer, a swapped buffer, a changed
+    adapter multiplier or a new adapter set prepares again; the entry goes with its state."""
+    import gc
+    import types
+    from krea2_svdquant_amd.kernels.hip import backend
+    prepared = []
+    monkeypatch.setattr(backend, "prepare_layer", lambda state, adapters, device: prepared.append(len(adapters)) or
+                        object())
+    monkeypatch.setattr(backend, "forward_prepared", lambda x, prep, **kw: prep)
+    st = _state(n=8, k=64)
+    x = torch.zeros(2, 64)
+    a = backend.svdquant_linear_hip_gfx950(x, st)
+    assert backend.svdquant_linear_hip_gfx950(x, st) is a and len(prepared) == 1
+    st.l1.add_(1.0)                                      # in-place edit: version counter moves
+    b = backend.svdquant_linear_hip_gfx950(x, st)
+    assert b is not a and len(prepared) == 2
+    st.bias = torch.zeros(8, dtype=torch.bfloat16)       # a new buffer
+    backend.svdquant_linear_hip_gfx950(x, st)
+    assert len(prepared) == 3
+    ad = types.SimpleNamespace(down_weight=torch.zeros(4, 64), up_weight=torch.zeros(8, 4), multiplier=0.5)
+    c = backend.svdquant_linear_hip_gfx950(x, st, adapters=[ad])
+    assert backend.svdquant_linear_hip_gfx950(x, st, adapters=[ad]) is c and prepared[-1] == 1
+    ad.multiplier = 0.25
+    assert backend.svdquant_linear_hip_gfx950(x, st, adapters=[ad]) is not c
+    key = id(st)
+    assert key in backend._SEAM_CACHE
+    del st
+    gc.collect()
+    assert key not in backend._SEAM_CACHE
