@@ -1354,18 +1354,31 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
     const int buf = st & 1;
     gload(min(st + D, nst - 1), q_c);   // set q was moved to LDS during the previous stage
     wait_set(QN{});                      // set q + 1 landed; the D - 1 newer sets may be in flight
+    // fragments of k-step ks + 1 are read while the MFMAs of k-step ks run (two register sets)
+    u32x4 a[2][RI], b[2][4];
+    auto read_frags = [&](int ks, u32x4 (&fa)[RI], u32x4 (&fb)[4]) {
+#pragma unroll
+      for (int i = 0; i < RI; ++i) fa[i] = *reinterpret_cast<const u32x4*>(&sA[buf][ra0 + 32 * i * PITCH + 32 * ks]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fb[j] = *reinterpret_cast<const u32x4*>(&sB[buf][rb0 + 32 * j * PITCH + 32 * ks]);
+    };
+    read_frags(0, a[0], b[0]);
 #pragma unroll
     for (int ks = 0; ks < KB / 16; ++ks) {
-      u32x4 a[RI], b[4];
-#pragma unroll
-      for (int i = 0; i < RI; ++i) a[i] = *reinterpret_cast<const u32x4*>(&sA[buf][ra0 + 32 * i * PITCH + 32 * ks]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4*>(&sB[buf][rb0 + 32 * j * PITCH + 32 * ks]);
+      const int c = ks & 1;
+      if (ks + 1 < KB / 16) read_frags(ks + 1, a[c ^ 1], b[c ^ 1]);
 #pragma unroll
       for (int i = 0; i < RI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16_32x32x16(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16_32x32x16(a[c][i], b[c][j], acc[i][j]);
       lstore_part(buf ^ 1, QN{}, ks);
+    }
+    // issue order: k-step 0's reads, then per k-step the next one's reads ahead of its MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, RI + 4, 0);
+#pragma unroll
+    for (int ks = 0; ks < KB / 16; ++ks) {
+      if (ks + 1 < KB / 16) __builtin_amdgcn_sched_group_barrier(0x100, RI + 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, RI * 4, 0);
     }
     __syncthreads();
   };
