@@ -29,6 +29,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import re
 import statistics
@@ -43,6 +44,7 @@ METRIC = "W4A4 SVDQuantLinear eff. TOPS @M4096 K6144 N16384; ms/denoise step @10
 MFMA_PEAK_TFLOPS = {"e3m2": 10100.0, "e4m3": 5000.0, "i8": 5000.0}   # MI355X dense MFMA peaks
 INT8_PEAK_TOPS = 5000.0
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
 MFMA_NAME = {"e3m2": "FP6", "e4m3": "FP8", "i8": "INT8"}
 KERNEL_NAME = {"e3m2": "w4a4_e3m2_kernel<64,false> (FP6 MFMA on exact INT4 codes)",
                "e4m3": "w4a4_kernel<64,0,false> (FP8 MFMA on exact INT4 codes)",
@@ -69,8 +71,8 @@ def parse():
     ap.add_argument("--cpu-reps", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-block", action="store_true", help="skip the config 1-4 extra lines")
-    ap.add_argument("--lines", default="block,w4a16,lora,denoise",
-                    help="extra lines to run (comma list of block, w4a16, lora, denoise)")
+    ap.add_argument("--lines", default="block,w4a16,lora,denoise,attention",
+                    help="extra lines to run (comma list of block, w4a16, lora, denoise, attention)")
     ap.add_argument("--pmc-pass", nargs="?", const="w4a4", default=None, choices=["w4a4", "w4a16"],
                     help="counter pass for rocprofv3: one copy kernel of known size, then 3 launches of the "
                          "config 1 ff.up W4A4 GEMM and 3 activation passes (w4a4), or of the config 2 ff.up "
@@ -274,7 +276,7 @@ def w4a16_line(args, dev) -> dict:
     total = b["total"]
     tflops = b["ops"] / (total * 1e-3) / 1e12
     return {"ms_per_layer": b["per"], "ms_per_block_linears": round(total, 4), "TFLOPs": round(tflops, 1),
-            "bf16_peak_frac": round(tflops / 2500.0, 4),
+            "bf16_peak_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
             "ms_per_block_in_order": round(b["seq"], 4),
             "ms_per_block_in_order_concurrent_siblings": round(b["conc"], 4),
             "note": "W4A16 (bf16 x_hat x in-register dequantized INT4 weights, bf16 MFMA), M=2304, layer = "
@@ -337,6 +339,14 @@ def denoise_line(args, dev) -> dict:
     ms_fused_sib, _ = run(True, True)
     ms, lat = run(False)
     same_sib = bool(torch.equal(lat, lat_sib))
+    # the same steps with the attention on PyTorch's fused SDPA kernels, for comparison
+    from krea2_svdquant_amd.runtime import krea2_standin as ks
+    ks.ATTENTION = "sdpa"
+    try:
+        model.denoise_step(text, latent, dt)
+        ms_sdpa, _ = run(False)
+    finally:
+        ks.ATTENTION = "hip"
     # one more step with HIP events around every quantized linear: their share of the step
     pairs = []
 
@@ -359,18 +369,57 @@ def denoise_line(args, dev) -> dict:
             "ms_per_denoise_step_fused_epilogues": round(ms_fused, 3),
             "ms_per_denoise_step_concurrent_siblings": round(ms_sib, 3),
             "ms_per_denoise_step_fused_epilogues_concurrent_siblings": round(ms_fused_sib, 3),
+            "ms_per_denoise_step_sdpa_attention": round(ms_sdpa, 3),
             "concurrent_siblings_bit_identical": same_sib,
             "linears_ms_per_step": round(lin_ms, 3), "rest_ms_per_step": round(ms - lin_ms, 3),
             "tokens": 4352, "blocks": dims.layers, "peak_hbm_GB": round(hbm_gb, 1), "finite": finite,
             "note": "stand-in Krea-2 denoiser (diffusers is absent): 28 blocks, 8 W4A4 linears each on this "
-                    "backend; attention (SDPA, 48 q / 12 kv heads), RMS norms, rotary embedding, gates and "
-                    "residuals in PyTorch-ROCm (ms_per_denoise_step; with the sigmoid gate, SwiGLU product and "
+                    "backend; attention (48 q / 12 kv heads, svdq::attention), adaptive RMS norms, per-head "
+                    "norm + rotary embedding on gfx950 kernels, gates and residuals in PyTorch-ROCm "
+                    "(ms_per_denoise_step; ms_per_denoise_step_sdpa_attention: the attention on PyTorch's "
+                    "fused SDPA kernels instead; with the sigmoid gate, SwiGLU product and "
                     "gated residuals fused into the stores of to_gate, ff.up, to_out.0 and ff.down instead: "
                     "ms_per_denoise_step_fused_epilogues; *_concurrent_siblings: the linears that read the same "
                     "input (to_q, to_gate, to_k, to_v; ff.up, ff.gate) issued on side streams); random-init "
                     "quantized weights, N(0,1) tokens; HIP "
                     "events around 8 Euler steps after one warm-up step of each; linears_ms_per_step: HIP events "
                     "around each linear of one forward"}
+
+
+def attention_line(args, dev) -> dict:
+    """The stand-in block's attention at config 3 (4352 tokens, 48 query heads over 12 KV heads,
+    d = 128): svdq::attention against PyTorch's fused SDPA kernels on the same inputs."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from krea2_svdquant_amd.kernels.hip import ops
+    t, heads, kvh, d = 4352, 48, 12, 128
+    gen = torch.Generator(device=dev).manual_seed(6)
+    q = torch.randn(t, heads, d, device=dev, generator=gen).to(torch.bfloat16)
+    k = torch.randn(t, kvh, d, device=dev, generator=gen).to(torch.bfloat16)
+    v = torch.randn(t, kvh, d, device=dev, generator=gen).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(d)
+    qh, kh, vh = (z.transpose(0, 1).unsqueeze(0) for z in (q, k, v))
+
+    def ours():
+        return ops.attention(q, k, v, scale)
+
+    def sdpa():
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, enable_gqa=True)
+    for f in (ours, sdpa):
+        for _ in range(5):
+            f()
+    ms = time_avg(ours, 20)
+    ms_sdpa = time_avg(sdpa, 20)
+    a, b = ours().float(), sdpa().squeeze(0).transpose(0, 1).float()
+    rel = float((a - b).norm() / b.norm())
+    flop = 4.0 * t * t * d * heads
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "TFLOPs": round(tf, 1), "bf16_peak_frac": round(tf / BF16_PEAK_TFLOPS, 4),
+            "ms_sdpa": round(ms_sdpa, 4), "TFLOPs_sdpa": round(flop / (ms_sdpa * 1e-3) / 1e12, 1),
+            "rel_l2_vs_sdpa": round(rel, 5),
+            "note": "softmax(q k^T / sqrt(d)) v, T=4352, 48 q / 12 kv heads, d=128, bf16, N(0,1) inputs; "
+                    "HIP events around 20 calls (all launches of a call), median of 3; flops = 4 T^2 d heads"}
 
 
 def pmc_pass_w4a16(args, dev) -> int:
@@ -550,6 +599,9 @@ def main() -> int:
         if "denoise" in lines:
             log("config 3: 28-block denoise steps at 1024px")
             result["denoise_config3"] = denoise_line(args, dev)
+        if "attention" in lines:
+            log("config 3: the block's attention")
+            result["attention_config3"] = attention_line(args, dev)
     if not args.no_cpu_baseline:
         log("cpu baseline (whole layer)")
         result["cpu_baseline"] = cpu_baseline(ds, x, args.cpu_reps)

@@ -224,6 +224,20 @@ int svdq_rms_norm_modulate(const void* x, int64_t ldx, const void* w, const void
 int svdq_head_rms_rope(const void* t, int T, int heads, const void* cos, const void* sin, int64_t ldcs, float eps,
                        void* out, hipStream_t stream);
 
+/* Softmax attention of the stand-in block (no mask), head dimension 128, grouped-query:
+ *   o[t, h, :] = sum_u softmax_u(scale * q[t, h, :] . k[u, h / (H / Hkv), :]) v[u, h / (H / Hkv), :]
+ * q, o: bf16 rows of H heads x 128 with row strides ldq, ldo; k, v: bf16 rows of Hkv heads x 128
+ * with row stride ldkv (elements; multiples of 8, pointers 16-byte aligned, o not overlapping the
+ * inputs).  Scores and softmax statistics float32, probabilities rounded to bf16 for the product
+ * with v, o rounded to bf16 once.  workspace: svdq_attention_workspace(T, H) bytes of device memory,
+ * 16-byte aligned, no initial contents (the call's kernels share it on the stream; overlapping
+ * calls need separate workspaces).  No counterpart in the reference: its blocks run in diffusers
+ * (reference src/krea2_svdquant/transformer.py:46-59), whose attention is PyTorch's
+ * scaled_dot_product_attention. */
+int64_t svdq_attention_workspace(int T, int H);
+int svdq_attention_fwd(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv, int T, int H,
+                       int Hkv, float scale, void* o, int64_t ldo, void* workspace, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,7 +17,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libsvdq_gfx950.so"
-SOURCES = ["svdq_act.hip", "svdq_gemm.hip", "svdq_block.hip", "svdq_capi.hip"]
+SOURCES = ["svdq_act.hip", "svdq_gemm.hip", "svdq_block.hip", "svdq_attn.hip", "svdq_capi.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -401,6 +401,28 @@ int svdq_head_rms_rope(const void* t, int T, int heads, const void* cos, const v
                   "head_rms_rope");
 }
 
+int64_t svdq_attention_workspace(int T, int H) {
+  return T > 0 && H > 0 ? (int64_t)svdq::attention_workspace_bytes(T, H) : 0;
+}
+
+int svdq_attention_fwd(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv, int T, int H,
+                       int Hkv, float scale, void* o, int64_t ldo, void* workspace, hipStream_t stream) {
+  if (!q || !k || !v || !o || !workspace) return fail(SVDQ_ERR_ARG, "attention_fwd: null pointer");
+  if (!aligned16(workspace)) return fail(SVDQ_ERR_ALIGN, "attention_fwd: workspace must be 16-byte aligned");
+  if (T <= 0 || H <= 0 || Hkv <= 0 || H % Hkv)
+    return fail(SVDQ_ERR_SHAPE, "attention_fwd: T=%d H=%d Hkv=%d (H must be a multiple of Hkv)", T, H, Hkv);
+  if (ldq < 128LL * H || ldo < 128LL * H || ldkv < 128LL * Hkv)
+    return fail(SVDQ_ERR_SHAPE, "attention_fwd: row strides ldq=%lld ldkv=%lld ldo=%lld below the heads' width",
+                (long long)ldq, (long long)ldkv, (long long)ldo);
+  if (!(scale > 0.0f) || !(scale < 1e30f)) return fail(SVDQ_ERR_ARG, "attention_fwd: scale must be positive and finite");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || ldq % 8 || ldkv % 8 || ldo % 8)
+    return fail(SVDQ_ERR_ALIGN, "attention_fwd: pointers must be 16-byte aligned and row strides multiples of 8");
+  return launched(svdq::launch_attention_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                             static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), T, H, Hkv,
+                                             ldq, ldkv, ldo, scale, workspace, stream),
+                  "attention_fwd");
+}
+
 int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const void* mid,
                     const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group, void* y,
                     int64_t ldy, int out_f32, hipStream_t stream) {

@@ -81,5 +81,10 @@ hipError_t launch_rms_norm_modulate(const uint16_t* x, long ldx, const uint16_t*
                                     int H, float eps, uint16_t* y, long ldy, hipStream_t st);
 hipError_t launch_head_rms_rope(const uint16_t* t, int T, int heads, const uint16_t* cs, const uint16_t* sn,
                                 long ldcs, float eps, uint16_t* out, hipStream_t st);
+// Stand-in block attention (svdq_attn.hip): softmax(scale q k^T) v, head dimension 128, H query heads
+// over Hkv key / value heads (H % Hkv == 0); rows of q / o hold H heads, rows of k / v Hkv heads
+hipError_t launch_attention_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int T, int H,
+                                int Hkv, long ldq, long ldkv, long ldo, float scale, void* workspace, hipStream_t st);
+long attention_workspace_bytes(int T, int H);
 
 }  // namespace svdq

@@ -381,3 +381,38 @@ def head_rms_rope(t: Tensor, cos: Tensor, sin: Tensor, eps: float) -> Tensor:
 @head_rms_rope.register_fake
 def _(t, cos, sin, eps):
     return torch.empty_like(t)
+
+
+@torch.library.custom_op("svdq::attention", mutates_args=())
+def attention(q: Tensor, k: Tensor, v: Tensor, scale: float) -> Tensor:
+    """Softmax attention ``softmax(scale q k^T) v`` without a mask: ``q`` [T, H, 128], ``k`` / ``v``
+    [T, Hkv, 128] (bf16, H a multiple of Hkv: query head h reads key / value head h // (H // Hkv))
+    -> [T, H, 128] bf16.  Rows may be strided (last two dimensions contiguous)."""
+    _need(q.is_cuda, RuntimeError, "svdq::attention needs GPU tensors")
+    dev = q.device
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _need(t.device == dev, ValueError, f"{name} is on {t.device}, expected {dev}")
+        _need(t.dtype == torch.bfloat16, TypeError, f"{name} must be torch.bfloat16, got {t.dtype}")
+        _need(t.dim() == 3 and t.shape[-1] == 128, ValueError, f"{name} must be [T, heads, 128], got {tuple(t.shape)}")
+    tok, heads, kvh = q.shape[0], q.shape[1], k.shape[1]
+    _need(k.shape == v.shape and k.shape[0] == tok, ValueError,
+          f"k and v must both be [{tok}, Hkv, 128], got {tuple(k.shape)} and {tuple(v.shape)}")
+    _need(heads % kvh == 0, ValueError, f"query heads ({heads}) must be a multiple of key / value heads ({kvh})")
+    _need(k.stride(0) == v.stride(0), ValueError, "k and v must share a row stride")
+
+    def rows(t: Tensor) -> Tensor:   # unit stride inside a row of heads, 16-byte aligned rows
+        ok = t.stride(2) == 1 and t.stride(1) == 128 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
+        return t if ok else t.contiguous()
+    q, k, v = rows(q), rows(k), rows(v)
+    if k.stride(0) != v.stride(0):
+        k, v = k.contiguous(), v.contiguous()
+    out = torch.empty((tok, heads, 128), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(lib.load().svdq_attention_workspace(tok, heads), dtype=torch.uint8, device=dev)
+    lib.call("svdq_attention_fwd", _vp(q), q.stride(0), _vp(k), _vp(v), k.stride(0), tok, heads, kvh,
+             ctypes.c_float(scale), _vp(out), out.stride(0), _vp(ws), _stream(dev))
+    return out
+
+
+@attention.register_fake
+def _(q, k, v, scale):
+    return q.new_empty((q.shape[0], q.shape[1], 128))

@@ -13,7 +13,7 @@ the concatenated text and latent tokens, modulation vectors fixed per block):
 
     h = rms_norm(x) * (1 + scale_a) + shift_a
     q, k, v = to_q(h), to_k(h), to_v(h);  per-head RMS norm of q and k;  rotary embedding on q, k
-    a = softmax(q k^T / sqrt(d)) v  (48 query heads over 12 KV heads, PyTorch SDPA)
+    a = softmax(q k^T / sqrt(d)) v  (48 query heads over 12 KV heads)
     x = x + gate_a * to_out.0(a * sigmoid(to_gate(h)))
     h = rms_norm(x) * (1 + scale_f) + shift_f
     x = x + gate_f * ff.down(silu(ff.gate(h)) * ff.up(h))
@@ -23,8 +23,10 @@ and the rotary embedding half by half: one bf16 rounding per fused op, fewer pas
 A denoise step is the 28 blocks over [text | latent] tokens followed by the Euler update of the
 latent tokens, ``latent += dt * velocity``.  On the GPU every quantized linear runs on the gfx950
 kernels (``SVDQuantLinear``), and so do the adaptive RMS norms and the per-head norm + rotary
-embedding (``svdq::rms_norm_modulate``, ``svdq::head_rms_rope``: one pass each); attention and
-the remaining elementwise work run in PyTorch-ROCm (on the CPU everything is torch).  With
+embedding (``svdq::rms_norm_modulate``, ``svdq::head_rms_rope``: one pass each) and the attention
+(``svdq::attention``, a flash-attention forward; ``ATTENTION = "sdpa"`` selects PyTorch's fused SDPA
+kernels instead); the remaining elementwise work runs in PyTorch-ROCm (on the CPU everything is
+torch).  With
 ``fused=True`` the sigmoid gate, the SwiGLU product and the two gated residual adds run inside
 the stores of to_gate, ff.up, to_out.0 and ff.down instead.
 """
@@ -239,14 +241,20 @@ class Krea2StandInBlock(nn.Module):
         return lin["ff.down"].forward_epilogue(f, "residual_gate", aux=x, vec=gate_f)
 
 
+ATTENTION = "hip"   # the GPU attention: "hip" (svdq::attention) or "sdpa" (PyTorch's fused kernels)
+
+
 def attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     """Softmax attention of q [T, H, d] over k, v [T, Hkv, d] (H a multiple of Hkv) -> [T, H*d].
 
-    On the GPU only the fused SDPA kernels are allowed (flash / memory-efficient); the math
+    On the GPU with d = 128 the gfx950 kernel (``svdq::attention``) unless ``ATTENTION`` is
+    "sdpa"; there only the fused SDPA kernels are allowed (flash / memory-efficient), the math
     path's batched products on transposed bf16 views are kept out.  Elsewhere (the CPU
     reference evaluation) SDPA picks its own path.
     """
     t, heads, dh = q.shape
+    if q.is_cuda and dh == 128 and ATTENTION == "hip":
+        return hip_ops.attention(q, k, v, 1.0 / math.sqrt(dh)).reshape(t, heads * dh)
     qh, kh, vh = (z.transpose(0, 1).unsqueeze(0) for z in (q, k, v))
     if q.is_cuda:
         from torch.nn.attention import SDPBackend, sdpa_kernel

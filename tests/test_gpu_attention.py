@@ -1,0 +1,137 @@
+"""GPU parity of the stand-in block's attention kernel (`svdq::attention`, `csrc/svdq_attn.hip`).
+
+The reference is the float32 evaluation of softmax(scale q k^T) v on the same bf16 inputs,
+per head with contiguous operands.  The kernel rounds the probabilities to bf16 before the
+product with v (as PyTorch's fused SDPA kernels do) and the output to bf16 once, so it is held
+to a relative L2 error of 4e-3 and, beside that, to an error no larger than twice SDPA's own on
+the same inputs (SDPA flash / memory-efficient, the path the stand-in used before).
+"""
+import math
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _reference(q, k, v, scale):
+    """float32 attention, one head at a time (q [T, H, d], k / v [T, Hkv, d]) -> [T, H, d]."""
+    t, heads, d = q.shape
+    g = heads // k.shape[1]
+    out = torch.empty((t, heads, d), dtype=torch.float32, device=q.device)
+    for hh in range(heads):
+        qh = q[:, hh].float().contiguous()
+        kh = k[:, hh // g].float().t().contiguous()
+        vh = v[:, hh // g].float().contiguous()
+        p = torch.softmax((qh @ kh) * scale, dim=-1)
+        out[:, hh] = p @ vh
+    return out
+
+
+def _sdpa(q, k, v):
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    qh, kh, vh = (z.transpose(0, 1).unsqueeze(0).contiguous() for z in (q, k, v))
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        o = torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, enable_gqa=True)
+    return o.squeeze(0).transpose(0, 1)
+
+
+def _rel(a, ref):
+    return float((a.float() - ref).norm() / ref.norm())
+
+
+def _check(q, k, v, tol=4e-3):
+    from krea2_svdquant_amd.kernels.hip import ops
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    out = ops.attention(q, k, v, scale)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+    ref = _reference(q, k, v, scale)
+    err = _rel(out, ref)
+    err_sdpa = _rel(_sdpa(q, k, v), ref)
+    assert err <= tol, f"rel-L2 {err:.2e} against the float32 evaluation"
+    assert err <= 2.0 * err_sdpa + 1e-4, f"rel-L2 {err:.2e}, SDPA {err_sdpa:.2e}"
+    return out
+
+
+def _inputs(t, heads, kvh, dev, seed, qscale=1.0):
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    q = (torch.randn(t, heads, 128, device=dev, generator=gen) * qscale).to(torch.bfloat16)
+    k = torch.randn(t, kvh, 128, device=dev, generator=gen).to(torch.bfloat16)
+    v = torch.randn(t, kvh, 128, device=dev, generator=gen).to(torch.bfloat16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("t,heads,kvh", [
+    (1, 4, 1),        # one key: softmax of a single score
+    (7, 8, 2),        # one partial key tile, one partial query block
+    (64, 8, 8),       # exactly one key tile, no grouping
+    (65, 8, 2),       # a second tile holding one key
+    (130, 12, 3),     # partial last tiles in both directions
+    (300, 48, 12),    # the stand-in's head counts
+])
+def test_attention_matches_float32(dev, t, heads, kvh):
+    q, k, v = _inputs(t, heads, kvh, dev, seed=t + heads)
+    _check(q, k, v)
+
+
+def test_attention_sharp_and_rising_scores(dev):
+    """Large scores (a near one-hot softmax) whose maximum grows from key tile to key tile: every
+    tile rescales the running output."""
+    t, heads, kvh = 333, 8, 2
+    q, k, v = _inputs(t, heads, kvh, dev, seed=5, qscale=6.0)
+    ramp = torch.linspace(0.5, 3.0, t, device=dev).view(t, 1, 1)
+    k = (k.float() * ramp).to(torch.bfloat16)
+    _check(q, k, v, tol=6e-3)
+
+
+def test_attention_scores_far_above_the_first_keys(dev):
+    """Keys 0..31 near zero, every later key aligned with q: later scores sit ~65 (log2 units)
+    above the first 32 keys' maximum, beyond what the fast kernel's fixed exponent offset takes,
+    so its waves hand their queries to the running-maximum kernel."""
+    t, heads, kvh = 200, 4, 2
+    gen = torch.Generator(device=dev).manual_seed(13)
+    q = (2.0 + 0.05 * torch.randn(t, heads, 128, device=dev, generator=gen)).to(torch.bfloat16)
+    k = 2.0 + 0.05 * torch.randn(t, kvh, 128, device=dev, generator=gen)
+    k[:32] = 0.01 * torch.randn(32, kvh, 128, device=dev, generator=gen)
+    k = k.to(torch.bfloat16)
+    v = torch.randn(t, kvh, 128, device=dev, generator=gen).to(torch.bfloat16)
+    scores = (q[:1, 0].float() @ k[:, 0].float().t().contiguous()) / math.sqrt(128) * math.log2(math.e)
+    assert float(scores[0, 32:].max() - scores[0, :32].max()) > 64
+    _check(q, k, v)
+
+
+def test_attention_strided_rows(dev):
+    """q, k, v as head slices of wider rows (row strides above the heads' width)."""
+    t, heads, kvh = 200, 8, 2
+    gen = torch.Generator(device=dev).manual_seed(9)
+    fused = torch.randn(t, (heads + 2 * kvh + 1) * 128, device=dev, generator=gen).to(torch.bfloat16)
+    q = fused[:, : heads * 128].view(t, heads, 128)
+    k = fused[:, heads * 128: (heads + kvh) * 128].view(t, kvh, 128)
+    v = fused[:, (heads + kvh) * 128: (heads + 2 * kvh) * 128].view(t, kvh, 128)
+    assert q.stride(0) == fused.shape[1] and not q.is_contiguous()
+    _check(q, k, v)
+
+
+def test_attention_config3_shape(dev):
+    """The stand-in block at config 3: 4096 latent + 256 text tokens, 48 query heads over 12."""
+    q, k, v = _inputs(4352, 48, 12, dev, seed=3)
+    _check(q, k, v)
+
+
+def test_attention_rejects_bad_shapes(dev):
+    from krea2_svdquant_amd.kernels.hip import ops
+    q, k, v = _inputs(16, 6, 4, dev, seed=1)
+    with pytest.raises(ValueError):
+        ops.attention(q, k, v, 0.1)                     # 6 heads over 4
+    with pytest.raises(ValueError):
+        ops.attention(q[..., :64].contiguous(), k, v, 0.1)
+    q2, k2, v2 = _inputs(16, 8, 2, dev, seed=2)
+    with pytest.raises(ValueError):
+        ops.attention(q2, k2, v2[:8], 0.1)
