@@ -23,17 +23,20 @@
 // each slice's keys permuted to that order, so one 16-byte read gives the matching A operand.
 //
 // Two kernels, one launch after the other on the same stream:
-//  * attn_fast_kernel (QB = 2, one wave per SIMD, O in AGPRs).  Each query's exponent offset is
-//    its maximum over the first 32 keys and never moves, so the output accumulators are touched
-//    by MFMAs only (an offset that follows the running maximum needs the output rescaled on the
-//    VALU, which makes the compiler shuttle the 128 accumulators between AGPRs and VGPRs every
-//    tile).  Later probabilities may exceed 1; up to 2^64 they are exact in bf16 / float32.  A
-//    wave whose scores rise further above the offset, or whose output is not finite, marks
-//    itself in the flag workspace (every wave writes its entry, so it needs no clearing) and
-//    stores nothing.
+//  * attn_fast_kernel (QB = 2, one wave per SIMD, O in AGPRs), software-pipelined so that the
+//    softmax of one half runs on the VALU between the MFMAs of the next half's scores and the
+//    previous half's output.  Each query's exponent offset is its maximum over the first 32 keys
+//    of its range and never moves, so the output accumulators are touched by MFMAs only (an offset
+//    that follows the running maximum needs the output rescaled on the VALU, which makes the
+//    compiler shuttle the 128 accumulators between AGPRs and VGPRs every tile).  Later
+//    probabilities may exceed 1; f32 and bf16 hold them exactly in range.  A wave whose row sum
+//    passes 2^64, or whose output is not finite, marks itself in the flag workspace (every wave
+//    writes its entry, so it needs no clearing) and stores nothing.
 //  * attn_safe_kernel (QB = 1, two waves per SIMD): the running-maximum formulation, output
 //    rescaled every tile.  A workgroup runs only if a fast wave of its queries was marked, and
 //    then writes those queries.
+// The items of the last, partly filled round over the CUs are cut along the keys into pieces whose
+// partial results attn_combine_kernel merges.
 #include "svdq_common.h"
 #include "svdq_kernels.h"
 
@@ -44,7 +47,7 @@ constexpr int AD = 128;               // head dimension
 constexpr int ABN = 64;               // keys per tile
 constexpr int KPITCH = AD * 2 + 16;   // LDS bytes per K row (272: 16 rows of a read hit distinct banks)
 constexpr int VPITCH = ABN * 2 + 16;  // LDS bytes per V^T row (144)
-constexpr float OFFSET_LIMIT = 64.0f; // log2 units above the fixed offset the fast kernel accepts
+constexpr float ROWSUM_LIMIT = 18446744073709551616.0f;   // 2^64: the fast kernel's largest accepted row sum
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -64,22 +67,27 @@ __device__ __forceinline__ float half_sum(float v) {
   return __uint_as_float(a) + __uint_as_float(b);
 }
 
-// The fast kernel's MFMAs as inline asm, so that the register classes are fixed: the scores in
-// VGPRs (read by the softmax), the output accumulators in AGPRs (read only at the end).  The
-// compiler does not see their hazards:
+// The fast kernel's MFMAs as volatile inline asm: the register classes are fixed (the scores in
+// VGPRs, read by the softmax; the output accumulators in AGPRs, read only at the end) and the
+// MFMAs keep their program order (and the LDS reads theirs around them).  The compiler does not
+// see their hazards, so the fast kernel keeps them itself:
 //  * an accumulator is only ever its own srcC (full overlap: no wait states);
 //  * k-step 0 of the scores uses a zero srcC, so no VALU-written zeros feed an MFMA;
-//  * the scores are read by VALU after score_fence (an 8-pass MFMA's result: 11 wait states);
-//  * the probabilities (VALU-written B operands) are read after 5 wait states;
+//  * VALU reads a score at least 16 MFMAs after it was written, or behind a 32-wait-state fence;
+//  * the probabilities (VALU-written B operands) are read at least one phase later, behind such a
+//    fence;
+//  * a source fragment's registers are not rewritten until two more MFMAs have issued, and the two
+//    MFMAs that share a fragment issue back to back (no VALU work between them);
 //  * the output is read after out_fence (2 x 16 wait states).
+// (tests/test_attn_mfma_order.py checks the last two rules on the built library.)
 __device__ __forceinline__ void mfma_score0(f32x16& acc, u32x4 a, u32x4 b) {
-  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
 }
 __device__ __forceinline__ void mfma_score(f32x16& acc, u32x4 a, u32x4 b) {
-  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
 }
 __device__ __forceinline__ void mfma_out(f32x16& acc, u32x4 a, u32x4 b) {
-  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
 // Work of the fast kernel: items (head, block of 256 queries), item = head * nq + block.  The
@@ -121,223 +129,421 @@ struct AttnArgs {
   int* part_flag;    // [tail * split, 4]: a piece's wave past the offset limit
 };
 
-template <bool FAST>
-__device__ __forceinline__ void attn_body(const AttnArgs& p) {
-  constexpr int QB = FAST ? 2 : 1;            // 32-query blocks per wave
-  constexpr int ABM = 4 * 32 * QB;            // queries per workgroup (4 waves)
-  __shared__ __attribute__((aligned(16))) uint8_t sK[2][ABN * KPITCH];
-  __shared__ __attribute__((aligned(16))) uint8_t sV[2][AD * VPITCH];
-  const int T = p.T;
-  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // fast kernel: item (or piece of one) -> head, query block, key tiles [j0, j1); safe kernel: the
-  // grid (query blocks of 128, heads)
-  const int nt = (T + ABN - 1) / ABN;
-  int head, q0, j0 = 0, j1 = nt, piece = -1;
-  if constexpr (FAST) {
-    const AttnPlan& pl = p.plan;
-    int item = blockIdx.x;
-    if (item >= pl.nmain) {
-      piece = item - pl.nmain;                       // tail piece index
-      item = pl.nmain + piece / pl.split;
-      j0 = (piece % pl.split) * pl.per;
-      j1 = min(nt, j0 + pl.per);
-    }
-    head = item / pl.nq;
-    q0 = (item % pl.nq) * ABM;
-  } else {
-    head = blockIdx.y;
-    q0 = blockIdx.x * ABM;
-  }
-  const int kvh = head / (p.H / p.Hkv);
-  const int qbase = q0 + wave * (32 * QB);   // the wave's first query
-  if constexpr (!FAST) {
-    // the two fast waves (64 queries each) that covered this workgroup's 128 queries
-    const int* fl = p.flags + (long)head * p.nflag + q0 / 64;
-    if (fl[0] == 0 && fl[1] == 0) return;   // workgroup-uniform
-  }
-
-  // Q^T fragments (B operand) of query block qb (queries qbase + 32 qb + lr): k-step s covers
-  // d = 16 s .. 16 s + 15, lane half h d 16 s + 8 h ..  (rows past T read row T - 1, never stored)
-  u32x4 qf[QB][AD / 16];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const long qc = min(qbase + 32 * qb + lr, T - 1);
-#pragma unroll
-    for (int s = 0; s < AD / 16; ++s) qf[qb][s] = ld16(p.q + qc * p.ldq + (long)head * AD + 16 * s + 8 * h);
-  }
-
-  // staging.  K: chunk idx = tid + 256 i (i = 0..3) is key row idx / 16, 16-byte d chunk idx % 16,
-  // stored as is.  V: thread t takes keys 4 (t % 16) .. 4 (t % 16) + 3 -- four keys whose V^T
-  // positions are adjacent -- at d chunk t / 16, and stores each of its 8 d rows' four values as
-  // one 8-byte write: a wave's 64 lanes then cover all 64 keys of 4 d rows (at most a 2-way bank
-  // conflict), where scattered 2-byte writes conflicted 8 ways.
-  const uint16_t* kbase = p.k + (long)kvh * AD;
-  const uint16_t* vbase = p.v + (long)kvh * AD;
-  const int vkg = tid & 15, vc = tid >> 4;   // V key group, d chunk
+// Global -> register -> LDS staging of a 64-key tile.  K: chunk idx = tid + 256 i (i = 0..3) is key
+// row tid / 16 + 16 i, 16-byte d chunk tid % 16, stored as is.  V: thread t takes keys
+// 4 (t % 16) .. + 3 -- four keys whose V^T positions are adjacent -- at d chunk t / 16, and stores
+// each of its 8 d rows' four values as one 8-byte write: a wave's 64 lanes then cover all 64 keys
+// of 4 d rows (at most a 2-way bank conflict), where scattered 2-byte writes conflicted 8 ways.
+// Keys past T read key T - 1; the scores mask them.
+struct TileStaging {
+  const uint16_t* kb;   // the KV head's K, this thread's d chunk
+  const uint16_t* vb;   // the KV head's V, this thread's d chunk
+  long ld;
+  int T, krow, vkey, kst, vst;
   u32x4 kr[4], vr[4];
-  auto gload = [&](int j) {
+  __device__ __forceinline__ TileStaging(const AttnArgs& p, int kvh, int tid) {
+    const int vkg = tid & 15, vc = tid >> 4;
+    kb = p.k + (long)kvh * AD + 8 * (tid & 15);
+    vb = p.v + (long)kvh * AD + 8 * vc;
+    ld = p.ldkv;
+    T = p.T;
+    krow = tid >> 4;
+    vkey = 4 * vkg;
+    kst = krow * KPITCH + 16 * (tid & 15);
+    // V^T byte column of key 4 vkg: slice vkg / 4, first position of keys 4 (vkg % 4) .. + 3
+    vst = 8 * vc * VPITCH + 2 * (16 * (vkg >> 2) + slice_pos(4 * (vkg & 3)));
+  }
+  __device__ __forceinline__ void load_k(int j) {
+    const int r0 = j * ABN + krow;
+    if ((j + 1) * ABN <= T) {
+      const uint16_t* src = kb + (long)r0 * ld;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i, row = idx >> 4, c = idx & 15;
-      // keys past T read key T - 1 and are masked
-      kr[i] = ld16(kbase + (long)min(j * ABN + row, T - 1) * p.ldkv + 8 * c);
-      vr[i] = ld16(vbase + (long)min(j * ABN + 4 * vkg + i, T - 1) * p.ldkv + 8 * vc);
-    }
-  };
-  // V^T byte column of key 4 vkg: slice vkg / 4, first position of keys 4 (vkg % 4) .. + 3
-  const int vcol = 2 * (16 * (vkg >> 2) + slice_pos(4 * (vkg & 3)));
-  auto lstore = [&](int buf) {
+      for (int i = 0; i < 4; ++i) kr[i] = ld16(src + 16 * i * ld);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i, row = idx >> 4, c = idx & 15;
-      *reinterpret_cast<u32x4*>(&sK[buf][row * KPITCH + 16 * c]) = kr[i];
+      for (int i = 0; i < 4; ++i) kr[i] = ld16(kb + (long)min(r0 + 16 * i, T - 1) * ld);
     }
+  }
+  __device__ __forceinline__ void load_v(int j) {
+    const int r0 = j * ABN + vkey;
+    if ((j + 1) * ABN <= T) {
+      const uint16_t* src = vb + (long)r0 * ld;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vr[i] = ld16(src + i * ld);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vr[i] = ld16(vb + (long)min(r0 + i, T - 1) * ld);
+    }
+  }
+  __device__ __forceinline__ void store_k(uint8_t* sk) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(sk + kst + 16 * i * KPITCH) = kr[i];
+  }
+  __device__ __forceinline__ void store_v(uint8_t* sv) const {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {   // d = 8 vc + 2 e (low halves) and 8 vc + 2 e + 1 (high halves)
       const u32x2 lo = {__builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x05040100u),
                         __builtin_amdgcn_perm(vr[3][e], vr[2][e], 0x05040100u)};
       const u32x2 hi = {__builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x07060302u),
                         __builtin_amdgcn_perm(vr[3][e], vr[2][e], 0x07060302u)};
-      *reinterpret_cast<u32x2*>(&sV[buf][(8 * vc + 2 * e) * VPITCH + vcol]) = lo;
-      *reinterpret_cast<u32x2*>(&sV[buf][(8 * vc + 2 * e + 1) * VPITCH + vcol]) = hi;
+      *reinterpret_cast<u32x2*>(sv + vst + 2 * e * VPITCH) = lo;
+      *reinterpret_cast<u32x2*>(sv + vst + (2 * e + 1) * VPITCH) = hi;
     }
-  };
+  }
+};
+
+// The safe kernel: one query block of 32 per wave, 128 queries per workgroup, the running-maximum
+// formulation (the output rescaled on the VALU whenever the maximum grows).  A workgroup runs only
+// if a fast wave of its queries was marked, and then writes all of its queries.
+__global__ void __launch_bounds__(256, 2) attn_safe_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t sK[2][ABN * KPITCH];
+  __shared__ __attribute__((aligned(16))) uint8_t sV[2][AD * VPITCH];
+  const int T = p.T;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nt = (T + ABN - 1) / ABN;
+  const int head = blockIdx.y, q0 = blockIdx.x * 128;
+  // the two fast waves (64 queries each) that covered these 128 queries
+  const int* fl = p.flags + (long)head * p.nflag + q0 / 64;
+  if (fl[0] == 0 && fl[1] == 0) return;   // workgroup-uniform
+  const int kvh = head / (p.H / p.Hkv);
+  const int qrow = q0 + 32 * wave + lr;
+  // Q^T fragments (B operand): k-step s covers d = 16 s .. 16 s + 15, lane half h d 16 s + 8 h ..
+  // (rows past T read row T - 1, never stored)
+  u32x4 qf[AD / 16];
+  const long qc = min(qrow, T - 1);
+#pragma unroll
+  for (int s = 0; s < AD / 16; ++s) qf[s] = ld16(p.q + qc * p.ldq + (long)head * AD + 16 * s + 8 * h);
+  TileStaging st(p, kvh, tid);
 
   // O^T accumulators: register r of d block db holds d = 32 db + 8 (r / 4) + 4 h + r % 4
-  f32x16 O[QB][AD / 32];
+  f32x16 O[AD / 32];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-    for (int db = 0; db < AD / 32; ++db) O[qb][db] = f32x16{};
-  float m_use[QB], l_lane[QB];   // exponent offset, the lane's share of the row sum
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    m_use[qb] = -INFINITY;
-    l_lane[qb] = 0.0f;
-  }
-  bool over = false;   // fast kernel: a score beyond the offset limit
+  for (int db = 0; db < AD / 32; ++db) O[db] = f32x16{};
+  float m_run = -INFINITY, l_lane = 0.0f;   // running maximum (log2 units), the lane's row sum
 
-  gload(j0);
-  lstore(0);
+  st.load_k(0);
+  st.load_v(0);
+  st.store_k(sK[0]);
+  st.store_v(sV[0]);
   __syncthreads();
-  for (int j = j0; j < j1; ++j) {
-    const int buf = (j - j0) & 1;
-    if (j + 1 < j1) gload(j + 1);
+  for (int j = 0; j < nt; ++j) {
+    const int buf = j & 1;
+    if (j + 1 < nt) {
+      st.load_k(j + 1);
+      st.load_v(j + 1);
+    }
     const int kvalid = T - j * ABN;   // keys of this tile below T (>= 1)
 #pragma unroll
     for (int hk = 0; hk < 2; ++hk) {
-      // S^T = K Q^T for keys 32 hk .. 32 hk + 31
-      f32x16 S[QB];
+      // S^T = K Q^T for keys 32 hk .. 32 hk + 31; register r holds key 32 hk + 8 (r / 4) + 4 h + r % 4
+      f32x16 S = {};
       const uint8_t* ka = &sK[buf][(32 * hk + lr) * KPITCH + 16 * h];
 #pragma unroll
-      for (int s = 0; s < AD / 16; ++s) {
-        const u32x4 a = ld16(ka + 32 * s);
+      for (int s = 0; s < AD / 16; ++s) S = mfma_bf16_32x32x16(ld16(ka + 32 * s), qf[s], S);
+      if (kvalid < 32 * hk + 32) {   // keys past T: -inf (wave-uniform)
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          if constexpr (FAST) {
-            if (s == 0) mfma_score0(S[qb], a, qf[qb][s]);
-            else mfma_score(S[qb], a, qf[qb][s]);
-          } else {
-            S[qb] = mfma_bf16_32x32x16(a, qf[qb][s], s == 0 ? f32x16{} : S[qb]);
-          }
+        for (int r = 0; r < 16; ++r)
+          if (32 * hk + 8 * (r >> 2) + 4 * h + (r & 3) >= kvalid) S[r] = -INFINITY;
+      }
+      float m = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m = fmaxf(m, S[r]);
+      // the scale is positive, so the maximum is taken over the raw scores
+      const float m_new = fmaxf(m_run, half_max(m) * p.scale_log2);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_lane *= alpha;
+#pragma unroll
+      for (int db = 0; db < AD / 32; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) O[db][r] *= alpha;
+      // probabilities rounded to bf16 (the B operands of P^T, one per 16-key slice); the row sum
+      // over the same bf16 values, two per v_dot2
+      u32x4 pf[2];
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(S[8 * sl + 2 * e], p.scale_log2, -m_run));
+          const float b = __builtin_amdgcn_exp2f(__builtin_fmaf(S[8 * sl + 2 * e + 1], p.scale_log2, -m_run));
+          const uint32_t w = pack_bf16x2(a, b);
+          pf[sl][e] = w;
+          l_lane = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                                   __builtin_bit_cast(bf16x2, 0x3F803F80u), l_lane, false);
         }
-      }
-      if constexpr (FAST) asm volatile("s_nop 10" : "+v"(S[0]), "+v"(S[1]));   // score_fence (QB = 2)
-      // softmax in log2 units, p = exp2(scale_log2 s - m) (the scale is positive, so the maximum
-      // is taken over the raw scores); register r holds key 32 hk + 8 (r / 4) + 4 h + r % 4.
-      // Keys past T (last tile only) get a score of -inf.
-      if (kvalid < 32 * hk + 32) {   // wave-uniform
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (32 * hk + 8 * (r >> 2) + 4 * h + (r & 3) >= kvalid) S[qb][r] = -INFINITY;
-      }
-      float mt[QB];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        float m = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) m = fmaxf(m, S[qb][r]);
-        mt[qb] = half_max(m) * p.scale_log2;
-      }
-      if constexpr (FAST) {
-        if (j == j0 && hk == 0) {
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) m_use[qb] = mt[qb];   // key 0 is valid: finite
-        }
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) over |= mt[qb] > m_use[qb] + OFFSET_LIMIT;
-      } else {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          const float m_new = fmaxf(m_use[qb], mt[qb]);
-          const float alpha = __builtin_amdgcn_exp2f(m_use[qb] - m_new);
-          m_use[qb] = m_new;
-          l_lane[qb] *= alpha;
-#pragma unroll
-          for (int db = 0; db < AD / 32; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) O[qb][db][r] *= alpha;
-        }
-      }
-      // probabilities rounded to bf16: the B operands of P^T, one per 16-key slice
-      u32x4 pf[QB][2];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)   // (a fast wave past the offset limit may overflow: it is marked)
-          S[qb][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[qb][r], p.scale_log2, -m_use[qb]));
-        // the row sum over the bf16 probabilities the P V product uses, two per v_dot2
-        float ls = l_lane[qb];
-#pragma unroll
-        for (int sl = 0; sl < 2; ++sl)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            // (the packed word goes through a scalar: bit-casting the vector element itself
-            // compiles to a read of element 0)
-            const uint32_t w = pack_bf16x2(S[qb][8 * sl + 2 * e], S[qb][8 * sl + 2 * e + 1]);
-            pf[qb][sl][e] = w;
-            ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3F803F80u),
-                                                 ls, false);
-          }
-        l_lane[qb] = ls;
-      }
-      if constexpr (FAST)   // the B operands were written by VALU
-        asm volatile("s_nop 4" : "+v"(pf[0][0]), "+v"(pf[0][1]), "+v"(pf[1][0]), "+v"(pf[1][1]));
       // O^T += V^T P^T over the half's two 16-key slices
 #pragma unroll
       for (int db = 0; db < AD / 32; ++db) {
         const uint8_t* va = &sV[buf][(32 * db + lr) * VPITCH + 16 * h + 64 * hk];
 #pragma unroll
-        for (int sl = 0; sl < 2; ++sl) {
-          const u32x4 a = ld16(va + 32 * sl);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) {
-            if constexpr (FAST) mfma_out(O[qb][db], a, pf[qb][sl]);
-            else O[qb][db] = mfma_bf16_32x32x16(a, pf[qb][sl], O[qb][db]);
-          }
-        }
+        for (int sl = 0; sl < 2; ++sl) O[db] = mfma_bf16_32x32x16(ld16(va + 32 * sl), pf[sl], O[db]);
       }
     }
-    if (j + 1 < j1) lstore(buf ^ 1);   // the buffer every wave finished reading before the last barrier
+    if (j + 1 < nt) {   // the buffer every wave finished reading before the last barrier
+      st.store_k(sK[buf ^ 1]);
+      st.store_v(sV[buf ^ 1]);
+    }
     __syncthreads();
   }
-  if constexpr (FAST) {
+  if (qrow < T) {
+    const float inv = 1.0f / half_sum(l_lane);
+    uint16_t* orow = p.o + (long)qrow * p.ldo + (long)head * AD;
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb)   // out_fence
-      asm volatile("s_nop 15\n\ts_nop 15" : "+a"(O[qb][0]), "+a"(O[qb][1]), "+a"(O[qb][2]), "+a"(O[qb][3]));
+    for (int db = 0; db < AD / 32; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * g + 4 * h) =
+            u32x2{pack_bf16x2(O[db][4 * g] * inv, O[db][4 * g + 1] * inv),
+                  pack_bf16x2(O[db][4 * g + 2] * inv, O[db][4 * g + 3] * inv)};
   }
-  if (FAST && piece >= 0) {
+}
+
+template <bool B> struct Flag { static constexpr bool value = B; };
+
+// pin(x): an empty asm that claims to rewrite x.  VALU work that reads x cannot move above it and
+// work that produces x cannot move below it; with the MFMAs as volatile asm (kept in program
+// order, and LDS reads with them) this fixes the interleaving of the fast kernel's phases.
+template <typename V> __device__ __forceinline__ void pin(V& x) { asm volatile("" : "+v"(x)); }
+// hold(x): an empty asm that reads x, so its registers stay allocated up to this point
+template <typename V> __device__ __forceinline__ void hold(const V& x) { asm volatile("" ::"v"(x)); }
+
+// The fast kernel: 64 queries per wave (two blocks of 32), 256 per workgroup, one wave per SIMD,
+// software-pipelined over half tiles of 32 keys.  Stage t holds K tile t and V tile t - 1 in one
+// LDS buffer and runs two phases; a phase issues
+//   the score MFMAs of the next half (16: S^T = K Q^T),
+//   the output MFMAs of the previous half (16: O^T += V^T P^T, P from the phase before),
+//   the softmax of the current half (its scores from the phase before),
+// interleaved one VALU part per MFMA, so the VALU work runs while the matrix cores are busy (a
+// wave's MFMAs and its own independent VALU work overlap when interleaved; phases of MFMAs only
+// and VALU only do not).  The exponent offset is fixed per query (its maximum over the range's
+// first 32 keys), so the output accumulators are touched by MFMAs only and stay in AGPRs; a wave
+// whose row sum passes 2^64, or whose output is not finite, is marked for the safe kernel.
+//
+// Hazards the compiler cannot see (MFMAs in asm): every score read by VALU was written at least 16
+// MFMAs earlier or behind a score fence (11 wait states), every probability read by an MFMA was
+// written by VALU at least one phase earlier and behind a 5-wait-state fence, accumulators are
+// only their own srcC, and the output is read after 2 x 16 wait states.
+__global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
+  constexpr int QB = 2;
+  __shared__ __attribute__((aligned(16))) uint8_t sK[2][ABN * KPITCH];
+  __shared__ __attribute__((aligned(16))) uint8_t sV[2][AD * VPITCH];
+  const int T = p.T;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nt = (T + ABN - 1) / ABN;
+  // item (or piece of one) -> head, query block, key tiles [j0, j1)
+  const AttnPlan& pl = p.plan;
+  int item = blockIdx.x, j0 = 0, j1 = nt, piece = -1;
+  if (item >= pl.nmain) {
+    piece = item - pl.nmain;
+    item = pl.nmain + piece / pl.split;
+    j0 = (piece % pl.split) * pl.per;
+    j1 = min(nt, j0 + pl.per);
+  }
+  const int head = item / pl.nq, q0 = (item % pl.nq) * 256;
+  const int kvh = head / (p.H / p.Hkv);
+  const int qbase = q0 + 64 * wave;   // the wave's first query
+
+  u32x4 qf[QB][AD / 16];   // Q^T fragments of query block qb (queries qbase + 32 qb + lr)
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const long qc = min(qbase + 32 * qb + lr, T - 1);
+#pragma unroll
+    for (int s = 0; s < AD / 16; ++s) qf[qb][s] = ld16(p.q + qc * p.ldq + (long)head * AD + 16 * s + 8 * h);
+  }
+  TileStaging st(p, kvh, tid);
+
+  f32x16 O[QB][AD / 32];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int db = 0; db < AD / 32; ++db) O[qb][db] = f32x16{};
+  f32x16 Sn[QB];              // scores of the next half (written by this phase's MFMAs)
+  float sc[QB][16];           // scores of the current half (register r: key 8 (r / 4) + 4 h + r % 4)
+  u32x4 pp[QB][2], pc[QB][2]; // bf16 probabilities of the previous / current half, per 16-key slice
+  float m_use[QB], ls[QB] = {0.0f, 0.0f};   // exponent offset, the lane's share of the row sum
+  const float sl2 = p.scale_log2;
+  const int klane = lr * KPITCH + 16 * h, vlane = lr * VPITCH + 16 * h;
+
+  auto phase = [&](auto s_, auto pv_, auto soft_, const uint8_t* ka, const uint8_t* va) {
+    constexpr bool DS = decltype(s_)::value, DPV = decltype(pv_)::value, DSOFT = decltype(soft_)::value;
+    constexpr int NF = 8 * (DS + DPV);   // A fragments: K rows of the 8 k-steps, V^T (d block, slice)
+    constexpr int AHEAD = 3;             // fragments read ahead of their first MFMA
+    auto frag = [&](int f) {
+      const int g = f - 8 * DS;
+      return DS && f < 8 ? ld16(ka + 32 * f) : ld16(va + (g >> 1) * (32 * VPITCH) + 32 * (g & 1));
+    };
+    u32x4 fr[16];
+#pragma unroll
+    for (int f = 0; f < AHEAD; ++f) fr[f] = frag(f);
+    float xs[16][2];
+    uint32_t pw[QB][2][4];
+    // softmax part i: pair k = i / 2 (query block qb, slice sl, word e: scores r, r + 1); even
+    // parts take exp2, odd parts pack the bf16 word and add it to the row sum
+    auto part = [&](int i) {
+      const int k = i >> 1, qb = k >> 3, sl = (k >> 2) & 1, e = k & 3, r = 8 * sl + 2 * e;
+      if ((i & 1) == 0) {
+        pin(sc[qb][r]);
+        pin(sc[qb][r + 1]);
+        xs[k][0] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][r], sl2, -m_use[qb]));
+        xs[k][1] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][r + 1], sl2, -m_use[qb]));
+        pin(xs[k][0]);
+        pin(xs[k][1]);
+      } else {
+        // (the packed word goes through a scalar: bit-casting a vector element compiles to a
+        // read of element 0)
+        pin(xs[k][0]);
+        pin(xs[k][1]);
+        const uint32_t w = pack_bf16x2(xs[k][0], xs[k][1]);
+        pw[qb][sl][e] = w;
+        ls[qb] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                                 __builtin_bit_cast(bf16x2, 0x3F803F80u), ls[qb], false);
+        pin(pw[qb][sl][e]);
+        pin(ls[qb]);
+      }
+    };
+    // per fragment: its share of the softmax parts, the LDS read AHEAD fragments on, then its two
+    // MFMAs (query blocks 0 and 1) back to back.  (VALU work issued between two MFMAs that share
+    // an A operand, while the first still runs, corrupted the second's result on gfx950 in
+    // testing; back-to-back pairs and VALU work between pairs are exact.)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      if constexpr (DSOFT) {
+#pragma unroll
+        for (int j = 0; j < 32 / NF; ++j) part(f * (32 / NF) + j);
+      }
+      if (f + AHEAD < NF) fr[f + AHEAD] = frag(f + AHEAD);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        if (DS && f < 8) {
+          if (f == 0) mfma_score0(Sn[qb], fr[f], qf[qb][f]);
+          else mfma_score(Sn[qb], fr[f], qf[qb][f & 7]);
+        } else {
+          const int g = max(f - 8 * DS, 0);
+          mfma_out(O[qb][g >> 1], fr[f], pp[qb][g & 1]);
+        }
+      }
+      // operand hold: fragment f - 1 was last read two MFMAs ago; until here its registers may
+      // not be rewritten (by the interleaved VALU work or an LDS read)
+      if (f >= 1) hold(fr[f - 1]);
+    }
+    if constexpr (DSOFT) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) pc[qb][sl] = u32x4{pw[qb][sl][0], pw[qb][sl][1], pw[qb][sl][2], pw[qb][sl][3]};
+    }
+    // phase fence (32 wait states: a whole 8-pass MFMA) before the registers of the phase's last
+    // operands -- the last fragment, the previous probabilities -- are released, and before VALU
+    // reads scores written by a phase that ends on score MFMAs
+    if constexpr (DPV)
+      asm volatile("s_nop 15\n\ts_nop 15" ::"v"(fr[NF - 1]), "v"(pp[0][0]), "v"(pp[0][1]), "v"(pp[1][0]), "v"(pp[1][1]));
+    else
+      asm volatile("s_nop 15\n\ts_nop 15" ::"v"(fr[NF - 1]));
+    if constexpr (DS) {   // (pins after the fence: the scores' readers stay below it)
+      pin(Sn[0]);
+      pin(Sn[1]);
+    }
+    if constexpr (DSOFT) {
+      pin(pc[0][0]);
+      pin(pc[0][1]);
+      pin(pc[1][0]);
+      pin(pc[1][1]);
+    }
+  };
+  auto take_scores = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[qb][r] = Sn[qb][r];
+  };
+  auto take_probs = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) pp[qb][sl] = pc[qb][sl];
+  };
+  // keys past T (last tile only) get a score of -inf
+  auto mask = [&](int j, int hk) {
+    const int kvalid = T - j * ABN;
+    if (kvalid < 32 * hk + 32) {   // wave-uniform
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (32 * hk + 8 * (r >> 2) + 4 * h + (r & 3) >= kvalid) sc[qb][r] = -INFINITY;
+    }
+  };
+  using Y = Flag<true>;
+  using N = Flag<false>;
+
+  // stage j0: K tile j0 only
+  st.load_k(j0);
+  st.store_k(sK[0]);
+  __syncthreads();
+  if (j0 + 1 < j1) st.load_k(j0 + 1);
+  st.load_v(j0);
+  phase(Y{}, N{}, N{}, &sK[0][klane], nullptr);
+  take_scores();
+  mask(j0, 0);
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {   // the offsets: the first 32 keys' maximum (key 64 j0 < T: finite)
+    float m = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m = fmaxf(m, sc[qb][r]);
+    m_use[qb] = half_max(m) * sl2;   // the scale is positive: the maximum of the raw scores
+  }
+  phase(Y{}, N{}, Y{}, &sK[0][32 * KPITCH + klane], nullptr);
+  take_probs();
+  take_scores();
+  if (j0 + 1 < j1) st.store_k(sK[1]);
+  st.store_v(sV[1]);
+  __syncthreads();
+  // stages j0 + 1 .. j1 - 1: K tile t, V tile t - 1
+  for (int t = j0 + 1; t < j1; ++t) {
+    const int b = (t - j0) & 1;
+    if (t + 1 < j1) st.load_k(t + 1);
+    st.load_v(t);
+    // softmax of tile t - 1's second half (not the range's last tile: no mask)
+    phase(Y{}, Y{}, Y{}, &sK[b][klane], &sV[b][vlane]);
+    take_probs();
+    take_scores();
+    mask(t, 0);
+    phase(Y{}, Y{}, Y{}, &sK[b][32 * KPITCH + klane], &sV[b][64 + vlane]);
+    take_probs();
+    take_scores();
+    if (t + 1 < j1) st.store_k(sK[b ^ 1]);
+    st.store_v(sV[b ^ 1]);
+    __syncthreads();
+  }
+  // stage j1: V tile j1 - 1 only
+  {
+    const int b = (j1 - j0) & 1;
+    mask(j1 - 1, 1);
+    phase(N{}, Y{}, Y{}, nullptr, &sV[b][vlane]);
+    take_probs();
+    phase(N{}, Y{}, N{}, nullptr, &sV[b][64 + vlane]);
+  }
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)   // output fence
+    asm volatile("s_nop 15\n\ts_nop 15" : "+a"(O[qb][0]), "+a"(O[qb][1]), "+a"(O[qb][2]), "+a"(O[qb][3]));
+
+  bool over = false;
+  float l[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    l[qb] = half_sum(ls[qb]);
+    over |= !(l[qb] <= ROWSUM_LIMIT);   // also catches inf / NaN
+  }
+  if (piece >= 0) {
     // a piece: its unnormalized output, offset and row sum for the combine (rows past T too)
     const bool mark = __any(over);
     if (lane == 0) p.part_flag[piece * 4 + wave] = mark ? 1 : 0;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      const long row = (long)piece * 256 + wave * (32 * QB) + 32 * qb + lr;
-      const float l = half_sum(l_lane[qb]);
-      if (h == 0) *reinterpret_cast<f32x2*>(p.part_ml + 2 * row) = f32x2{m_use[qb], l};
+      const long row = (long)piece * 256 + 64 * wave + 32 * qb + lr;
+      if (h == 0) *reinterpret_cast<f32x2*>(p.part_ml + 2 * row) = f32x2{m_use[qb], l[qb]};
       float* orow = p.part_o + row * AD;
 #pragma unroll
       for (int db = 0; db < AD / 32; ++db)
@@ -348,25 +554,23 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
     }
     return;
   }
-  // normalize (lanes l and l ^ 32 hold the same query); the fast kernel checks every value first
+  // normalize (lanes l and l ^ 32 hold the same query), checking every value first
   uint32_t pk[QB][AD / 32][8];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    const float inv = 1.0f / half_sum(l_lane[qb]);
+    const float inv = 1.0f / l[qb];
     const bool live = qbase + 32 * qb + lr < T;
 #pragma unroll
     for (int db = 0; db < AD / 32; ++db)
 #pragma unroll
       for (int g = 0; g < 8; ++g) {
         const float a = O[qb][db][2 * g] * inv, b = O[qb][db][2 * g + 1] * inv;
-        if (FAST) over |= live && !(__builtin_isfinite(a) && __builtin_isfinite(b));
+        over |= live && !(__builtin_isfinite(a) && __builtin_isfinite(b));
         pk[qb][db][g] = pack_bf16x2(a, b);
       }
   }
-  const bool mark = FAST && __any(over);   // wave-uniform
-  if constexpr (FAST) {
-    if (lane == 0) p.flags[(long)head * p.nflag + qbase / 64] = mark ? 1 : 0;
-  }
+  const bool mark = __any(over);   // wave-uniform
+  if (lane == 0) p.flags[(long)head * p.nflag + qbase / 64] = mark ? 1 : 0;
   if (!mark) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -382,9 +586,6 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
     }
   }
 }
-
-__global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) { attn_body<true>(p); }
-__global__ void __launch_bounds__(256, 2) attn_safe_kernel(AttnArgs p) { attn_body<false>(p); }
 
 // Merges the pieces of a tail item, 16 threads per query (one 8-column chunk each, so that a
 // wave reads 4 whole 512-byte rows of a piece): workgroup g takes queries 16 (g % 16) ...

@@ -91,10 +91,29 @@ def test_attention_sharp_and_rising_scores(dev):
     _check(q, k, v, tol=6e-3)
 
 
+def _fast_flags(q, k, v, scale):
+    """Run the C-ABI entry point with a workspace of our own and return (output, the per-wave
+    flags it leaves at the workspace's start: [H, 4 ceil(T / 256)] int32, 1 = query block
+    written by the running-maximum kernel)."""
+    import ctypes
+    from krea2_svdquant_amd.kernels.hip import lib
+    t, heads, kvh = q.shape[0], q.shape[1], k.shape[1]
+    out = torch.empty_like(q)
+    ws = torch.empty(lib.load().svdq_attention_workspace(t, heads), dtype=torch.uint8, device=q.device)
+    vp = lambda z: ctypes.c_void_p(z.data_ptr())
+    lib.call("svdq_attention_fwd", vp(q), q.stride(0), vp(k), vp(v), k.stride(0), t, heads, kvh,
+             ctypes.c_float(scale), vp(out), out.stride(0), vp(ws),
+             ctypes.c_void_p(torch.cuda.current_stream(q.device).cuda_stream))
+    nflag = 4 * ((t + 255) // 256)
+    flags = ws[: heads * nflag * 4].view(torch.int32).view(heads, nflag)
+    return out, flags
+
+
 def test_attention_scores_far_above_the_first_keys(dev):
     """Keys 0..31 near zero, every later key aligned with q: later scores sit ~65 (log2 units)
-    above the first 32 keys' maximum, beyond what the fast kernel's fixed exponent offset takes,
-    so its waves hand their queries to the running-maximum kernel."""
+    above the first 32 keys' maximum (the fast kernel's fixed exponent offset), so the fast
+    kernel's row sums pass 2^64 and its waves hand their queries to the running-maximum kernel,
+    whose output is checked here."""
     t, heads, kvh = 200, 4, 2
     gen = torch.Generator(device=dev).manual_seed(13)
     q = (2.0 + 0.05 * torch.randn(t, heads, 128, device=dev, generator=gen)).to(torch.bfloat16)
@@ -104,7 +123,18 @@ def test_attention_scores_far_above_the_first_keys(dev):
     v = torch.randn(t, kvh, 128, device=dev, generator=gen).to(torch.bfloat16)
     scores = (q[:1, 0].float() @ k[:, 0].float().t().contiguous()) / math.sqrt(128) * math.log2(math.e)
     assert float(scores[0, 32:].max() - scores[0, :32].max()) > 64
-    _check(q, k, v)
+    out = _check(q, k, v)
+    out2, flags = _fast_flags(q, k, v, 1.0 / math.sqrt(128))
+    live = flags[:, : (t + 63) // 64]           # query blocks of 64 that hold queries below T
+    assert bool((live == 1).all()), flags
+    assert torch.equal(out2, out)
+
+
+def test_attention_random_inputs_stay_on_the_fast_kernel(dev):
+    """N(0, 1) inputs at the config-3 head counts: no fast wave hands its queries over."""
+    q, k, v = _inputs(1000, 48, 12, dev, seed=21)
+    _, flags = _fast_flags(q, k, v, 1.0 / math.sqrt(128))
+    assert int(flags.sum()) == 0
 
 
 def test_attention_strided_rows(dev):
