@@ -136,43 +136,43 @@ struct AttnArgs {
 // of 4 d rows (at most a 2-way bank conflict), where scattered 2-byte writes conflicted 8 ways.
 // Keys past T read key T - 1; the scores mask them.
 struct TileStaging {
-  const uint16_t* kb;   // the KV head's K, this thread's d chunk
-  const uint16_t* vb;   // the KV head's V, this thread's d chunk
+  const uint16_t* kb;   // the KV head's K, this thread's first row and d chunk
+  const uint16_t* vb;   // the KV head's V, this thread's first row and d chunk
   long ld;
   int T, krow, vkey, kst, vst;
   u32x4 kr[4], vr[4];
   __device__ __forceinline__ TileStaging(const AttnArgs& p, int kvh, int tid) {
     const int vkg = tid & 15, vc = tid >> 4;
-    kb = p.k + (long)kvh * AD + 8 * (tid & 15);
-    vb = p.v + (long)kvh * AD + 8 * vc;
     ld = p.ldkv;
     T = p.T;
     krow = tid >> 4;
     vkey = 4 * vkg;
+    kb = p.k + (long)kvh * AD + 8 * (tid & 15) + krow * ld;
+    vb = p.v + (long)kvh * AD + 8 * vc + vkey * ld;
     kst = krow * KPITCH + 16 * (tid & 15);
     // V^T byte column of key 4 vkg: slice vkg / 4, first position of keys 4 (vkg % 4) .. + 3
     vst = 8 * vc * VPITCH + 2 * (16 * (vkg >> 2) + slice_pos(4 * (vkg & 3)));
   }
+  // rows of tile j: whole tiles step the row pointers by 64 rows (uniform offsets); the last,
+  // partial tile clamps each row to T - 1
   __device__ __forceinline__ void load_k(int j) {
-    const int r0 = j * ABN + krow;
     if ((j + 1) * ABN <= T) {
-      const uint16_t* src = kb + (long)r0 * ld;
+      const uint16_t* src = kb + (long)j * ABN * ld;
 #pragma unroll
       for (int i = 0; i < 4; ++i) kr[i] = ld16(src + 16 * i * ld);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[i] = ld16(kb + (long)min(r0 + 16 * i, T - 1) * ld);
+      for (int i = 0; i < 4; ++i) kr[i] = ld16(kb + (long)(min(j * ABN + krow + 16 * i, T - 1) - krow) * ld);
     }
   }
   __device__ __forceinline__ void load_v(int j) {
-    const int r0 = j * ABN + vkey;
     if ((j + 1) * ABN <= T) {
-      const uint16_t* src = vb + (long)r0 * ld;
+      const uint16_t* src = vb + (long)j * ABN * ld;
 #pragma unroll
       for (int i = 0; i < 4; ++i) vr[i] = ld16(src + i * ld);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vr[i] = ld16(vb + (long)min(r0 + i, T - 1) * ld);
+      for (int i = 0; i < 4; ++i) vr[i] = ld16(vb + (long)(min(j * ABN + vkey + i, T - 1) - vkey) * ld);
     }
   }
   __device__ __forceinline__ void store_k(uint8_t* sk) const {
@@ -366,17 +366,49 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
   const float sl2 = p.scale_log2;
   const int klane = lr * KPITCH + 16 * h, vlane = lr * VPITCH + 16 * h;
 
-  auto phase = [&](auto s_, auto pv_, auto soft_, const uint8_t* ka, const uint8_t* va) {
-    constexpr bool DS = decltype(s_)::value, DPV = decltype(pv_)::value, DSOFT = decltype(soft_)::value;
-    constexpr int NF = 8 * (DS + DPV);   // A fragments: K rows of the 8 k-steps, V^T (d block, slice)
-    constexpr int AHEAD = 3;             // fragments read ahead of their first MFMA
-    auto frag = [&](int f) {
-      const int g = f - 8 * DS;
-      return DS && f < 8 ? ld16(ka + 32 * f) : ld16(va + (g >> 1) * (32 * VPITCH) + 32 * (g & 1));
-    };
-    u32x4 fr[16];
+  // A fragments of a phase: id < 8 the K rows of k-step id (if the phase has score MFMAs), then
+  // V^T (d block, slice).  A phase issues its MFMAs in slots:
+  //  * with both kinds, S_g q0, PV_g q0, S_g q1, PV_g q1 for g = 0..7 (32 slots): no two adjacent
+  //    MFMAs read the same fragment, so one softmax part goes before every MFMA;
+  //  * with one kind, the two MFMAs of a fragment back to back (16 slots), the softmax parts
+  //    before the first of each pair.
+  // (VALU work issued between two adjacent MFMAs that read the same fragment, while the first
+  // still ran, corrupted the second's result on gfx950 in testing; with no VALU work between them,
+  // or an MFMA of another fragment, they are exact.  One wave per SIMD stalls in order behind an
+  // MFMA that waits for the matrix pipe, so VALU work placed between MFMAs of different fragments
+  // hides under twice as much MFMA time as work placed only between pairs.)
+  // A fragment is read from LDS LEAD slots before its first use; the ones used earlier than that
+  // come from pre, read during the phase before (or by prefetch after a barrier).
+  constexpr int LEAD = 6;
+  u32x4 pre[4];
+  auto slot_id = [](bool both, int i) { return both ? ((i & 1) ? 8 + (i >> 2) : (i >> 2)) : (i >> 1); };
+  auto slot_qb = [](bool both, int i) { return both ? (i >> 1) & 1 : i & 1; };
+  auto first_use = [](bool both, int id) { return both ? (id < 8 ? 4 * id : 4 * (id - 8) + 1) : 2 * id; };
+  auto last_use = [](bool both, int id) { return both ? (id < 8 ? 4 * id + 2 : 4 * (id - 8) + 3) : 2 * id + 1; };
+  auto npre = [](bool both) { return both ? 4 : 3; };                         // first use < LEAD
+  auto pre_id = [](bool both, int r) { return both ? ((r & 1) ? 8 + (r >> 1) : (r >> 1)) : r; };
+  auto frag_at = [](bool ds, const uint8_t* ka, const uint8_t* va, int id) {
+    const int g = id - 8 * ds;
+    return ds && id < 8 ? ld16(ka + 32 * id) : ld16(va + (g >> 1) * (32 * VPITCH) + 32 * (g & 1));
+  };
+  auto prefetch = [&](auto s_, auto pv_, const uint8_t* ka, const uint8_t* va) {
+    constexpr bool DS = decltype(s_)::value, BOTH = DS && decltype(pv_)::value;
 #pragma unroll
-    for (int f = 0; f < AHEAD; ++f) fr[f] = frag(f);
+    for (int r = 0; r < npre(BOTH); ++r) pre[r] = frag_at(DS, ka, va, pre_id(BOTH, r));
+  };
+  // nx_: the next phase, whose first fragments are read during this one's last slots (0: none, it
+  // follows a barrier; 1: score MFMAs only, K rows nka; 2: output MFMAs only, V^T rows nva; 3: both)
+  auto phase = [&](auto s_, auto pv_, auto soft_, const uint8_t* ka, const uint8_t* va, auto nx_,
+                   const uint8_t* nka, const uint8_t* nva) {
+    constexpr bool DS = decltype(s_)::value, DPV = decltype(pv_)::value, DSOFT = decltype(soft_)::value;
+    constexpr int NX = decltype(nx_)::value;
+    constexpr bool NDS = NX & 1, NBOTH = NX == 3;
+    constexpr bool BOTH = DS && DPV;
+    constexpr int NS = BOTH ? 32 : 16;   // slots (MFMAs)
+    constexpr int NF = BOTH ? 16 : 8;    // fragments
+    u32x4 fr[16];                        // by fragment id
+#pragma unroll
+    for (int r = 0; r < npre(BOTH); ++r) fr[pre_id(BOTH, r)] = pre[r];
     float xs[16][2];
     uint32_t pw[QB][2][4];
     // softmax part i: pair k = i / 2 (query block qb, slice sl, word e: scores r, r + 1); even
@@ -403,44 +435,67 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
         pin(ls[qb]);
       }
     };
-    // per fragment: its share of the softmax parts, the LDS read AHEAD fragments on, then its two
-    // MFMAs (query blocks 0 and 1) back to back.  (VALU work issued between two MFMAs that share
-    // an A operand, while the first still runs, corrupted the second's result on gfx950 in
-    // testing; back-to-back pairs and VALU work between pairs are exact.)
 #pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      if constexpr (DSOFT) {
+    for (int i = 0; i < NS; ++i) {
+      // LDS reads LEAD slots ahead: this phase's fragments, then the next phase's first ones
 #pragma unroll
-        for (int j = 0; j < 32 / NF; ++j) part(f * (32 / NF) + j);
+      for (int id = 0; id < NF; ++id)
+        if (first_use(BOTH, id) - LEAD == i) fr[id] = frag_at(DS, ka, va, id);
+      if constexpr (NX != 0) {
+#pragma unroll
+        for (int r = 0; r < npre(NBOTH); ++r)
+          if (NS + first_use(NBOTH, pre_id(NBOTH, r)) - LEAD == i) pre[r] = frag_at(NDS, nka, nva, pre_id(NBOTH, r));
       }
-      if (f + AHEAD < NF) fr[f + AHEAD] = frag(f + AHEAD);
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        if (DS && f < 8) {
-          if (f == 0) mfma_score0(Sn[qb], fr[f], qf[qb][f]);
-          else mfma_score(Sn[qb], fr[f], qf[qb][f & 7]);
-        } else {
-          const int g = max(f - 8 * DS, 0);
-          mfma_out(O[qb][g >> 1], fr[f], pp[qb][g & 1]);
+      // softmax parts, software-pipelined: a pair's pack + sum comes well after its exp2
+      if constexpr (DSOFT) {
+        if (BOTH) {
+          if ((i & 1) == 0) part(2 * (i >> 1));
+          else if (i >= 3) part(2 * ((i - 3) >> 1) + 1);
+        } else if ((i & 1) == 0) {
+          const int m = i >> 1;   // fragment m: exp2 of pairs 2m, 2m + 1, pack + sum of 2m - 2, 2m - 1
+          part(4 * m);
+          part(4 * m + 2);
+          if (m > 0) {
+            part(4 * m - 3);
+            part(4 * m - 1);
+          }
         }
       }
-      // operand hold: fragment f - 1 was last read two MFMAs ago; until here its registers may
-      // not be rewritten (by the interleaved VALU work or an LDS read)
-      if (f >= 1) hold(fr[f - 1]);
+      const int id = slot_id(BOTH, i), qb = slot_qb(BOTH, i);
+      if (DS && id < 8) {
+        if (id == 0) mfma_score0(Sn[qb], fr[id], qf[qb][0]);
+        else mfma_score(Sn[qb], fr[id], qf[qb][id & 7]);
+      } else {
+        const int g = max(id - 8 * DS, 0);
+        mfma_out(O[qb][g >> 1], fr[id], pp[qb][g & 1]);
+      }
+      // operand hold: a fragment last read two slots ago keeps its registers until here (no
+      // VALU or LDS write reaches them earlier)
+#pragma unroll
+      for (int id2 = 0; id2 < NF; ++id2)
+        if (last_use(BOTH, id2) == i - 2) hold(fr[id2]);
     }
     if constexpr (DSOFT) {
+      if (BOTH) {
+        part(31);
+      } else {
+        part(29);
+        part(31);
+      }
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) pc[qb][sl] = u32x4{pw[qb][sl][0], pw[qb][sl][1], pw[qb][sl][2], pw[qb][sl][3]};
     }
     // phase fence (32 wait states: a whole 8-pass MFMA) before the registers of the phase's last
-    // operands -- the last fragment, the previous probabilities -- are released, and before VALU
-    // reads scores written by a phase that ends on score MFMAs
+    // operands -- the fragments read in its last two slots, the previous probabilities -- are
+    // released, and before VALU reads scores written by this phase
+    constexpr int LA = BOTH ? 7 : NF - 1, LB = BOTH ? 15 : NF - 1;
     if constexpr (DPV)
-      asm volatile("s_nop 15\n\ts_nop 15" ::"v"(fr[NF - 1]), "v"(pp[0][0]), "v"(pp[0][1]), "v"(pp[1][0]), "v"(pp[1][1]));
+      asm volatile("s_nop 15\n\ts_nop 15" ::"v"(fr[LA]), "v"(fr[LB]), "v"(pp[0][0]), "v"(pp[0][1]), "v"(pp[1][0]),
+                   "v"(pp[1][1]));
     else
-      asm volatile("s_nop 15\n\ts_nop 15" ::"v"(fr[NF - 1]));
+      asm volatile("s_nop 15\n\ts_nop 15" ::"v"(fr[LA]), "v"(fr[LB]));
     if constexpr (DS) {   // (pins after the fence: the scores' readers stay below it)
       pin(Sn[0]);
       pin(Sn[1]);
@@ -477,14 +532,19 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
   };
   using Y = Flag<true>;
   using N = Flag<false>;
+  using NONE = std::integral_constant<int, 0>;
+  using NEXT_S = std::integral_constant<int, 1>;
+  using NEXT_PV = std::integral_constant<int, 2>;
+  using NEXT_BOTH = std::integral_constant<int, 3>;
 
   // stage j0: K tile j0 only
   st.load_k(j0);
   st.store_k(sK[0]);
   __syncthreads();
+  prefetch(Y{}, N{}, &sK[0][klane], nullptr);
   if (j0 + 1 < j1) st.load_k(j0 + 1);
   st.load_v(j0);
-  phase(Y{}, N{}, N{}, &sK[0][klane], nullptr);
+  phase(Y{}, N{}, N{}, &sK[0][klane], nullptr, NEXT_S{}, &sK[0][32 * KPITCH + klane], nullptr);
   take_scores();
   mask(j0, 0);
 #pragma unroll
@@ -494,7 +554,7 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
     for (int r = 0; r < 16; ++r) m = fmaxf(m, sc[qb][r]);
     m_use[qb] = half_max(m) * sl2;   // the scale is positive: the maximum of the raw scores
   }
-  phase(Y{}, N{}, Y{}, &sK[0][32 * KPITCH + klane], nullptr);
+  phase(Y{}, N{}, Y{}, &sK[0][32 * KPITCH + klane], nullptr, NONE{}, nullptr, nullptr);
   take_probs();
   take_scores();
   if (j0 + 1 < j1) st.store_k(sK[1]);
@@ -503,14 +563,15 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
   // stages j0 + 1 .. j1 - 1: K tile t, V tile t - 1
   for (int t = j0 + 1; t < j1; ++t) {
     const int b = (t - j0) & 1;
+    prefetch(Y{}, Y{}, &sK[b][klane], &sV[b][vlane]);
     if (t + 1 < j1) st.load_k(t + 1);
     st.load_v(t);
     // softmax of tile t - 1's second half (not the range's last tile: no mask)
-    phase(Y{}, Y{}, Y{}, &sK[b][klane], &sV[b][vlane]);
+    phase(Y{}, Y{}, Y{}, &sK[b][klane], &sV[b][vlane], NEXT_BOTH{}, &sK[b][32 * KPITCH + klane], &sV[b][64 + vlane]);
     take_probs();
     take_scores();
     mask(t, 0);
-    phase(Y{}, Y{}, Y{}, &sK[b][32 * KPITCH + klane], &sV[b][64 + vlane]);
+    phase(Y{}, Y{}, Y{}, &sK[b][32 * KPITCH + klane], &sV[b][64 + vlane], NONE{}, nullptr, nullptr);
     take_probs();
     take_scores();
     if (t + 1 < j1) st.store_k(sK[b ^ 1]);
@@ -520,10 +581,11 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
   // stage j1: V tile j1 - 1 only
   {
     const int b = (j1 - j0) & 1;
+    prefetch(N{}, Y{}, nullptr, &sV[b][vlane]);
     mask(j1 - 1, 1);
-    phase(N{}, Y{}, Y{}, nullptr, &sV[b][vlane]);
+    phase(N{}, Y{}, Y{}, nullptr, &sV[b][vlane], NEXT_PV{}, nullptr, &sV[b][64 + vlane]);
     take_probs();
-    phase(N{}, Y{}, N{}, nullptr, &sV[b][64 + vlane]);
+    phase(N{}, Y{}, N{}, nullptr, &sV[b][64 + vlane], NONE{}, nullptr, nullptr);
   }
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb)   // output fence
