@@ -73,10 +73,10 @@ def parse():
     ap.add_argument("--no-block", action="store_true", help="skip the config 1-4 extra lines")
     ap.add_argument("--lines", default="block,w4a16,lora,denoise,attention",
                     help="extra lines to run (comma list of block, w4a16, lora, denoise, attention)")
-    ap.add_argument("--pmc-pass", nargs="?", const="w4a4", default=None, choices=["w4a4", "w4a16"],
+    ap.add_argument("--pmc-pass", nargs="?", const="w4a4", default=None, choices=["w4a4", "w4a16", "attention"],
                     help="counter pass for rocprofv3: one copy kernel of known size, then 3 launches of the "
                          "config 1 ff.up W4A4 GEMM and 3 activation passes (w4a4), or of the config 2 ff.up "
-                         "W4A16 GEMM at M=2304 (w4a16)")
+                         "W4A16 GEMM at M=2304 (w4a16); attention: 3 calls of the config 3 block attention")
     return ap.parse_args()
 
 
@@ -440,6 +440,21 @@ def pmc_pass_w4a16(args, dev) -> int:
     return 0
 
 
+def pmc_pass_attention(args, dev) -> int:
+    """Counter pass of the config 3 block attention (T=4352, 48 q / 12 kv heads): 3 calls."""
+    import torch
+    from krea2_svdquant_amd.kernels.hip import ops
+    gen = torch.Generator(device=dev).manual_seed(6)
+    q = torch.randn(4352, 48, 128, device=dev, generator=gen).to(torch.bfloat16)
+    k = torch.randn(4352, 12, 128, device=dev, generator=gen).to(torch.bfloat16)
+    v = torch.randn(4352, 12, 128, device=dev, generator=gen).to(torch.bfloat16)
+    for _ in range(3):
+        ops.attention(q, k, v, 1.0 / math.sqrt(128))
+    torch.cuda.synchronize()
+    log("pmc pass done: 3 calls of svdq::attention (T=4352, 48 q / 12 kv heads)")
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -454,6 +469,8 @@ def main() -> int:
     m, k, n, r, g = args.m, args.k, args.n, args.rank, args.group
     if args.pmc_pass == "w4a16":
         return pmc_pass_w4a16(args, dev)
+    if args.pmc_pass == "attention":
+        return pmc_pass_attention(args, dev)
     log(f"device {torch.cuda.get_device_name(dev)}; building state M={m} K={k} N={n} r={r} g={g}")
     x, ds, prep = make_layer(n, k, m, r, g, dev, seed=1)
     opc = ops.OPERAND_NAMES[args.operand]
