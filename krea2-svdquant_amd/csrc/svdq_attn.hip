@@ -76,8 +76,9 @@ __device__ __forceinline__ float half_sum(float v) {
 //  * VALU reads a score at least 16 MFMAs after it was written, or behind a 32-wait-state fence;
 //  * the probabilities (VALU-written B operands) are read at least one phase later, behind such a
 //    fence;
-//  * a source fragment's registers are not rewritten until two more MFMAs have issued, and the two
-//    MFMAs that share a fragment issue back to back (no VALU work between them);
+//  * a source fragment's registers are not rewritten until two more MFMAs have issued;
+//  * no VALU work sits between two adjacent MFMAs that read the same fragment (a layout rule kept
+//    because a layout that broke it gave wrong results, cause unknown);
 //  * the output is read after out_fence (2 x 16 wait states).
 // (tests/test_attn_mfma_order.py checks the last two rules on the built library.)
 __device__ __forceinline__ void mfma_score0(f32x16& acc, u32x4 a, u32x4 b) {
@@ -372,11 +373,13 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
   //    MFMAs read the same fragment, so one softmax part goes before every MFMA;
   //  * with one kind, the two MFMAs of a fragment back to back (16 slots), the softmax parts
   //    before the first of each pair.
-  // (VALU work issued between two adjacent MFMAs that read the same fragment, while the first
-  // still ran, corrupted the second's result on gfx950 in testing; with no VALU work between them,
-  // or an MFMA of another fragment, they are exact.  One wave per SIMD stalls in order behind an
-  // MFMA that waits for the matrix pipe, so VALU work placed between MFMAs of different fragments
-  // hides under twice as much MFMA time as work placed only between pairs.)
+  // (An earlier layout that put softmax work between the two adjacent MFMAs of a fragment gave
+  // wrong results for the second of every pair, deterministically; the cause was not found -- the
+  // same instruction sequence in a standalone probe is exact -- so the kernel keeps to layouts
+  // that test exact: no VALU work between two adjacent MFMAs that read the same fragment.  One
+  // wave per SIMD stalls in order behind an MFMA that waits for the matrix pipe, so VALU work
+  // placed between MFMAs of different fragments hides under twice as much MFMA time as work
+  // placed only between pairs.)
   // A fragment is read from LDS LEAD slots before its first use; the ones used earlier than that
   // come from pre, read during the phase before (or by prefetch after a barrier).
   constexpr int LEAD = 6;

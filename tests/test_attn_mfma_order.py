@@ -5,9 +5,10 @@ VALU work between them, so the compiler's hazard recognizer does not guard the M
 The kernel's source keeps two rules, which this test checks in the gfx950 disassembly of our own
 build (llvm-objdump), in instruction order:
 
-* no VALU instruction between two consecutive MFMAs that read the same A operand (VALU work
-  issued there, while the first MFMA still ran, corrupted the second's result in testing; the
-  kernel issues each fragment's two MFMAs back to back);
+* no VALU instruction between two consecutive MFMAs that read the same A operand (an earlier
+  layout that put softmax work there gave wrong results for the second MFMA of every pair; the
+  cause was not found -- the same sequence in a standalone probe is exact -- so the kernel keeps
+  to the layouts that test exact);
 * no instruction writes an MFMA's A or B source registers (VALU, LDS or global load destination)
   until two more MFMAs have issued or 32 wait states of `s_nop` have passed (the kernel holds each
   fragment two MFMAs past its last use and ends each phase with a 32-wait-state fence).
