@@ -339,14 +339,18 @@ def denoise_line(args, dev) -> dict:
     ms_fused_sib, _ = run(True, True)
     ms, lat = run(False)
     same_sib = bool(torch.equal(lat, lat_sib))
-    # the same steps with the attention on PyTorch's fused SDPA kernels, for comparison
+    # the same steps with the attention on PyTorch's fused SDPA kernels, and with the norms in
+    # torch as well (config 3 as BASELINE states it: attention and norms in PyTorch-ROCm)
     from krea2_svdquant_amd.runtime import krea2_standin as ks
-    ks.ATTENTION = "sdpa"
     try:
+        ks.ATTENTION = "sdpa"
         model.denoise_step(text, latent, dt)
         ms_sdpa, _ = run(False)
+        ks.NORMS = "torch"
+        model.denoise_step(text, latent, dt)
+        ms_torch_glue, _ = run(False)
     finally:
-        ks.ATTENTION = "hip"
+        ks.ATTENTION, ks.NORMS = "hip", "hip"
     # one more step with HIP events around every quantized linear: their share of the step
     pairs = []
 
@@ -370,6 +374,7 @@ def denoise_line(args, dev) -> dict:
             "ms_per_denoise_step_concurrent_siblings": round(ms_sib, 3),
             "ms_per_denoise_step_fused_epilogues_concurrent_siblings": round(ms_fused_sib, 3),
             "ms_per_denoise_step_sdpa_attention": round(ms_sdpa, 3),
+            "ms_per_denoise_step_torch_attention_and_norms": round(ms_torch_glue, 3),
             "concurrent_siblings_bit_identical": same_sib,
             "linears_ms_per_step": round(lin_ms, 3), "rest_ms_per_step": round(ms - lin_ms, 3),
             "tokens": 4352, "blocks": dims.layers, "peak_hbm_GB": round(hbm_gb, 1), "finite": finite,
@@ -377,7 +382,9 @@ def denoise_line(args, dev) -> dict:
                     "backend; attention (48 q / 12 kv heads, svdq::attention), adaptive RMS norms, per-head "
                     "norm + rotary embedding on gfx950 kernels, gates and residuals in PyTorch-ROCm "
                     "(ms_per_denoise_step; ms_per_denoise_step_sdpa_attention: the attention on PyTorch's "
-                    "fused SDPA kernels instead; with the sigmoid gate, SwiGLU product and "
+                    "fused SDPA kernels instead; ms_per_denoise_step_torch_attention_and_norms: attention and "
+                    "norms both in PyTorch-ROCm, the configuration as BASELINE states it; with the sigmoid gate, "
+                    "SwiGLU product and "
                     "gated residuals fused into the stores of to_gate, ff.up, to_out.0 and ff.down instead: "
                     "ms_per_denoise_step_fused_epilogues; *_concurrent_siblings: the linears that read the same "
                     "input (to_q, to_gate, to_k, to_v; ff.up, ff.gate) issued on side streams); random-init "

@@ -23,10 +23,10 @@ and the rotary embedding half by half: one bf16 rounding per fused op, fewer pas
 A denoise step is the 28 blocks over [text | latent] tokens followed by the Euler update of the
 latent tokens, ``latent += dt * velocity``.  On the GPU every quantized linear runs on the gfx950
 kernels (``SVDQuantLinear``), and so do the adaptive RMS norms and the per-head norm + rotary
-embedding (``svdq::rms_norm_modulate``, ``svdq::head_rms_rope``: one pass each) and the attention
-(``svdq::attention``, a flash-attention forward; ``ATTENTION = "sdpa"`` selects PyTorch's fused SDPA
-kernels instead); the remaining elementwise work runs in PyTorch-ROCm (on the CPU everything is
-torch).  With
+embedding (``svdq::rms_norm_modulate``, ``svdq::head_rms_rope``: one pass each; ``NORMS = "torch"``
+selects the torch ops) and the attention (``svdq::attention``, a flash-attention forward;
+``ATTENTION = "sdpa"`` selects PyTorch's fused SDPA kernels); the remaining elementwise work runs in
+PyTorch-ROCm (on the CPU everything is torch).  With
 ``fused=True`` the sigmoid gate, the SwiGLU product and the two gated residual adds run inside
 the stores of to_gate, ff.up, to_out.0 and ff.down instead.
 """
@@ -100,19 +100,23 @@ def rms_norm(x: Tensor, eps: float = 1e-6, weight: Optional[Tensor] = None) -> T
     return F.rms_norm(x, (x.shape[-1],), weight=weight, eps=eps)
 
 
+NORMS = "hip"   # the GPU norms: "hip" (the gfx950 kernels) or "torch" (the torch ops, as on the CPU)
+
+
 def norm_modulate(x: Tensor, scale: Tensor, shift: Tensor, eps: float = 1e-6) -> Tensor:
     """The block's adaptive RMS norm ``rms_norm(x) * (1 + scale) + shift``: one gfx950 kernel on
-    the GPU (``svdq::rms_norm_modulate``), the torch ops elsewhere."""
+    the GPU (``svdq::rms_norm_modulate``) unless ``NORMS`` is "torch", the torch ops elsewhere."""
     w = 1 + scale
-    if x.is_cuda:
+    if x.is_cuda and NORMS == "hip":
         return hip_ops.rms_norm_modulate(x, w, shift, eps)
     return rms_norm(x, eps, weight=w) + shift
 
 
 def head_norm_rope(t: Tensor, cos: Tensor, sin: Tensor, eps: float = 1e-6) -> Tensor:
     """Per-head RMS norm of q or k [T, heads, head_dim] and the rotary embedding: one gfx950
-    kernel on the GPU for head_dim 128 (``svdq::head_rms_rope``), the torch ops elsewhere."""
-    if t.is_cuda:
+    kernel on the GPU for head_dim 128 (``svdq::head_rms_rope``) unless ``NORMS`` is "torch",
+    the torch ops elsewhere."""
+    if t.is_cuda and NORMS == "hip":
         return hip_ops.head_rms_rope(t, cos, sin, eps)
     return apply_rope(rms_norm(t, eps), cos, sin)
 
