@@ -243,13 +243,22 @@ def block_layers(args, dev, m: int, mode: str, seed0: int) -> dict:
         for group in BLOCK_ORDER:
             x, fns = layers[group[0]][0], [fwd(nm) for nm in group]
             run_concurrent(x, fns) if concurrent else [f(x) for f in fns]
+
+    def block_grouped():   # W4A4: the siblings' GEMMs as one launch
+        for group in BLOCK_ORDER:
+            backend.forward_prepared_siblings(layers[group[0]][0], [layers[nm][1] for nm in group])
     for c in (False, True):
         block(c)
     ms_seq = time_avg(lambda: block(False), 10)
     ms_conc = time_avg(lambda: block(True), 10)
+    ms_grp = None
+    if mode == "w4a4":
+        block_grouped()
+        ms_grp = time_avg(block_grouped, 10)
     del layers
     torch.cuda.empty_cache()
-    return {"per": per, "total": sum(per.values()), "ops": ops_total, "seq": ms_seq, "conc": ms_conc}
+    return {"per": per, "total": sum(per.values()), "ops": ops_total, "seq": ms_seq, "conc": ms_conc,
+            "grp": ms_grp}
 
 
 def block_line(args, dev) -> dict:
@@ -262,11 +271,12 @@ def block_line(args, dev) -> dict:
             "linears_ms_per_denoise_step_28_blocks": round(28 * total, 3),
             "ms_per_block_in_order": round(b["seq"], 4),
             "ms_per_block_in_order_concurrent_siblings": round(b["conc"], 4),
+            "ms_per_block_in_order_grouped_siblings": round(b["grp"], 4),
             "note": "W4A4 linears only (M=4096, no text tokens, no attention / norms): the part of the "
                     "denoise step this backend replaces; ms_per_block_linears = each layer timed alone, "
                     "summed; *_in_order: the 8 layers back to back in block order, the siblings that read "
-                    "the same input (to_q, to_gate, to_k, to_v; ff.up, ff.gate) one after another or "
-                    "concurrently on side streams"}
+                    "the same input (to_q, to_gate, to_k, to_v; ff.up, ff.gate) one after another, "
+                    "concurrently on side streams, or with their GEMMs as one launch"}
 
 
 def w4a16_line(args, dev) -> dict:
@@ -319,14 +329,13 @@ def denoise_line(args, dev) -> dict:
     text = torch.randn(256, dims.hidden, device=dev, generator=gen).to(torch.bfloat16)
     latent = torch.randn(4096, dims.hidden, device=dev, generator=gen).to(torch.bfloat16)
     steps, dt = 8, -1.0 / 8
-    lat = model.denoise_step(text, latent, dt)      # warm-up: builds every layer's kernel operands
-    lat = model.denoise_step(text, latent, dt, fused=True)
-    lat = model.denoise_step(text, latent, dt, siblings=True)
-    lat = model.denoise_step(text, latent, dt, fused=True, siblings=True)
+    for fused in (False, True):                     # warm-up: builds every layer's kernel operands
+        for siblings in ("grouped", False, True):
+            lat = model.denoise_step(text, latent, dt, fused=fused, siblings=siblings)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    def run(fused: bool, siblings: bool = False) -> tuple[float, "torch.Tensor"]:
+    def run(fused: bool, siblings: bool | str = "grouped") -> tuple[float, "torch.Tensor"]:
         lat = latent
         a.record()
         for _ in range(steps):
@@ -337,8 +346,11 @@ def denoise_line(args, dev) -> dict:
     ms_fused, _ = run(True)
     ms_sib, lat_sib = run(False, True)
     ms_fused_sib, _ = run(True, True)
+    ms_seq, lat_seq = run(False, False)
+    ms_fused_seq, _ = run(True, False)
     ms, lat = run(False)
     same_sib = bool(torch.equal(lat, lat_sib))
+    same_seq = bool(torch.equal(lat, lat_seq))
     # the same steps with the attention on PyTorch's fused SDPA kernels, and with the norms in
     # torch as well (config 3 as BASELINE states it: attention and norms in PyTorch-ROCm)
     from krea2_svdquant_amd.runtime import krea2_standin as ks
@@ -375,7 +387,9 @@ def denoise_line(args, dev) -> dict:
             "ms_per_denoise_step_fused_epilogues_concurrent_siblings": round(ms_fused_sib, 3),
             "ms_per_denoise_step_sdpa_attention": round(ms_sdpa, 3),
             "ms_per_denoise_step_torch_attention_and_norms": round(ms_torch_glue, 3),
-            "concurrent_siblings_bit_identical": same_sib,
+            "ms_per_denoise_step_sequential_siblings": round(ms_seq, 3),
+            "ms_per_denoise_step_fused_epilogues_sequential_siblings": round(ms_fused_seq, 3),
+            "concurrent_siblings_bit_identical": same_sib, "sequential_siblings_bit_identical": same_seq,
             "linears_ms_per_step": round(lin_ms, 3), "rest_ms_per_step": round(ms - lin_ms, 3),
             "tokens": 4352, "blocks": dims.layers, "peak_hbm_GB": round(hbm_gb, 1), "finite": finite,
             "note": "stand-in Krea-2 denoiser (diffusers is absent): 28 blocks, 8 W4A4 linears each on this "
@@ -386,8 +400,9 @@ def denoise_line(args, dev) -> dict:
                     "norms both in PyTorch-ROCm, the configuration as BASELINE states it; with the sigmoid gate, "
                     "SwiGLU product and "
                     "gated residuals fused into the stores of to_gate, ff.up, to_out.0 and ff.down instead: "
-                    "ms_per_denoise_step_fused_epilogues; *_concurrent_siblings: the linears that read the same "
-                    "input (to_q, to_gate, to_k, to_v; ff.up, ff.gate) issued on side streams); random-init "
+                    "ms_per_denoise_step_fused_epilogues; the linears that read the same input (to_q, to_gate, "
+                    "to_k, to_v; ff.up, ff.gate) run their GEMMs as one launch (svdq_w4a4_gemm_siblings), or "
+                    "*_sequential_siblings: one after another, *_concurrent_siblings: on side streams); random-init "
                     "quantized weights, N(0,1) tokens; HIP "
                     "events around 8 Euler steps after one warm-up step of each; linears_ms_per_step: HIP events "
                     "around each linear of one forward"}

@@ -206,6 +206,34 @@ int svdq_w4a16_gemm_epi(const void* xhat, int64_t ldxh, const void* qw, const vo
                         int64_t ldy, int out_f32, int epi, const void* aux, int64_t ldaux, const void* vec,
                         hipStream_t stream);
 
+/* Sibling linears in one launch: up to SVDQ_MAX_SIBLINGS W4A4 GEMMs over the same activation rows
+ * (same M, K and group; each layer with its own operands, scales, low-rank factors, bias and
+ * output), e.g. attn.to_q / to_k / to_v / to_gate or ff.gate / ff.up of one block.  The reference
+ * calls such layers one after another, each through SVDQuantLinear.forward
+ * (runtime/linear.py:156-161; the layer names are in README.md:41-51); each output here equals
+ * svdq_w4a4_gemm's for that layer bit for bit.  With SVDQ_OPERAND_E3M2, group 64 or 128 and
+ * K % 512 == 0 the layers' output tiles run in one launch, so that the tiles of small layers
+ * and the last partial round of workgroups of each layer share the CUs; otherwise the layers are
+ * launched one after another on `stream`.
+ *   layers[i]: the per-layer arguments of svdq_w4a4_gemm (qa and sxp from that layer's own
+ *              svdq_act_quant: the smoothing differs per layer), with out_f32 = 0 or 1 for all. */
+#define SVDQ_MAX_SIBLINGS 4
+typedef struct svdq_w4a4_sibling {
+  const void* qa;
+  const void* sxp;
+  const void* qwe;
+  const void* swp;
+  const void* mid;
+  const void* l1cat;
+  int RTp;
+  const void* bias;
+  int N;
+  void* y;
+  int64_t ldy;
+} svdq_w4a4_sibling;
+int svdq_w4a4_gemm_siblings(const svdq_w4a4_sibling* layers, int count, int operand, int M, int K, int group,
+                            int out_f32, hipStream_t stream);
+
 /* Normalizations of the stand-in Krea-2 block around its quantized linears.  No counterpart in
  * the reference: its blocks run in diffusers (reference src/krea2_svdquant/transformer.py:46-59),
  * whose internals it does not contain.  bf16 in and out, float32 math, one pass over the rows.

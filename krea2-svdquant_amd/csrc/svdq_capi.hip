@@ -336,40 +336,78 @@ int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe
                             SVDQ_EPI_NONE, nullptr, 0, nullptr, stream);
 }
 
-int svdq_w4a4_gemm_epi(const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
-                       const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
-                       void* y, int64_t ldy, int out_f32, int epi, const void* aux, int64_t ldaux, const void* vec,
-                       hipStream_t stream) {
-  const void* sw = swp;
-  if (int e = gemm_common_checks("w4a4_gemm", qwe, sw, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32))
-    return e;
-  if (int e = epi_checks("w4a4_gemm", epi, aux, ldaux, vec, N, out_f32)) return e;
-  if (!qa || !sxp) return fail(SVDQ_ERR_ARG, "w4a4_gemm: null pointer");
+// Checks of one W4A4 layer's arguments and its kernel parameters (no fused op yet).
+static int w4a4_layer(const char* who, const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
+                      const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                      void* y, int64_t ldy, int out_f32, svdq::GemmParams& p) {
+  if (int e = gemm_common_checks(who, qwe, swp, mid, l1cat, RTp, M, N, K, group, y, ldy, out_f32)) return e;
+  if (!qa || !sxp) return fail(SVDQ_ERR_ARG, "%s: null pointer", who);
   if (operand != SVDQ_OPERAND_E4M3 && operand != SVDQ_OPERAND_I8 && operand != SVDQ_OPERAND_E3M2)
-    return fail(SVDQ_ERR_ARG, "w4a4_gemm: operand format %d", operand);
+    return fail(SVDQ_ERR_ARG, "%s: operand format %d", who, operand);
   if (!aligned16(qa) || !aligned16(qwe) || reinterpret_cast<uintptr_t>(sxp) % 4 || reinterpret_cast<uintptr_t>(swp) % 4)
-    return fail(SVDQ_ERR_ALIGN, "w4a4_gemm: qa, qwe must be 16-byte aligned, sxp, swp 4-byte aligned");
+    return fail(SVDQ_ERR_ALIGN, "%s: qa, qwe must be 16-byte aligned, sxp, swp 4-byte aligned", who);
   // The 8-bit kernels address qa and qwe with 32-bit byte offsets (the e3m2 kernel with 64-bit
   // plane bases and 32-bit row offsets).
   if (operand != SVDQ_OPERAND_E3M2 && fast_group(group) &&
       ((int64_t)M * K > INT32_MAX || (int64_t)N * K > INT32_MAX || (int64_t)M * (K / group) * 4 > INT32_MAX ||
        (int64_t)N * (K / group) * 4 > INT32_MAX))
-    return fail(SVDQ_ERR_SHAPE, "w4a4_gemm: M*K=%lld or N*K=%lld exceeds 2^31-1 bytes; split the call",
+    return fail(SVDQ_ERR_SHAPE, "%s: M*K=%lld or N*K=%lld exceeds 2^31-1 bytes; split the call", who,
                 (long long)M * K, (long long)N * K);
-  svdq::GemmParams p = gemm_params(nullptr, sw, mid, l1cat, RTp, bias, M, N, K, y, ldy);
+  if (!fast_group(group) && operand != SVDQ_OPERAND_I8)
+    return fail(SVDQ_ERR_UNSUPPORTED, "%s: group size %d has int8 operands only (SVDQ_OPERAND_I8)", who, group);
+  p = gemm_params(nullptr, swp, mid, l1cat, RTp, bias, M, N, K, y, ldy);
   p.qwe = static_cast<const uint8_t*>(qwe);
   p.qa = static_cast<const uint8_t*>(qa);
   p.sxp = static_cast<const uint32_t*>(sxp);
   p.swp = static_cast<const uint32_t*>(swp);
+  return SVDQ_OK;
+}
+
+static hipError_t launch_w4a4_layer(const svdq::GemmParams& p, int group, int operand, int out_f32, hipStream_t stream) {
+  if (!fast_group(group)) return svdq::launch_w4a4_any_group(p, group, out_f32 == 1, stream);
+  return svdq::launch_w4a4(p, group, operand, out_f32 == 1, stream);
+}
+
+int svdq_w4a4_gemm_epi(const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
+                       const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
+                       void* y, int64_t ldy, int out_f32, int epi, const void* aux, int64_t ldaux, const void* vec,
+                       hipStream_t stream) {
+  svdq::GemmParams p;
+  if (int e = w4a4_layer("w4a4_gemm", qa, operand, sxp, qwe, swp, mid, l1cat, RTp, bias, M, N, K, group, y, ldy,
+                         out_f32, p))
+    return e;
+  if (int e = epi_checks("w4a4_gemm", epi, aux, ldaux, vec, N, out_f32)) return e;
   set_epi(p, epi, aux, ldaux, vec);
-  if (!fast_group(group)) {
-    if (operand != SVDQ_OPERAND_I8)
-      return fail(SVDQ_ERR_UNSUPPORTED, "w4a4_gemm: group size %d has int8 operands only (SVDQ_OPERAND_I8)", group);
-    if (epi != SVDQ_EPI_NONE)
-      return fail(SVDQ_ERR_UNSUPPORTED, "w4a4_gemm: group size %d has no fused epilogue ops", group);
-    return launched(svdq::launch_w4a4_any_group(p, group, out_f32 == 1, stream), "w4a4_gemm (any group)");
+  if (!fast_group(group) && epi != SVDQ_EPI_NONE)
+    return fail(SVDQ_ERR_UNSUPPORTED, "w4a4_gemm: group size %d has no fused epilogue ops", group);
+  return launched(launch_w4a4_layer(p, group, operand, out_f32, stream),
+                  fast_group(group) ? "w4a4_gemm" : "w4a4_gemm (any group)");
+}
+
+int svdq_w4a4_gemm_siblings(const svdq_w4a4_sibling* layers, int count, int operand, int M, int K, int group,
+                            int out_f32, hipStream_t stream) {
+  if (!layers) return fail(SVDQ_ERR_ARG, "w4a4_gemm_siblings: null layer array");
+  if (count < 1 || count > SVDQ_MAX_SIBLINGS)
+    return fail(SVDQ_ERR_ARG, "w4a4_gemm_siblings: count=%d, must be 1..%d", count, SVDQ_MAX_SIBLINGS);
+  svdq::GemmSiblings gs{};
+  gs.count = count;
+  int tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    const svdq_w4a4_sibling& l = layers[i];
+    if (int e = w4a4_layer("w4a4_gemm_siblings", l.qa, operand, l.sxp, l.qwe, l.swp, l.mid, l.l1cat, l.RTp, l.bias,
+                           M, l.N, K, group, l.y, l.ldy, out_f32, gs.layer[i]))
+      return e;
+    gs.tile0[i] = tiles;
+    tiles += ((M + 255) / 256) * ((l.N + 127) / 128);
   }
-  return launched(svdq::launch_w4a4(p, group, operand, out_f32 == 1, stream), "w4a4_gemm");
+  gs.tile0[count] = tiles;
+  if (operand == SVDQ_OPERAND_E3M2 && fast_group(group) && K % 512 == 0)
+    return launched(svdq::launch_w4a4_siblings(gs, group, out_f32 == 1, stream), "w4a4_gemm_siblings");
+  // other formats, groups and K: one launch per layer, in order
+  for (int i = 0; i < count; ++i)
+    if (int e = launched(launch_w4a4_layer(gs.layer[i], group, operand, out_f32, stream), "w4a4_gemm_siblings"))
+      return e;
+  return SVDQ_OK;
 }
 
 int svdq_rms_norm_modulate(const void* x, int64_t ldx, const void* w, const void* shift, int T, int H, float eps,

@@ -629,7 +629,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
 // stage is peeled (no DMA, the epilogue's prefetch), and the DMA sources are wave-uniform
 // pointers advanced one stage at a time.  Other K take the general loop.
 template <int G, bool OUT_F32, bool FULL, bool EPI = false>
-__global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
+__device__ __forceinline__ void w4a4_e3m2_tile(const GemmParams& p, int bm, int bn) {
   constexpr int TBM = 256, TBN = 128, NBUF = 2;
   constexpr int KB = 256;                     // K columns per pipeline stage
   constexpr int KT = KB / 64;                 // k-steps per stage
@@ -653,9 +653,6 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
-  int bm, bn;
-  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
   const int m0 = bm * TBM, n0 = bn * TBN;
   const int K = p.K, ngroups = K / G, nkt = K / 64, nstages = (K + KB - 1) / KB, H = 2 * ngroups;
   const int Mp = (p.M + 1) & ~1, Np = (p.N + 1) & ~1;
@@ -996,6 +993,35 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
   unrotate_acc(acc);
   epilogue<OUT_F32, EPI>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[lbuf][0] + wave * 4096,
                     epi_lds ? &sAQ[lbuf ^ 1][0] : nullptr, epi_lds ? &sBQ[lbuf ^ 1][0] : nullptr, 64 * wm, 64 * wn);
+}
+
+template <int G, bool OUT_F32, bool FULL, bool EPI = false>
+__global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
+  const int nbm = (p.M + 255) / 256, nbn = (p.N + 127) / 128;
+  int bm, bn;
+  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
+  w4a4_e3m2_tile<G, OUT_F32, FULL, EPI>(p, bm, bn);
+}
+
+// Sibling layers (same rows M, same K and group) in one launch: the layers' 256 x 128 tiles are
+// numbered back to back (layer i from tile0[i]), that order is spread over the XCDs as in
+// tile_coords, and each workgroup runs one tile of one layer with that layer's parameters.  The
+// tiles are the single-layer kernel's, so every output is bit-identical to a launch per layer;
+// what changes is that the layers' tiles share the rounds of workgroups over the CUs.
+template <int G, bool OUT_F32>
+__global__ void __launch_bounds__(512, 1) w4a4_e3m2_siblings_kernel(GemmSiblings gs) {
+  const int total = gs.tile0[gs.count];
+  int lin = blockIdx.x;
+  if (total % 8 == 0) lin = (lin % 8) * (total / 8) + lin / 8;
+  int i = 0;
+#pragma unroll
+  for (int c = 1; c < MAX_SIBLINGS; ++c) i += (c < gs.count && lin >= gs.tile0[c]) ? 1 : 0;
+  i = __builtin_amdgcn_readfirstlane(i);
+  const GemmParams& p = gs.layer[i];
+  const int nbm = (p.M + 255) / 256, nbn = (p.N + 127) / 128;
+  int bm, bn;
+  tile_of_linear(lin - gs.tile0[i], nbm, nbn, 4, bm, bn);
+  w4a4_e3m2_tile<G, OUT_F32, true>(p, bm, bn);
 }
 
 // Weight operand of the W4A4 GEMM, once per layer: each packed dword (8 nibbles, k0 in the
@@ -1564,6 +1590,29 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
 #undef SVDQ_E3M2
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_w4a4_siblings(const GemmSiblings& gs, int G, bool out_f32, hipStream_t st) {
+  if (gs.count < 1 || gs.count > MAX_SIBLINGS) return hipErrorInvalidValue;
+  const int K = gs.layer[0].K, M = gs.layer[0].M;
+  int tiles = 0;
+  for (int i = 0; i < gs.count; ++i) {
+    const GemmParams& p = gs.layer[i];
+    if (p.K != K || p.M != M || p.epi || gs.tile0[i] != tiles) return hipErrorInvalidValue;
+    tiles += ((p.M + 255) / 256) * ((p.N + 127) / 128);
+  }
+  if (gs.tile0[gs.count] != tiles || K % 512) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)tiles);
+  if (G == 64) {
+    if (out_f32) w4a4_e3m2_siblings_kernel<64, true><<<grid, 512, 0, st>>>(gs);
+    else w4a4_e3m2_siblings_kernel<64, false><<<grid, 512, 0, st>>>(gs);
+  } else if (G == 128) {
+    if (out_f32) w4a4_e3m2_siblings_kernel<128, true><<<grid, 512, 0, st>>>(gs);
+    else w4a4_e3m2_siblings_kernel<128, false><<<grid, 512, 0, st>>>(gs);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, int n, int ngroups, int mode, hipStream_t st) {

@@ -52,6 +52,16 @@ struct GemmParams {
   int aux_vec;              // 1: aux (and evec) take 16-byte loads (aligned, ldaux % 8 == 0)
 };
 
+// Up to MAX_SIBLINGS W4A4 layers over the same activation rows (same M, K and group size), run
+// as one launch of the e3m2 kernel; tile0[i] = the first tile of layer i (256 x 128 tiles,
+// prefix sums, tile0[count] = all tiles).  No fused store ops.
+constexpr int MAX_SIBLINGS = 4;
+struct GemmSiblings {
+  GemmParams layer[MAX_SIBLINGS];
+  int count;
+  int tile0[MAX_SIBLINGS + 1];
+};
+
 int act_splits(int M, int K, int G);
 // oper: 0 = no codes (x_hat only), 1 = e4m3 operand codes, 2 = int8 16*q operand codes, 3 = e3m2;
 // nt: column tiles of the down projections from p.t0 (at most 4); with p.t0 > 0 the launch computes
@@ -68,6 +78,8 @@ hipError_t launch_quant_any_group(const uint16_t* xhat, long ldxh, int M, int K,
 // mode: 0 = e4m3 operands on the FP8 MFMA, 1 = int8 operands on the INT8 MFMA, 2 = e3m2 planar
 // operands on the FP6 MFMA
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st);
+// e3m2 operands, G = 64 or 128, K % 512 == 0, every layer without fused store ops
+hipError_t launch_w4a4_siblings(const GemmSiblings& gs, int G, bool out_f32, hipStream_t st);
 hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, int n, int ngroups, int mode, hipStream_t st);
 // mode: 0 = e4m3, 1 = int8 16*q (both [N, K] bytes), 2 = e3m2 planar ((N + 1) & ~1 rows, K * 3 / 4
 // bytes per row)

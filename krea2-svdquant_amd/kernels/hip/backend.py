@@ -228,6 +228,42 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
     return y.reshape(*lead, prep.n)
 
 
+def forward_prepared_siblings(x: Tensor, preps: Sequence[PreparedLayer], *, out_f32: bool = False,
+                              exact_div: bool = False, operand: str = "e3m2") -> list[Tensor]:
+    """W4A4 forwards of sibling layers (same input ``x``, same K and group size) on prepared
+    operands: one activation pass per layer (each layer has its own smoothing), then the layers'
+    GEMMs as one launch (``svdq::w4a4_gemm_siblings``).  Every output is bit-identical to
+    ``forward_prepared(x, prep)`` of its layer."""
+    if not x.is_cuda:
+        raise RuntimeError("HIP gfx950 backend needs a GPU tensor")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"HIP gfx950 backend takes bfloat16 activations, got {x.dtype}")
+    if not 1 <= len(preps) <= ops.lib.SVDQ_MAX_SIBLINGS:
+        raise ValueError(f"1..{ops.lib.SVDQ_MAX_SIBLINGS} sibling layers, got {len(preps)}")
+    p0 = preps[0]
+    for p in preps:
+        if p.device != x.device:
+            raise ValueError(f"activation on {x.device}, layer on {p.device}")
+        if (p.kp, p.group_size) != (p0.kp, p0.group_size):
+            raise ValueError("sibling layers need the same padded in_features and group size")
+    if p0.group_size not in FAST_GROUPS:
+        raise ValueError(f"sibling launch needs group size 64 or 128, got {p0.group_size}")
+    if operand not in ops.OPERAND_NAMES:
+        raise ValueError(f"operand must be 'e4m3', 'e3m2' or 'i8', got {operand!r}")
+    opc = ops.OPERAND_NAMES[operand]
+    x2, lead = _flatten(x)
+    if x2.shape[1] > p0.kp:
+        raise ValueError(f"activation K={x2.shape[1]} exceeds packed weight K={p0.kp}")
+    if x2.shape[1] != p0.kp:
+        x2 = _pad_cols(x2, p0.kp)
+    acts = [ops.act_quant(x2, p.srs, p.l2, p.lora_down, p.lora_mult, p.group_size, p.rtp, opc, False, False,
+                          exact_div, True) for p in preps]
+    ys = ops.w4a4_gemm_siblings([a[0] for a in acts], [a[1] for a in acts], [p.weight_operand(opc) for p in preps],
+                                [p.weight_scale_pairs(opc) for p in preps], [a[4] for a in acts],
+                                [p.l1cat for p in preps], [p.bias for p in preps], p0.group_size, opc, out_f32)
+    return [y.reshape(*lead, p.n) for y, p in zip(ys, preps)]
+
+
 # Prepared operands of the stateless entry, per state object: id(state) -> (key, PreparedLayer).  An
 # entry is dropped when its state is garbage-collected and replaced when any buffer of the state
 # or of an adapter is swapped or edited in place (storage and version counter in the key) or an

@@ -33,6 +33,9 @@ SVDQ_EPI_MUL_SIGMOID = 1
 SVDQ_EPI_SILU_MUL = 2
 SVDQ_EPI_RESIDUAL_GATE = 3
 
+# sibling layers of one svdq_w4a4_gemm_siblings call (SVDQ_MAX_SIBLINGS)
+SVDQ_MAX_SIBLINGS = 4
+
 STATUS = {0: "SVDQ_OK", -1: "SVDQ_ERR_ARG", -2: "SVDQ_ERR_SHAPE", -3: "SVDQ_ERR_ALIGN",
           -4: "SVDQ_ERR_UNSUPPORTED", -5: "SVDQ_ERR_LAUNCH"}
 
@@ -40,6 +43,13 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _L = ctypes.c_int64
 _U = ctypes.c_uint
+
+
+class W4A4Sibling(ctypes.Structure):
+    """``svdq_w4a4_sibling``: one layer of ``svdq_w4a4_gemm_siblings``."""
+    _fields_ = [("qa", _P), ("sxp", _P), ("qwe", _P), ("swp", _P), ("mid", _P), ("l1cat", _P), ("RTp", _I),
+                ("bias", _P), ("N", _I), ("y", _P), ("ldy", _L)]
+
 
 # name -> (restype, argtypes); the exact set of symbols include/svdq_gfx950.h declares.
 SIGNATURES = {
@@ -60,6 +70,7 @@ SIGNATURES = {
                                 _I, _P, _L, _P, _P]),
     "svdq_w4a16_gemm_epi": (_I, [_P, _L, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I,
                                  _I, _P, _L, _P, _P]),
+    "svdq_w4a4_gemm_siblings": (_I, [ctypes.POINTER(W4A4Sibling), _I, _I, _I, _I, _I, _I, _P]),
     "svdq_rms_norm_modulate": (_I, [_P, _L, _P, _P, _I, _I, ctypes.c_float, _P, _L, _P]),
     "svdq_head_rms_rope": (_I, [_P, _I, _I, _P, _P, _L, ctypes.c_float, _P, _P]),
     "svdq_attention_workspace": (_L, [_I, _I]),

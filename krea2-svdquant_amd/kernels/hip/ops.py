@@ -277,21 +277,9 @@ def w4a4_gemm(qa: Tensor, sx_pairs: Tensor, weight_operand: Tensor, weight_scale
     """
     _need(qa.is_cuda, RuntimeError, "svdq::w4a4_gemm needs GPU tensors")
     dev = qa.device
-    _check_dev("qa", qa, dev, torch.uint8)
-    _check_dev("sx_pairs", sx_pairs, dev, torch.int32)
-    _need(sx_pairs.dim() == 2, ValueError, "sx_pairs must be [K/G, M]")
     _need(operand in _OPERANDS, ValueError, f"operand={operand}")
-    m, k = sx_pairs.shape[1], sx_pairs.shape[0] * group_size
-    _need(tuple(qa.shape) == _operand_shape(m, k, operand), ValueError,
-          f"qa must be {_operand_shape(m, k, operand)} for M={m}, K={k}, got {tuple(qa.shape)}")
-    _check_dev("weight_operand", weight_operand, dev, torch.uint8)
-    _check_dev("weight_scale_pairs", weight_scale_pairs, dev, torch.int32)
-    _need(weight_scale_pairs.dim() == 2 and weight_scale_pairs.shape[0] == k // group_size, ValueError,
-          f"weight_scale_pairs must be [{k // group_size}, N], got {tuple(weight_scale_pairs.shape)}")
-    n = weight_scale_pairs.shape[1]
-    _need(tuple(weight_operand.shape) == _operand_shape(n, k, operand), ValueError,
-          f"weight_operand must be {_operand_shape(n, k, operand)}, got {tuple(weight_operand.shape)}")
-    _check_epilogue(mid, l1cat, bias, m, n, dev)
+    m, n, k = _check_w4a4_operands(qa, sx_pairs, weight_operand, weight_scale_pairs, mid, l1cat, bias, group_size,
+                                   operand, dev)
     _check_epi(epi, aux, vec, m, n, out_f32, dev)
     y = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
     lib.call("svdq_w4a4_gemm_epi", _vp(qa), operand, _vp(sx_pairs), _vp(weight_operand), _vp(weight_scale_pairs),
@@ -305,6 +293,62 @@ def _(qa, sx_pairs, weight_operand, weight_scale_pairs, mid, l1cat, bias, group_
       epi=0, aux=None, vec=None):
     return qa.new_empty((sx_pairs.shape[1], weight_scale_pairs.shape[1]),
                         dtype=torch.float32 if out_f32 else torch.bfloat16)
+
+
+def _check_w4a4_operands(qa: Tensor, sx_pairs: Tensor, weight_operand: Tensor, weight_scale_pairs: Tensor,
+                         mid: Tensor, l1cat: Tensor, bias: Optional[Tensor], group_size: int, operand: int,
+                         dev: torch.device, who: str = "") -> tuple[int, int, int]:
+    """Checks of one W4A4 layer's GEMM operands; returns (M, N, K)."""
+    _check_dev(f"{who}qa", qa, dev, torch.uint8)
+    _check_dev(f"{who}sx_pairs", sx_pairs, dev, torch.int32)
+    _need(sx_pairs.dim() == 2, ValueError, f"{who}sx_pairs must be [K/G, M]")
+    m, k = sx_pairs.shape[1], sx_pairs.shape[0] * group_size
+    _need(tuple(qa.shape) == _operand_shape(m, k, operand), ValueError,
+          f"{who}qa must be {_operand_shape(m, k, operand)} for M={m}, K={k}, got {tuple(qa.shape)}")
+    _check_dev(f"{who}weight_operand", weight_operand, dev, torch.uint8)
+    _check_dev(f"{who}weight_scale_pairs", weight_scale_pairs, dev, torch.int32)
+    _need(weight_scale_pairs.dim() == 2 and weight_scale_pairs.shape[0] == k // group_size, ValueError,
+          f"{who}weight_scale_pairs must be [{k // group_size}, N], got {tuple(weight_scale_pairs.shape)}")
+    n = weight_scale_pairs.shape[1]
+    _need(tuple(weight_operand.shape) == _operand_shape(n, k, operand), ValueError,
+          f"{who}weight_operand must be {_operand_shape(n, k, operand)}, got {tuple(weight_operand.shape)}")
+    _check_epilogue(mid, l1cat, bias, m, n, dev)
+    return m, n, k
+
+
+@torch.library.custom_op("svdq::w4a4_gemm_siblings", mutates_args=())
+def w4a4_gemm_siblings(qa: list[Tensor], sx_pairs: list[Tensor], weight_operand: list[Tensor],
+                       weight_scale_pairs: list[Tensor], mid: list[Tensor], l1cat: list[Tensor],
+                       bias: list[Optional[Tensor]], group_size: int, operand: int, out_f32: bool) -> list[Tensor]:
+    """``w4a4_gemm`` of up to ``lib.SVDQ_MAX_SIBLINGS`` layers over the same rows (the i-th entry
+    of every list belongs to layer i), in one launch (``svdq_w4a4_gemm_siblings``); each output is
+    bit-identical to that layer's ``w4a4_gemm``."""
+    count = len(qa)
+    _need(1 <= count <= lib.SVDQ_MAX_SIBLINGS, ValueError, f"1..{lib.SVDQ_MAX_SIBLINGS} layers, got {count}")
+    _need(all(len(a) == count for a in (sx_pairs, weight_operand, weight_scale_pairs, mid, l1cat, bias)),
+          ValueError, "one entry per layer in every list")
+    _need(qa[0].is_cuda, RuntimeError, "svdq::w4a4_gemm_siblings needs GPU tensors")
+    _need(operand in _OPERANDS, ValueError, f"operand={operand}")
+    dev = qa[0].device
+    shapes = [_check_w4a4_operands(qa[i], sx_pairs[i], weight_operand[i], weight_scale_pairs[i], mid[i], l1cat[i],
+                                   bias[i], group_size, operand, dev, f"layer {i}: ") for i in range(count)]
+    m, _, k = shapes[0]
+    _need(all(s[0] == m and s[2] == k for s in shapes), ValueError,
+          f"sibling layers need the same M and K, got {[(s[0], s[2]) for s in shapes]}")
+    ys = [torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev) for _, n, _ in shapes]
+    arr = (lib.W4A4Sibling * count)()
+    for i, (y, (_, n, _)) in enumerate(zip(ys, shapes)):
+        arr[i] = lib.W4A4Sibling(qa[i].data_ptr(), sx_pairs[i].data_ptr(), weight_operand[i].data_ptr(),
+                                 weight_scale_pairs[i].data_ptr(), mid[i].data_ptr(), l1cat[i].data_ptr(),
+                                 mid[i].shape[2], _vp(bias[i]), n, y.data_ptr(), n)
+    lib.call("svdq_w4a4_gemm_siblings", arr, count, operand, m, k, group_size, int(out_f32), _stream(dev))
+    return ys
+
+
+@w4a4_gemm_siblings.register_fake
+def _(qa, sx_pairs, weight_operand, weight_scale_pairs, mid, l1cat, bias, group_size, operand, out_f32):
+    return [a.new_empty((s.shape[1], w.shape[1]), dtype=torch.float32 if out_f32 else torch.bfloat16)
+            for a, s, w in zip(qa, sx_pairs, weight_scale_pairs)]
 
 
 @torch.library.custom_op("svdq::w4a16_gemm", mutates_args=())

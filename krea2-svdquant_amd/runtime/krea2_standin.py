@@ -28,7 +28,9 @@ selects the torch ops) and the attention (``svdq::attention``, a flash-attention
 ``ATTENTION = "sdpa"`` selects PyTorch's fused SDPA kernels); the remaining elementwise work runs in
 PyTorch-ROCm (on the CPU everything is torch).  With
 ``fused=True`` the sigmoid gate, the SwiGLU product and the two gated residual adds run inside
-the stores of to_gate, ff.up, to_out.0 and ff.down instead.
+the stores of to_gate, ff.up, to_out.0 and ff.down instead.  The linears that read the same input
+(to_q, to_k, to_v, to_gate; ff.gate, ff.up) run their GEMMs as one launch by default
+(``run_grouped``; bit-identical to calling them one after another).
 """
 from __future__ import annotations
 
@@ -44,7 +46,7 @@ from torch import Tensor, nn
 from ..kernels.hip import ops as hip_ops
 from ..quant.state import SVDQuantLinearState
 from .linear import SVDQuantLinear
-from .siblings import run_concurrent
+from .siblings import run_concurrent, run_grouped
 
 LINEAR_NAMES = ("attn.to_q", "attn.to_k", "attn.to_v", "attn.to_gate", "attn.to_out.0",
                 "ff.gate", "ff.up", "ff.down")
@@ -186,15 +188,17 @@ class Krea2StandInBlock(nn.Module):
                 "attn.to_out.0": a.to_out[0], "ff.gate": f.gate, "ff.up": f.up, "ff.down": f.down}
 
     def forward(self, x: Tensor, cos: Tensor, sin: Tensor, linear: LinearFn = _module_linear,
-                modulation: Optional[Tensor] = None, fused: bool = False, siblings: bool = False) -> Tensor:
+                modulation: Optional[Tensor] = None, fused: bool = False, siblings: bool | str = "grouped") -> Tensor:
         """x [T, hidden] -> [T, hidden].  ``linear(name, module, input)`` evaluates a quantized
         linear (default: the module itself); ``modulation`` overrides the block's buffer (a
         reference evaluation on another device passes its own copy).  ``fused=True`` runs the
         modules with the ops that follow to_gate, to_out.0, ff.up and ff.down fused into their
         kernels' stores (``SVDQuantLinear.forward_epilogue``: the same ops, the same bf16
-        rounding); ``linear`` is then not used.  ``siblings=True`` issues the linears that read
-        the same input (to_q, to_k, to_v, to_gate; ff.gate, ff.up) concurrently on side streams
-        (``run_concurrent``: same kernels, bit-identical outputs)."""
+        rounding); ``linear`` is then not used.  ``siblings`` groups the linears that read the
+        same input (to_q, to_k, to_v, to_gate; ff.gate, ff.up): ``"grouped"`` (default) runs their
+        GEMMs as one launch (``run_grouped``; with the default ``linear`` only), ``True`` or
+        ``"concurrent"`` issues them concurrently on side streams (``run_concurrent``), ``False``
+        one after another; all three give bit-identical outputs."""
         d = self.dims
         mod = self.modulation if modulation is None else modulation
         shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = (m.to(x.dtype) for m in mod)
@@ -205,8 +209,12 @@ class Krea2StandInBlock(nn.Module):
                                        siblings)
 
         def siblings_of(z: Tensor, *names: str) -> list[Tensor]:
+            if siblings == "grouped" and linear is _module_linear:
+                return run_grouped(z, [lin[n] for n in names])
             fns = [partial(linear, n, lin[n]) for n in names]
-            return run_concurrent(z, fns) if siblings else [f(z) for f in fns]
+            if siblings is True or siblings == "concurrent":
+                return run_concurrent(z, fns)
+            return [f(z) for f in fns]
 
         h = norm_modulate(x, scale_a, shift_a)
         q, g, k, v = siblings_of(h, "attn.to_q", "attn.to_gate", "attn.to_k", "attn.to_v")
@@ -223,7 +231,7 @@ class Krea2StandInBlock(nn.Module):
         return torch.addcmul(x, gate_f, linear("ff.down", lin["ff.down"], f))
 
     def _forward_fused(self, x: Tensor, cos: Tensor, sin: Tensor, lin: dict, mods: tuple,
-                       siblings: bool = False) -> Tensor:
+                       siblings: bool | str = "grouped") -> Tensor:
         """``forward`` with the gates, SwiGLU and residuals in the linears' epilogues (to_gate and
         ff.up then need the attention output and ff.gate's output: only to_q, to_k and to_v
         remain siblings)."""
@@ -232,7 +240,12 @@ class Krea2StandInBlock(nn.Module):
         t = x.shape[0]
         h = norm_modulate(x, scale_a, shift_a)
         fns = [lin["attn.to_q"], lin["attn.to_k"], lin["attn.to_v"]]
-        q, k, v = run_concurrent(h, fns) if siblings else [f(h) for f in fns]
+        if siblings == "grouped":
+            q, k, v = run_grouped(h, fns)
+        elif siblings is True or siblings == "concurrent":
+            q, k, v = run_concurrent(h, fns)
+        else:
+            q, k, v = [f(h) for f in fns]
         q, k, v = (z.view(t, -1, d.head_dim) for z in (q, k, v))
         q = head_norm_rope(q, cos, sin)
         k = head_norm_rope(k, cos, sin)
@@ -296,7 +309,7 @@ class Krea2StandInTransformer(nn.Module):
         return cls(dims, blocks)
 
     def forward(self, tokens: Tensor, linear: LinearFn = _module_linear, fused: bool = False,
-                siblings: bool = False) -> Tensor:
+                siblings: bool | str = "grouped") -> Tensor:
         """tokens [T, hidden] -> [T, hidden] through every block (``linear``, ``fused``,
         ``siblings`` as in the block)."""
         cos, sin = rope_tables(tokens.shape[0], self.dims.head_dim, tokens.device, tokens.dtype)
@@ -306,7 +319,7 @@ class Krea2StandInTransformer(nn.Module):
         return x
 
     def denoise_step(self, text: Tensor, latent: Tensor, dt: float, fused: bool = False,
-                     siblings: bool = False) -> Tensor:
+                     siblings: bool | str = "grouped") -> Tensor:
         """One Euler step of the flow: the denoiser over [text | latent], then
         ``latent + dt * velocity`` for the latent tokens."""
         out = self.forward(torch.cat([text, latent], dim=0), fused=fused, siblings=siblings)

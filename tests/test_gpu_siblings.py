@@ -60,3 +60,68 @@ def test_standin_siblings_bit_identical(dev):
         torch.cuda.synchronize()
         assert torch.equal(a, b), f"fused={fused}"
         assert torch.equal(c, d), f"fused={fused}"
+
+
+# ---- one launch for the siblings' GEMMs (svdq_w4a4_gemm_siblings) -------------------------------
+
+def _prepared(mods, dev):
+    return [m._prepare(dev, with_adapters=bool(m.lora_adapters)) for m in mods]
+
+
+@pytest.mark.parametrize("out_f32", [False, True])
+@pytest.mark.parametrize("k", [1024, 768])   # one launch (K % 512 == 0); one launch per layer
+def test_grouped_gemms_match_single_layer_forwards(dev, k, out_f32):
+    from krea2_svdquant_amd.kernels.hip.backend import forward_prepared, forward_prepared_siblings
+    # partial column tiles (160, 96), a LoRA adapter that widens one layer's rank tiles (RTp 96)
+    mods = _layers(dev, [(640, k), (160, k), (384, k), (96, k)], seed=31, backend="hip_gfx950")
+    gen_l = torch.Generator(device=dev).manual_seed(6)
+    mods[1].add_lora_adapter((torch.randn(48, k, device=dev, generator=gen_l) * 0.05).to(torch.bfloat16),
+                             (torch.randn(160, 48, device=dev, generator=gen_l) * 0.05).to(torch.bfloat16),
+                             scale=0.8)
+    preps = _prepared(mods, dev)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    for m in (300, 64, 517, 256):                  # ragged row counts: partial row tiles
+        x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+        single = [forward_prepared(x, p, out_f32=out_f32) for p in preps]
+        for count in (4, 2, 1):
+            grouped = forward_prepared_siblings(x, preps[:count], out_f32=out_f32)
+            assert [tuple(y.shape) for y in grouped] == [tuple(y.shape) for y in single[:count]]
+            for i, (a, b) in enumerate(zip(single, grouped)):
+                assert torch.equal(a, b), f"m={m} count={count} layer {i}"
+
+
+def test_grouped_gemms_at_the_block_shapes(dev):
+    """to_q, to_k, to_v, to_gate at M = 4352 (2040 tiles over the XCDs) and ff.up, ff.gate."""
+    from krea2_svdquant_amd.kernels.hip.backend import forward_prepared, forward_prepared_siblings
+    gen = torch.Generator(device=dev).manual_seed(8)
+    x = torch.randn(4352, 6144, device=dev, generator=gen).to(torch.bfloat16)
+    for shapes, seed in (([(6144, 6144), (1536, 6144), (1536, 6144), (6144, 6144)], 41),
+                         ([(16384, 6144), (16384, 6144)], 42)):
+        preps = _prepared(_layers(dev, shapes, seed=seed, backend="hip_gfx950"), dev)
+        grouped = forward_prepared_siblings(x, preps)
+        for i, p in enumerate(preps):
+            assert torch.equal(forward_prepared(x, p), grouped[i]), f"layer {i} of {shapes}"
+        del preps, grouped
+        torch.cuda.empty_cache()
+
+
+def test_run_grouped_modules_and_standin(dev):
+    from krea2_svdquant_amd.runtime.krea2_standin import Krea2Dims, Krea2StandInTransformer
+    from krea2_svdquant_amd.runtime.siblings import run_grouped
+    mods = _layers(dev, [(512, 512), (256, 512), (128, 512)], seed=51, backend="hip_gfx950")
+    gen = torch.Generator(device=dev).manual_seed(12)
+    x = torch.randn(2, 150, 512, device=dev, generator=gen).to(torch.bfloat16)   # leading dims kept
+    for a, b in zip([m(x) for m in mods], run_grouped(x, mods)):
+        assert a.shape == b.shape and torch.equal(a, b)
+    w16 = _layers(dev, [(256, 512), (256, 512)], seed=52, backend="hip_gfx950_w4a16")   # not groupable
+    for a, b in zip([m(x) for m in w16], run_grouped(x, w16)):
+        assert torch.equal(a, b)
+    dims = Krea2Dims(layers=2, hidden=512, heads=4, kv_heads=1, head_dim=128, mlp=1024)   # K % 512 == 0
+    model = Krea2StandInTransformer.random(dims, rank=32, group_size=64, device=dev, seed=13)
+    text = torch.randn(16, 512, device=dev, generator=gen).to(torch.bfloat16)
+    latent = torch.randn(80, 512, device=dev, generator=gen).to(torch.bfloat16)
+    for fused in (False, True):
+        a = model.denoise_step(text, latent, dt=-0.125, fused=fused)
+        b = model.denoise_step(text, latent, dt=-0.125, fused=fused, siblings="grouped")
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"fused={fused}"
