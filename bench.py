@@ -351,18 +351,19 @@ def denoise_line(args, dev) -> dict:
     ms, lat = run(False)
     same_sib = bool(torch.equal(lat, lat_sib))
     same_seq = bool(torch.equal(lat, lat_seq))
-    # the same steps with the attention on PyTorch's fused SDPA kernels, and with the norms in
-    # torch as well (config 3 as BASELINE states it: attention and norms in PyTorch-ROCm)
+    # the same steps with the attention on PyTorch's fused SDPA kernels, and with the norms and
+    # gate ops in torch as well (config 3 as BASELINE states it: everything but the linears in
+    # PyTorch-ROCm)
     from krea2_svdquant_amd.runtime import krea2_standin as ks
     try:
         ks.ATTENTION = "sdpa"
         model.denoise_step(text, latent, dt)
         ms_sdpa, _ = run(False)
-        ks.NORMS = "torch"
+        ks.NORMS = ks.GATES = "torch"
         model.denoise_step(text, latent, dt)
         ms_torch_glue, _ = run(False)
     finally:
-        ks.ATTENTION, ks.NORMS = "hip", "hip"
+        ks.ATTENTION, ks.NORMS, ks.GATES = "hip", "hip", "hip"
     # one more step with HIP events around every quantized linear: their share of the step
     pairs = []
 
@@ -386,26 +387,25 @@ def denoise_line(args, dev) -> dict:
             "ms_per_denoise_step_concurrent_siblings": round(ms_sib, 3),
             "ms_per_denoise_step_fused_epilogues_concurrent_siblings": round(ms_fused_sib, 3),
             "ms_per_denoise_step_sdpa_attention": round(ms_sdpa, 3),
-            "ms_per_denoise_step_torch_attention_and_norms": round(ms_torch_glue, 3),
+            "ms_per_denoise_step_torch_attention_norms_gates": round(ms_torch_glue, 3),
             "ms_per_denoise_step_sequential_siblings": round(ms_seq, 3),
             "ms_per_denoise_step_fused_epilogues_sequential_siblings": round(ms_fused_seq, 3),
             "concurrent_siblings_bit_identical": same_sib, "sequential_siblings_bit_identical": same_seq,
             "linears_ms_per_step": round(lin_ms, 3), "rest_ms_per_step": round(ms - lin_ms, 3),
             "tokens": 4352, "blocks": dims.layers, "peak_hbm_GB": round(hbm_gb, 1), "finite": finite,
             "note": "stand-in Krea-2 denoiser (diffusers is absent): 28 blocks, 8 W4A4 linears each on this "
-                    "backend; attention (48 q / 12 kv heads, svdq::attention), adaptive RMS norms, per-head "
-                    "norm + rotary embedding on gfx950 kernels, gates and residuals in PyTorch-ROCm "
-                    "(ms_per_denoise_step; ms_per_denoise_step_sdpa_attention: the attention on PyTorch's "
-                    "fused SDPA kernels instead; ms_per_denoise_step_torch_attention_and_norms: attention and "
-                    "norms both in PyTorch-ROCm, the configuration as BASELINE states it; with the sigmoid gate, "
-                    "SwiGLU product and "
-                    "gated residuals fused into the stores of to_gate, ff.up, to_out.0 and ff.down instead: "
-                    "ms_per_denoise_step_fused_epilogues; the linears that read the same input (to_q, to_gate, "
-                    "to_k, to_v; ff.up, ff.gate) run their GEMMs as one launch (svdq_w4a4_gemm_siblings), or "
-                    "*_sequential_siblings: one after another, *_concurrent_siblings: on side streams); random-init "
-                    "quantized weights, N(0,1) tokens; HIP "
-                    "events around 8 Euler steps after one warm-up step of each; linears_ms_per_step: HIP events "
-                    "around each linear of one forward"}
+                    "backend, the linears that read the same input (to_q, to_gate, to_k, to_v; ff.up, ff.gate) "
+                    "with their GEMMs as one launch (svdq_w4a4_gemm_siblings); attention (48 q / 12 kv heads, "
+                    "svdq::attention), adaptive RMS norms, per-head norm + rotary embedding, sigmoid gate and "
+                    "SwiGLU product (svdq::gate_op) on gfx950 kernels, gated residuals as torch.addcmul "
+                    "(ms_per_denoise_step). Variants: *_sdpa_attention: the attention on PyTorch's fused SDPA "
+                    "kernels; *_torch_attention_norms_gates: attention, norms and gate ops in PyTorch-ROCm (the "
+                    "configuration as BASELINE states it); *_fused_epilogues: sigmoid gate, SwiGLU product and "
+                    "gated residuals fused into the stores of to_gate, ff.up, to_out.0 and ff.down; "
+                    "*_sequential_siblings: the sibling linears one after another, *_concurrent_siblings: on "
+                    "side streams. Random-init quantized weights, N(0,1) tokens; HIP events around 8 Euler "
+                    "steps after one warm-up step of each; linears_ms_per_step: HIP events around each linear "
+                    "of one forward"}
 
 
 def attention_line(args, dev) -> dict:

@@ -234,6 +234,14 @@ typedef struct svdq_w4a4_sibling {
 int svdq_w4a4_gemm_siblings(const svdq_w4a4_sibling* layers, int count, int operand, int M, int K, int group,
                             int out_f32, hipStream_t stream);
 
+/* The sigmoid output gate and the SwiGLU product of a DiT block as one pass each over contiguous
+ * bf16 tensors: out[i] = op(y[i], aux[i]) with op SVDQ_EPI_MUL_SIGMOID (aux * sigmoid(y)) or
+ * SVDQ_EPI_SILU_MUL (silu(aux) * y), rounded as the fused store ops above (and as the torch ops on
+ * bf16 tensors).  No counterpart inside the reference (its blocks run these ops in diffusers); for
+ * the callers of svdq_w4a4_gemm_siblings, whose grouped layers cannot carry a fused op.
+ *   y, aux, out: 16-byte aligned, n elements each (out may equal y or aux) */
+int svdq_gate_op(int op, const void* y, const void* aux, void* out, int64_t n, hipStream_t stream);
+
 /* Normalizations of the stand-in Krea-2 block around its quantized linears.  No counterpart in
  * the reference: its blocks run in diffusers (reference src/krea2_svdquant/transformer.py:46-59),
  * whose internals it does not contain.  bf16 in and out, float32 math, one pass over the rows.

@@ -410,6 +410,19 @@ int svdq_w4a4_gemm_siblings(const svdq_w4a4_sibling* layers, int count, int oper
   return SVDQ_OK;
 }
 
+int svdq_gate_op(int op, const void* y, const void* aux, void* out, int64_t n, hipStream_t stream) {
+  if (op != SVDQ_EPI_MUL_SIGMOID && op != SVDQ_EPI_SILU_MUL)
+    return fail(SVDQ_ERR_ARG, "gate_op: op=%d (SVDQ_EPI_MUL_SIGMOID or SVDQ_EPI_SILU_MUL)", op);
+  if (!y || !aux || !out) return fail(SVDQ_ERR_ARG, "gate_op: null pointer");
+  if (n < 0) return fail(SVDQ_ERR_SHAPE, "gate_op: n=%lld", (long long)n);
+  if (!aligned16(y) || !aligned16(aux) || !aligned16(out))
+    return fail(SVDQ_ERR_ALIGN, "gate_op: y, aux, out must be 16-byte aligned");
+  if (n == 0) return SVDQ_OK;
+  return launched(svdq::launch_gate_op(op, static_cast<const uint16_t*>(y), static_cast<const uint16_t*>(aux),
+                                       static_cast<uint16_t*>(out), n, stream),
+                  "gate_op");
+}
+
 int svdq_rms_norm_modulate(const void* x, int64_t ldx, const void* w, const void* shift, int T, int H, float eps,
                            void* y, int64_t ldy, hipStream_t stream) {
   if (!x || !w || !shift || !y) return fail(SVDQ_ERR_ARG, "rms_norm_modulate: null pointer");

@@ -1026,6 +1026,29 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_siblings_kernel(GemmSiblings
 
 // Weight operand of the W4A4 GEMM, once per layer: each packed dword (8 nibbles, k0 in the
 // low nibble) becomes 8 operand bytes [k0 k2 k4 k6 k1 k3 k5 k7].
+// The sigmoid gate and SwiGLU product as their own pass over contiguous bf16 tensors (the same op
+// code as the GEMM store's): out = op(y, aux) for n elements, 8 per thread and step (16-byte
+// loads and stores), the last n % 8 elements by thread 0 of workgroup 0.
+template <int E>
+__global__ void __launch_bounds__(256) gate_op_kernel(const uint16_t* __restrict__ y, const uint16_t* __restrict__ aux,
+                                                      uint16_t* __restrict__ out, long n) {
+  const long chunks = n / 8;
+  for (long c = (long)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += (long)gridDim.x * blockDim.x) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(y + 8 * c);
+    const u32x4 a = *reinterpret_cast<const u32x4*>(aux + 8 * c);
+    *reinterpret_cast<u32x4*>(out + 8 * c) = epi_apply_op<E>(v, a, u32x4{});
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0 && n % 8) {
+    u32x4 v{}, a{};
+    for (long e = 8 * chunks; e < n; ++e) {
+      v[(e % 8) / 2] |= (uint32_t)y[e] << (16 * (e % 2));
+      a[(e % 8) / 2] |= (uint32_t)aux[e] << (16 * (e % 2));
+    }
+    const u32x4 o = epi_apply_op<E>(v, a, u32x4{});
+    for (long e = 8 * chunks; e < n; ++e) out[e] = (uint16_t)(o[(e % 8) / 2] >> (16 * (e % 2)));
+  }
+}
+
 __global__ void weight_operand_kernel(const uint32_t* __restrict__ qw, u32x2* __restrict__ out, long n, int mode) {
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
     uint32_t lo, hi;
@@ -1612,6 +1635,14 @@ hipError_t launch_w4a4_siblings(const GemmSiblings& gs, int G, bool out_f32, hip
   } else {
     return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_gate_op(int op, const uint16_t* y, const uint16_t* aux, uint16_t* out, long n, hipStream_t st) {
+  const long blocks = std::max<long>(1, std::min<long>((n / 8 + 255) / 256, 4096));
+  if (op == 1) gate_op_kernel<1><<<(unsigned)blocks, 256, 0, st>>>(y, aux, out, n);
+  else if (op == 2) gate_op_kernel<2><<<(unsigned)blocks, 256, 0, st>>>(y, aux, out, n);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -80,6 +80,9 @@ hipError_t launch_quant_any_group(const uint16_t* xhat, long ldxh, int M, int K,
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st);
 // e3m2 operands, G = 64 or 128, K % 512 == 0, every layer without fused store ops
 hipError_t launch_w4a4_siblings(const GemmSiblings& gs, int G, bool out_f32, hipStream_t st);
+// out = op(y, aux) elementwise over n contiguous bf16 values (op 1 mul_sigmoid, 2 silu_mul; the
+// GEMM store's op code), pointers 16-byte aligned
+hipError_t launch_gate_op(int op, const uint16_t* y, const uint16_t* aux, uint16_t* out, long n, hipStream_t st);
 hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, int n, int ngroups, int mode, hipStream_t st);
 // mode: 0 = e4m3, 1 = int8 16*q (both [N, K] bytes), 2 = e3m2 planar ((N + 1) & ~1 rows, K * 3 / 4
 // bytes per row)

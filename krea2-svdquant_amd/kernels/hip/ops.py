@@ -376,6 +376,29 @@ def _(xhat, qweight, weight_scales, mid, l1cat, bias, group_size, out_f32, epi=0
 
 
 # ---- stand-in block normalizations -------------------------------------------------------------
+@torch.library.custom_op("svdq::gate_op", mutates_args=())
+def gate_op(y: Tensor, aux: Tensor, op: int) -> Tensor:
+    """``aux * sigmoid(y)`` (op ``EPILOGUES["mul_sigmoid"]``) or ``silu(aux) * y`` (op
+    ``EPILOGUES["silu_mul"]``), elementwise over bf16 tensors of one shape, rounded as the torch ops
+    on bf16 tensors; one pass (``svdq_gate_op``)."""
+    _need(y.is_cuda, RuntimeError, "svdq::gate_op needs GPU tensors")
+    _need(op in (EPILOGUES["mul_sigmoid"], EPILOGUES["silu_mul"]), ValueError, f"op={op}")
+    _check_dev("y", y, y.device, torch.bfloat16)
+    _check_dev("aux", aux, y.device, torch.bfloat16)
+    _need(y.shape == aux.shape, ValueError, f"y {tuple(y.shape)} and aux {tuple(aux.shape)} differ")
+    y2, a2 = y.contiguous(), aux.contiguous()
+    y2 = y2 if y2.data_ptr() % 16 == 0 else y2.clone()
+    a2 = a2 if a2.data_ptr() % 16 == 0 else a2.clone()
+    out = torch.empty_like(y2)
+    lib.call("svdq_gate_op", op, _vp(y2), _vp(a2), _vp(out), y2.numel(), _stream(y.device))
+    return out
+
+
+@gate_op.register_fake
+def _(y, aux, op):
+    return torch.empty_like(y)
+
+
 @torch.library.custom_op("svdq::rms_norm_modulate", mutates_args=())
 def rms_norm_modulate(x: Tensor, weight: Tensor, shift: Tensor, eps: float) -> Tensor:
     """``bf16(bf16(x * rsqrt(mean(x^2) + eps) * weight) + shift)`` over the last dimension of a

@@ -25,8 +25,9 @@ latent tokens, ``latent += dt * velocity``.  On the GPU every quantized linear r
 kernels (``SVDQuantLinear``), and so do the adaptive RMS norms and the per-head norm + rotary
 embedding (``svdq::rms_norm_modulate``, ``svdq::head_rms_rope``: one pass each; ``NORMS = "torch"``
 selects the torch ops) and the attention (``svdq::attention``, a flash-attention forward;
-``ATTENTION = "sdpa"`` selects PyTorch's fused SDPA kernels); the remaining elementwise work runs in
-PyTorch-ROCm (on the CPU everything is torch).  With
+``ATTENTION = "sdpa"`` selects PyTorch's fused SDPA kernels), and so do the sigmoid gate and the
+SwiGLU product (``svdq::gate_op``, one pass each, torch's bf16 rounding; ``GATES = "torch"`` selects
+the torch ops); the gated residual adds run as ``torch.addcmul`` (on the CPU everything is torch).  With
 ``fused=True`` the sigmoid gate, the SwiGLU product and the two gated residual adds run inside
 the stores of to_gate, ff.up, to_out.0 and ff.down instead.  The linears that read the same input
 (to_q, to_k, to_v, to_gate; ff.gate, ff.up) run their GEMMs as one launch by default
@@ -121,6 +122,25 @@ def head_norm_rope(t: Tensor, cos: Tensor, sin: Tensor, eps: float = 1e-6) -> Te
     if t.is_cuda and NORMS == "hip":
         return hip_ops.head_rms_rope(t, cos, sin, eps)
     return apply_rope(rms_norm(t, eps), cos, sin)
+
+
+GATES = "hip"   # the GPU sigmoid gate and SwiGLU product: "hip" (svdq::gate_op) or "torch"
+
+
+def gate_mul_sigmoid(a: Tensor, g: Tensor) -> Tensor:
+    """``a * sigmoid(g)`` in bf16 (torch's rounding): one gfx950 pass on the GPU unless ``GATES``
+    is "torch"."""
+    if a.is_cuda and GATES == "hip":
+        return hip_ops.gate_op(g, a, hip_ops.EPILOGUES["mul_sigmoid"])
+    return a * torch.sigmoid(g)
+
+
+def gate_silu_mul(g: Tensor, u: Tensor) -> Tensor:
+    """The SwiGLU product ``silu(g) * u`` in bf16 (torch's rounding): one gfx950 pass on the GPU
+    unless ``GATES`` is "torch"."""
+    if u.is_cuda and GATES == "hip":
+        return hip_ops.gate_op(u, g, hip_ops.EPILOGUES["silu_mul"])
+    return F.silu(g) * u
 
 
 def rope_tables(tokens: int, head_dim: int, device, dtype, theta: float = 10000.0) -> tuple[Tensor, Tensor]:
@@ -222,12 +242,12 @@ class Krea2StandInBlock(nn.Module):
         q = head_norm_rope(q, cos, sin)
         k = head_norm_rope(k, cos, sin)
         a = attention(q, k, v)                                   # [T, heads * head_dim]
-        a = a * torch.sigmoid(g)
+        a = gate_mul_sigmoid(a, g)
         x = torch.addcmul(x, gate_a, linear("attn.to_out.0", lin["attn.to_out.0"], a))
 
         h = norm_modulate(x, scale_f, shift_f)
         u, g = siblings_of(h, "ff.up", "ff.gate")
-        f = F.silu(g) * u
+        f = gate_silu_mul(g, u)
         return torch.addcmul(x, gate_f, linear("ff.down", lin["ff.down"], f))
 
     def _forward_fused(self, x: Tensor, cos: Tensor, sin: Tensor, lin: dict, mods: tuple,

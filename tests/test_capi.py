@@ -165,3 +165,25 @@ def test_generic_group_rejects_fast_only_formats_before_any_launch():
         lib.call("svdq_w4a4_gemm_epi", fake, 1, fake, fake, fake, fake, fake, 32, nul, 128, 128, 128, 32, fake, 128,
                  0, lib.SVDQ_EPI_SILU_MUL, fake, 128, nul, nul)
     assert ei.value.status == -4 and "epilogue" in str(ei.value)
+
+
+def test_gate_op_and_siblings_reject_bad_arguments_before_any_launch():
+    fake = ctypes.c_void_p(0x1000)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_gate_op", 3, fake, fake, fake, 8, None)
+    assert ei.value.status == -1 and "op=3" in str(ei.value)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_gate_op", lib.SVDQ_EPI_SILU_MUL, ctypes.c_void_p(0x1002), fake, fake, 8, None)
+    assert ei.value.status == -3
+    lib.call("svdq_gate_op", lib.SVDQ_EPI_SILU_MUL, fake, fake, fake, 0, None)   # nothing to do
+    layers = (lib.W4A4Sibling * 5)()
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a4_gemm_siblings", layers, 5, 2, 256, 1024, 64, 0, None)
+    assert ei.value.status == -1 and "count=5" in str(ei.value)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a4_gemm_siblings", layers, 2, 2, 256, 1024, 64, 0, None)   # N = 0
+    assert ei.value.status == -1 and "N=0" in str(ei.value)
+    layers[0].N = layers[1].N = 128
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a4_gemm_siblings", layers, 2, 2, 256, 1024, 64, 0, None)   # null pointers
+    assert ei.value.status == -1 and "null pointer" in str(ei.value)
