@@ -459,9 +459,11 @@ hipError_t launch_act_g(const ActParams& p, int nt, int oper, bool xhat, dim3 gr
 }  // namespace
 
 int act_splits(int M, int K, int G) {
+  // 512 workgroups fill the 256 CUs once (two 4-wave workgroups per CU): as many K splits as keep
+  // row_tiles * splits within that, so no workgroups are left over for a second round
   const int row_tiles = (M + 63) / 64;
   const int ngroups = K / G;
-  int s = (512 + row_tiles - 1) / row_tiles;
+  int s = 512 / row_tiles;
   const int smax = ngroups / 4 > 0 ? ngroups / 4 : 1;
   if (s > smax) s = smax;
   if (s < 1) s = 1;
