@@ -252,6 +252,15 @@ int svdq_gate_op(int op, const void* y, const void* aux, void* out, int64_t n, h
 int svdq_rms_norm_modulate(const void* x, int64_t ldx, const void* w, const void* shift, int T, int H, float eps,
                            void* y, int64_t ldy, hipStream_t stream);
 
+/* The gated residual add that precedes the norm, in the same pass:
+ *   xo = bf16(x + g * v)   (torch.addcmul(x, g, v): one rounding; g: bf16 [H], v: bf16 [T, ldv])
+ *   y  = the adaptive RMS norm above of xo
+ * All pointers 16-byte aligned, leading dimensions multiples of 8; xo may equal x, y overlaps
+ * neither. */
+int svdq_residual_rms_norm_modulate(const void* x, int64_t ldx, const void* v, int64_t ldv, const void* g,
+                                    const void* w, const void* shift, int T, int H, float eps, void* xo, int64_t ldxo,
+                                    void* y, int64_t ldy, hipStream_t stream);
+
 /* Per-head RMS norm and rotate-half rotary embedding of t, contiguous bf16 [T, heads, 128] (q or
  * k), into out (same layout, may not overlap t).  cos / sin: bf16 [T, ldcs] position tables, of
  * which columns 0..63 are read (the rotate-half tables repeat their first half).  Per head:

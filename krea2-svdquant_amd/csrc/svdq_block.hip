@@ -25,23 +25,47 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// The gated residual add bf16(x + g * v) in one rounding (torch.addcmul(x, g, v)) on a chunk of 8.
+__device__ __forceinline__ u32x4 addcmul8(u32x4 x, u32x4 g, u32x4 v) {
+  u32x4 o;
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    o[d] = pack_bf16x2(__builtin_fmaf(bf16lo(g[d]), bf16lo(v[d]), bf16lo(x[d])),
+                       __builtin_fmaf(bf16hi(g[d]), bf16hi(v[d]), bf16hi(x[d])));
+  return o;
+}
+
 // Adaptive RMS norm, one 256-thread workgroup per row.  Pass 1 sums the squares of the row's
 // 16-byte chunks (thread t takes chunks t, t + 256, ...; the first NR of them stay in registers),
 // pass 2 writes the normalized, weighted and shifted chunks (chunks beyond NR re-read from L2).
-template <int NR>
+// RES: the row is first formed as the gated residual x + g * v (g a vector [H], v the layer output
+// [T, ldv]) and written to xo, and that row is normalized (chunks beyond NR re-read from xo).
+template <int NR, bool RES = false>
 __global__ void __launch_bounds__(256) rms_norm_modulate_kernel(const uint16_t* __restrict__ x, long ldx,
                                                                 const uint16_t* __restrict__ w,
                                                                 const uint16_t* __restrict__ shift, int H,
-                                                                float eps, uint16_t* __restrict__ y, long ldy) {
+                                                                float eps, uint16_t* __restrict__ y, long ldy,
+                                                                const uint16_t* __restrict__ v = nullptr,
+                                                                long ldv = 0, const uint16_t* __restrict__ g = nullptr,
+                                                                uint16_t* __restrict__ xo = nullptr, long ldxo = 0) {
   __shared__ float part[4];
   const int tid = threadIdx.x, nc = H / 8;
   const uint16_t* xr = x + (long)blockIdx.x * ldx;
+  uint16_t* xor_ = RES ? xo + (long)blockIdx.x * ldxo : nullptr;
+  auto row_chunk = [&](int c) {   // the chunk to normalize (RES: formed and stored first)
+    u32x4 r = ld16(xr + 8 * c);
+    if (RES) {
+      r = addcmul8(r, ld16(g + 8 * c), ld16(v + (long)blockIdx.x * ldv + 8 * c));
+      *reinterpret_cast<u32x4*>(xor_ + 8 * c) = r;
+    }
+    return r;
+  };
   u32x4 keep[NR];
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
     const int c = tid + 256 * i;
-    keep[i] = c < nc ? ld16(xr + 8 * c) : u32x4{};
+    keep[i] = c < nc ? row_chunk(c) : u32x4{};
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       const float a = bf16lo(keep[i][d]), b = bf16hi(keep[i][d]);
@@ -50,7 +74,7 @@ __global__ void __launch_bounds__(256) rms_norm_modulate_kernel(const uint16_t* 
     }
   }
   for (int c = tid + 256 * NR; c < nc; c += 256) {
-    const u32x4 v = ld16(xr + 8 * c);
+    const u32x4 v = row_chunk(c);
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       const float a = bf16lo(v[d]), b = bf16hi(v[d]);
@@ -79,7 +103,7 @@ __global__ void __launch_bounds__(256) rms_norm_modulate_kernel(const uint16_t* 
     const int c = tid + 256 * i;
     if (c < nc) put(c, keep[i]);
   }
-  for (int c = tid + 256 * NR; c < nc; c += 256) put(c, ld16(xr + 8 * c));
+  for (int c = tid + 256 * NR; c < nc; c += 256) put(c, ld16((RES ? xor_ : xr) + 8 * c));
 }
 
 // Per-head RMS norm and rotary embedding, one wave per (token, head) row of 128 channels: lane j
@@ -155,6 +179,14 @@ hipError_t launch_rms_norm_modulate(const uint16_t* x, long ldx, const uint16_t*
                                     int H, float eps, uint16_t* y, long ldy, hipStream_t st) {
   // rows of up to 4 * 256 chunks (H <= 8192) stay in registers between the passes
   rms_norm_modulate_kernel<4><<<T, 256, 0, st>>>(x, ldx, w, shift, H, eps, y, ldy);
+  return hipGetLastError();
+}
+
+hipError_t launch_residual_rms_norm_modulate(const uint16_t* x, long ldx, const uint16_t* v, long ldv,
+                                             const uint16_t* g, const uint16_t* w, const uint16_t* shift, int T, int H,
+                                             float eps, uint16_t* xo, long ldxo, uint16_t* y, long ldy,
+                                             hipStream_t st) {
+  rms_norm_modulate_kernel<4, true><<<T, 256, 0, st>>>(x, ldx, w, shift, H, eps, y, ldy, v, ldv, g, xo, ldxo);
   return hipGetLastError();
 }
 

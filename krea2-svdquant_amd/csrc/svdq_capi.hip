@@ -437,6 +437,25 @@ int svdq_rms_norm_modulate(const void* x, int64_t ldx, const void* w, const void
                   "rms_norm_modulate");
 }
 
+int svdq_residual_rms_norm_modulate(const void* x, int64_t ldx, const void* v, int64_t ldv, const void* g,
+                                    const void* w, const void* shift, int T, int H, float eps, void* xo, int64_t ldxo,
+                                    void* y, int64_t ldy, hipStream_t stream) {
+  if (!x || !v || !g || !w || !shift || !xo || !y) return fail(SVDQ_ERR_ARG, "residual_rms_norm_modulate: null pointer");
+  if (T <= 0 || H <= 0 || H % 8)
+    return fail(SVDQ_ERR_SHAPE, "residual_rms_norm_modulate: T=%d, H=%d (H %% 8 == 0)", T, H);
+  if (!(eps >= 0.0f)) return fail(SVDQ_ERR_ARG, "residual_rms_norm_modulate: eps must be >= 0");
+  if (ldx < H || ldv < H || ldxo < H || ldy < H || ldx % 8 || ldv % 8 || ldxo % 8 || ldy % 8 || !aligned16(x) ||
+      !aligned16(v) || !aligned16(g) || !aligned16(w) || !aligned16(shift) || !aligned16(xo) || !aligned16(y))
+    return fail(SVDQ_ERR_ALIGN,
+                "residual_rms_norm_modulate: 16-byte aligned pointers, leading dimensions >= H and multiples of 8");
+  return launched(svdq::launch_residual_rms_norm_modulate(
+                      static_cast<const uint16_t*>(x), ldx, static_cast<const uint16_t*>(v), ldv,
+                      static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(w),
+                      static_cast<const uint16_t*>(shift), T, H, eps, static_cast<uint16_t*>(xo), ldxo,
+                      static_cast<uint16_t*>(y), ldy, stream),
+                  "residual_rms_norm_modulate");
+}
+
 int svdq_head_rms_rope(const void* t, int T, int heads, const void* cos, const void* sin, int64_t ldcs, float eps,
                        void* out, hipStream_t stream) {
   if (!t || !cos || !sin || !out) return fail(SVDQ_ERR_ARG, "head_rms_rope: null pointer");

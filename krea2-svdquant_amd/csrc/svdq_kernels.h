@@ -94,6 +94,11 @@ hipError_t launch_w4a4_any_group(const GemmParams& p, int G, bool out_f32, hipSt
 // per-head RMS norm + rotary embedding of contiguous [T, heads, 128]
 hipError_t launch_rms_norm_modulate(const uint16_t* x, long ldx, const uint16_t* w, const uint16_t* shift, int T,
                                     int H, float eps, uint16_t* y, long ldy, hipStream_t st);
+// xo = bf16(x + g * v) (torch.addcmul, g a vector [H]), then y = the adaptive RMS norm of xo
+hipError_t launch_residual_rms_norm_modulate(const uint16_t* x, long ldx, const uint16_t* v, long ldv,
+                                             const uint16_t* g, const uint16_t* w, const uint16_t* shift, int T, int H,
+                                             float eps, uint16_t* xo, long ldxo, uint16_t* y, long ldy,
+                                             hipStream_t st);
 hipError_t launch_head_rms_rope(const uint16_t* t, int T, int heads, const uint16_t* cs, const uint16_t* sn,
                                 long ldcs, float eps, uint16_t* out, hipStream_t st);
 // Stand-in block attention (svdq_attn.hip): softmax(scale q k^T) v, head dimension 128, H query heads

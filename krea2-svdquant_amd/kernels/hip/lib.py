@@ -73,6 +73,8 @@ SIGNATURES = {
     "svdq_w4a4_gemm_siblings": (_I, [ctypes.POINTER(W4A4Sibling), _I, _I, _I, _I, _I, _I, _P]),
     "svdq_gate_op": (_I, [_I, _P, _P, _P, _L, _P]),
     "svdq_rms_norm_modulate": (_I, [_P, _L, _P, _P, _I, _I, ctypes.c_float, _P, _L, _P]),
+    "svdq_residual_rms_norm_modulate": (_I, [_P, _L, _P, _L, _P, _P, _P, _I, _I, ctypes.c_float, _P, _L, _P, _L,
+                                             _P]),
     "svdq_head_rms_rope": (_I, [_P, _I, _I, _P, _P, _L, ctypes.c_float, _P, _P]),
     "svdq_attention_workspace": (_L, [_I, _I]),
     "svdq_attention_fwd": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, ctypes.c_float, _P, _L, _P, _P]),

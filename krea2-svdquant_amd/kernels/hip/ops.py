@@ -424,6 +424,44 @@ def _(x, weight, shift, eps):
     return torch.empty_like(x)
 
 
+def _rows16(t: Tensor, h: int) -> Tensor:
+    """[..., h] as rows with unit stride, a leading dimension % 8 == 0 and a 16-byte aligned start."""
+    t2 = t.reshape(-1, h)
+    if t2.stride(-1) != 1 or t2.stride(0) % 8 or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    if t2.data_ptr() % 16:
+        t2 = t2.clone()
+    return t2
+
+
+@torch.library.custom_op("svdq::residual_rms_norm_modulate", mutates_args=())
+def residual_rms_norm_modulate(x: Tensor, v: Tensor, gate: Tensor, weight: Tensor, shift: Tensor,
+                               eps: float) -> tuple[Tensor, Tensor]:
+    """``xo = torch.addcmul(x, gate, v)`` (bf16, one rounding) and ``rms_norm_modulate(xo, weight,
+    shift, eps)`` in one pass; returns ``(xo, y)``.  ``x``, ``v`` bf16 [..., H] of one shape,
+    ``gate``, ``weight``, ``shift`` bf16 [H]."""
+    _need(x.is_cuda, RuntimeError, "svdq::residual_rms_norm_modulate needs GPU tensors")
+    dev = x.device
+    h = x.shape[-1]
+    _need(x.dtype == torch.bfloat16 and v.dtype == torch.bfloat16, TypeError, "x and v must be bf16")
+    _need(v.shape == x.shape and v.device == dev, ValueError, f"v {tuple(v.shape)} must match x {tuple(x.shape)}")
+    for name, t in (("gate", gate), ("weight", weight), ("shift", shift)):
+        _check_dev(name, t, dev, torch.bfloat16)
+        _need(t.numel() == h, ValueError, f"{name} must have {h} elements, got {t.numel()}")
+    gate, weight, shift = (t if t.data_ptr() % 16 == 0 else t.clone() for t in (gate, weight, shift))
+    x2, v2 = _rows16(x, h), _rows16(v, h)
+    xo = torch.empty((x2.shape[0], h), dtype=torch.bfloat16, device=dev)
+    y = torch.empty_like(xo)
+    lib.call("svdq_residual_rms_norm_modulate", _vp(x2), x2.stride(0), _vp(v2), v2.stride(0), _vp(gate),
+             _vp(weight), _vp(shift), x2.shape[0], h, ctypes.c_float(eps), _vp(xo), h, _vp(y), h, _stream(dev))
+    return xo.view(x.shape), y.view(x.shape)
+
+
+@residual_rms_norm_modulate.register_fake
+def _(x, v, gate, weight, shift, eps):
+    return torch.empty_like(x), torch.empty_like(x)
+
+
 @torch.library.custom_op("svdq::head_rms_rope", mutates_args=())
 def head_rms_rope(t: Tensor, cos: Tensor, sin: Tensor, eps: float) -> Tensor:
     """Per-head RMS norm of ``t`` [T, heads, 128] (bf16) followed by the rotate-half rotary

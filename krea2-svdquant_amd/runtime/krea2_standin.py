@@ -115,6 +115,17 @@ def norm_modulate(x: Tensor, scale: Tensor, shift: Tensor, eps: float = 1e-6) ->
     return rms_norm(x, eps, weight=w) + shift
 
 
+def residual_norm_modulate(x: Tensor, gate: Tensor, v: Tensor, scale: Tensor, shift: Tensor,
+                           eps: float = 1e-6) -> tuple[Tensor, Tensor]:
+    """The gated residual ``x + gate * v`` (``torch.addcmul``, one bf16 rounding) and the adaptive
+    RMS norm of the result: one gfx950 pass on the GPU (``svdq::residual_rms_norm_modulate``)
+    unless ``NORMS`` is "torch".  Returns (new residual, normed activation)."""
+    if x.is_cuda and NORMS == "hip":
+        return hip_ops.residual_rms_norm_modulate(x, v, gate, 1 + scale, shift, eps)
+    x = torch.addcmul(x, gate, v)
+    return x, norm_modulate(x, scale, shift, eps)
+
+
 def head_norm_rope(t: Tensor, cos: Tensor, sin: Tensor, eps: float = 1e-6) -> Tensor:
     """Per-head RMS norm of q or k [T, heads, head_dim] and the rotary embedding: one gfx950
     kernel on the GPU for head_dim 128 (``svdq::head_rms_rope``) unless ``NORMS`` is "torch",
@@ -219,14 +230,22 @@ class Krea2StandInBlock(nn.Module):
         GEMMs as one launch (``run_grouped``; with the default ``linear`` only), ``True`` or
         ``"concurrent"`` issues them concurrently on side streams (``run_concurrent``), ``False``
         one after another; all three give bit-identical outputs."""
-        d = self.dims
         mod = self.modulation if modulation is None else modulation
+        if fused:
+            return self._forward_fused(x, cos, sin, self.linears(), tuple(m.to(x.dtype) for m in mod), siblings)
+        x, (g_f, y_f) = self._forward_deferred(x, cos, sin, linear, mod, siblings, None)
+        return torch.addcmul(x, g_f, y_f)
+
+    def _forward_deferred(self, x: Tensor, cos: Tensor, sin: Tensor, linear: LinearFn, mod: Tensor,
+                          siblings: bool | str, pending: Optional[tuple[Tensor, Tensor]]
+                          ) -> tuple[Tensor, tuple[Tensor, Tensor]]:
+        """The unfused block with its last gated residual left to the caller: returns ``(x, (g, y))``
+        with the block output ``x + g * y``.  ``pending`` = the previous block's ``(g, y)``: its
+        residual add is formed in the same pass as this block's first norm (one gfx950 kernel)."""
+        d = self.dims
         shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = (m.to(x.dtype) for m in mod)
         lin = self.linears()
         t = x.shape[0]
-        if fused:
-            return self._forward_fused(x, cos, sin, lin, (shift_a, scale_a, gate_a, shift_f, scale_f, gate_f),
-                                       siblings)
 
         def siblings_of(z: Tensor, *names: str) -> list[Tensor]:
             if siblings == "grouped" and linear is _module_linear:
@@ -236,19 +255,20 @@ class Krea2StandInBlock(nn.Module):
                 return run_concurrent(z, fns)
             return [f(z) for f in fns]
 
-        h = norm_modulate(x, scale_a, shift_a)
+        if pending is None:
+            h = norm_modulate(x, scale_a, shift_a)
+        else:
+            x, h = residual_norm_modulate(x, pending[0], pending[1], scale_a, shift_a)
         q, g, k, v = siblings_of(h, "attn.to_q", "attn.to_gate", "attn.to_k", "attn.to_v")
         q, k, v = (z.view(t, -1, d.head_dim) for z in (q, k, v))
         q = head_norm_rope(q, cos, sin)
         k = head_norm_rope(k, cos, sin)
         a = attention(q, k, v)                                   # [T, heads * head_dim]
         a = gate_mul_sigmoid(a, g)
-        x = torch.addcmul(x, gate_a, linear("attn.to_out.0", lin["attn.to_out.0"], a))
-
-        h = norm_modulate(x, scale_f, shift_f)
+        x, h = residual_norm_modulate(x, gate_a, linear("attn.to_out.0", lin["attn.to_out.0"], a), scale_f, shift_f)
         u, g = siblings_of(h, "ff.up", "ff.gate")
         f = gate_silu_mul(g, u)
-        return torch.addcmul(x, gate_f, linear("ff.down", lin["ff.down"], f))
+        return x, (gate_f, linear("ff.down", lin["ff.down"], f))
 
     def _forward_fused(self, x: Tensor, cos: Tensor, sin: Tensor, lin: dict, mods: tuple,
                        siblings: bool | str = "grouped") -> Tensor:
@@ -334,9 +354,15 @@ class Krea2StandInTransformer(nn.Module):
         ``siblings`` as in the block)."""
         cos, sin = rope_tables(tokens.shape[0], self.dims.head_dim, tokens.device, tokens.dtype)
         x = tokens
+        if fused:
+            for blk in self.transformer_blocks:
+                x = blk(x, cos, sin, linear, fused=True, siblings=siblings)
+            return x
+        # each block's last gated residual is formed with the next block's first norm
+        pending = None
         for blk in self.transformer_blocks:
-            x = blk(x, cos, sin, linear, fused=fused, siblings=siblings)
-        return x
+            x, pending = blk._forward_deferred(x, cos, sin, linear, blk.modulation, siblings, pending)
+        return torch.addcmul(x, *pending)
 
     def denoise_step(self, text: Tensor, latent: Tensor, dt: float, fused: bool = False,
                      siblings: bool | str = "grouped") -> Tensor:

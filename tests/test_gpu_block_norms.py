@@ -81,3 +81,25 @@ def test_block_norm_ops_reject_bad_shapes(dev):
     tab = torch.zeros(4, 128, device=dev, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="128"):
         ops.head_rms_rope(t, tab, tab, 1e-6)
+
+
+@pytest.mark.parametrize("t,h,ld", [(4352, 6144, 6144), (257, 1024, 1024), (33, 6144, 6160), (5, 8200, 8200)])
+def test_residual_rms_norm_modulate(dev, t, h, ld):
+    """xo = the gated residual in one rounding, against torch.addcmul (one bf16 ulp of xo where
+    torch's float product and sum round differently from one fused multiply-add; bit-equal almost
+    everywhere), and y bit-equal to svdq::rms_norm_modulate of that xo: the residual changes
+    nothing in the norm.  Rows in registers and re-read (H = 8200), a leading dimension beyond H."""
+    from krea2_svdquant_amd.kernels.hip import ops
+    gen = torch.Generator(device=dev).manual_seed(3 * t + h)
+    big = (torch.randn(2, t, ld, device=dev, generator=gen) * 3).to(torch.bfloat16)
+    x, v = big[0, :, :h], big[1, :, :h]
+    gate = (torch.rand(h, device=dev, generator=gen) + 0.2).to(torch.bfloat16)
+    w = (1 + torch.randn(h, device=dev, generator=gen) * 0.1).to(torch.bfloat16)
+    shift = (torch.randn(h, device=dev, generator=gen) * 0.1).to(torch.bfloat16)
+    xo, y = ops.residual_rms_norm_modulate(x, v, gate, w, shift, 1e-6)
+    ref = torch.addcmul(x, gate, v)
+    torch.cuda.synchronize()
+    diff = (xo.float() - ref.float()).abs()
+    assert bool((diff <= _ulp(ref)).all()), "residual beyond one bf16 ulp of torch.addcmul"
+    assert float((xo == ref).float().mean()) > 0.999
+    assert torch.equal(y, ops.rms_norm_modulate(xo, w, shift, 1e-6))
