@@ -106,24 +106,27 @@ def rms_norm(x: Tensor, eps: float = 1e-6, weight: Optional[Tensor] = None) -> T
 NORMS = "hip"   # the GPU norms: "hip" (the gfx950 kernels) or "torch" (the torch ops, as on the CPU)
 
 
-def norm_modulate(x: Tensor, scale: Tensor, shift: Tensor, eps: float = 1e-6) -> Tensor:
+def norm_modulate(x: Tensor, scale: Tensor, shift: Tensor, eps: float = 1e-6,
+                  weight: Optional[Tensor] = None) -> Tensor:
     """The block's adaptive RMS norm ``rms_norm(x) * (1 + scale) + shift``: one gfx950 kernel on
-    the GPU (``svdq::rms_norm_modulate``) unless ``NORMS`` is "torch", the torch ops elsewhere."""
-    w = 1 + scale
+    the GPU (``svdq::rms_norm_modulate``) unless ``NORMS`` is "torch", the torch ops elsewhere.
+    ``weight``: ``1 + scale`` when the caller holds it already."""
+    w = 1 + scale if weight is None else weight
     if x.is_cuda and NORMS == "hip":
         return hip_ops.rms_norm_modulate(x, w, shift, eps)
     return rms_norm(x, eps, weight=w) + shift
 
 
 def residual_norm_modulate(x: Tensor, gate: Tensor, v: Tensor, scale: Tensor, shift: Tensor,
-                           eps: float = 1e-6) -> tuple[Tensor, Tensor]:
+                           eps: float = 1e-6, weight: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
     """The gated residual ``x + gate * v`` (``torch.addcmul``, one bf16 rounding) and the adaptive
     RMS norm of the result: one gfx950 pass on the GPU (``svdq::residual_rms_norm_modulate``)
     unless ``NORMS`` is "torch".  Returns (new residual, normed activation)."""
+    w = 1 + scale if weight is None else weight
     if x.is_cuda and NORMS == "hip":
-        return hip_ops.residual_rms_norm_modulate(x, v, gate, 1 + scale, shift, eps)
+        return hip_ops.residual_rms_norm_modulate(x, v, gate, w, shift, eps)
     x = torch.addcmul(x, gate, v)
-    return x, norm_modulate(x, scale, shift, eps)
+    return x, norm_modulate(x, scale, shift, eps, weight=w)
 
 
 def head_norm_rope(t: Tensor, cos: Tensor, sin: Tensor, eps: float = 1e-6) -> Tensor:
@@ -236,6 +239,16 @@ class Krea2StandInBlock(nn.Module):
         x, (g_f, y_f) = self._forward_deferred(x, cos, sin, linear, mod, siblings, None)
         return torch.addcmul(x, g_f, y_f)
 
+    def _norm_weights(self, mod: Tensor, dtype: torch.dtype) -> tuple[Tensor, Tensor]:
+        """``1 + scale`` of the two norms, computed once per modulation tensor (storage, version,
+        dtype) instead of once per forward."""
+        key = (mod.data_ptr(), mod._version, str(mod.device), dtype)
+        hit = getattr(self, "_norm_w", None)
+        if hit is None or hit[0] != key:
+            hit = (key, (1 + mod[1].to(dtype), 1 + mod[4].to(dtype)))
+            self._norm_w = hit
+        return hit[1]
+
     def _forward_deferred(self, x: Tensor, cos: Tensor, sin: Tensor, linear: LinearFn, mod: Tensor,
                           siblings: bool | str, pending: Optional[tuple[Tensor, Tensor]]
                           ) -> tuple[Tensor, tuple[Tensor, Tensor]]:
@@ -244,6 +257,7 @@ class Krea2StandInBlock(nn.Module):
         residual add is formed in the same pass as this block's first norm (one gfx950 kernel)."""
         d = self.dims
         shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = (m.to(x.dtype) for m in mod)
+        w_a, w_f = self._norm_weights(mod, x.dtype)
         lin = self.linears()
         t = x.shape[0]
 
@@ -256,16 +270,17 @@ class Krea2StandInBlock(nn.Module):
             return [f(z) for f in fns]
 
         if pending is None:
-            h = norm_modulate(x, scale_a, shift_a)
+            h = norm_modulate(x, scale_a, shift_a, weight=w_a)
         else:
-            x, h = residual_norm_modulate(x, pending[0], pending[1], scale_a, shift_a)
+            x, h = residual_norm_modulate(x, pending[0], pending[1], scale_a, shift_a, weight=w_a)
         q, g, k, v = siblings_of(h, "attn.to_q", "attn.to_gate", "attn.to_k", "attn.to_v")
         q, k, v = (z.view(t, -1, d.head_dim) for z in (q, k, v))
         q = head_norm_rope(q, cos, sin)
         k = head_norm_rope(k, cos, sin)
         a = attention(q, k, v)                                   # [T, heads * head_dim]
         a = gate_mul_sigmoid(a, g)
-        x, h = residual_norm_modulate(x, gate_a, linear("attn.to_out.0", lin["attn.to_out.0"], a), scale_f, shift_f)
+        x, h = residual_norm_modulate(x, gate_a, linear("attn.to_out.0", lin["attn.to_out.0"], a), scale_f, shift_f,
+                                      weight=w_f)
         u, g = siblings_of(h, "ff.up", "ff.gate")
         f = gate_silu_mul(g, u)
         return x, (gate_f, linear("ff.down", lin["ff.down"], f))
