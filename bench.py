@@ -73,7 +73,8 @@ def parse():
     ap.add_argument("--no-block", action="store_true", help="skip the config 1-4 extra lines")
     ap.add_argument("--lines", default="block,w4a16,lora,denoise,attention",
                     help="extra lines to run (comma list of block, w4a16, lora, denoise, attention)")
-    ap.add_argument("--pmc-pass", nargs="?", const="w4a4", default=None, choices=["w4a4", "w4a16", "attention"],
+    ap.add_argument("--pmc-pass", nargs="?", const="w4a4", default=None,
+                    choices=["w4a4", "w4a16", "attention", "denoise"],
                     help="counter pass for rocprofv3: one copy kernel of known size, then 3 launches of the "
                          "config 1 ff.up W4A4 GEMM and 3 activation passes (w4a4), or of the config 2 ff.up "
                          "W4A16 GEMM at M=2304 (w4a16); attention: 3 calls of the config 3 block attention")
@@ -477,6 +478,27 @@ def pmc_pass_attention(args, dev) -> int:
     return 0
 
 
+def pmc_pass_denoise(args, dev) -> int:
+    """Trace pass of config 3: one warm-up and 3 default denoise steps of the stand-in model."""
+    import torch
+    from krea2_svdquant_amd.runtime.krea2_standin import Krea2Dims, Krea2StandInTransformer
+    dims = Krea2Dims()
+    model = Krea2StandInTransformer.random(dims, rank=args.rank, group_size=args.group, device=dev, seed=3)
+    gen = torch.Generator(device=dev).manual_seed(4)
+    text = torch.randn(256, dims.hidden, device=dev, generator=gen).to(torch.bfloat16)
+    lat = torch.randn(4096, dims.hidden, device=dev, generator=gen).to(torch.bfloat16)
+    lat = model.denoise_step(text, lat, -0.125)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(3):
+        lat = model.denoise_step(text, lat, -0.125)
+    b.record()
+    torch.cuda.synchronize()
+    log(f"pmc pass done: 1 + 3 default denoise steps, {a.elapsed_time(b) / 3:.2f} ms per timed step")
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -493,6 +515,8 @@ def main() -> int:
         return pmc_pass_w4a16(args, dev)
     if args.pmc_pass == "attention":
         return pmc_pass_attention(args, dev)
+    if args.pmc_pass == "denoise":
+        return pmc_pass_denoise(args, dev)
     log(f"device {torch.cuda.get_device_name(dev)}; building state M={m} K={k} N={n} r={r} g={g}")
     x, ds, prep = make_layer(n, k, m, r, g, dev, seed=1)
     opc = ops.OPERAND_NAMES[args.operand]
