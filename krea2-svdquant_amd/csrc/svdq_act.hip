@@ -338,8 +338,8 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
 // Final low-rank operand of the GEMM epilogue: the split partials summed in split order
 // (a fixed order, so the result is deterministic), then split into bf16 hi and lo planes
 // [M, 2, RTp] (the bf16 MFMA operands of mid @ l1cat^T).  One thread per 8 columns of a row.
-__global__ void mid_finalize_kernel(const float* __restrict__ part, int S, int M, int RTp,
-                                    uint16_t* __restrict__ midp) {
+__global__ void __launch_bounds__(256) mid_finalize_kernel(const float* __restrict__ part, int S, int M,
+                                                           int RTp, uint16_t* __restrict__ midp) {
   const int chunks = RTp / 8;
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)M * chunks) return;
@@ -347,10 +347,23 @@ __global__ void mid_finalize_kernel(const float* __restrict__ part, int S, int M
   const int c = (int)(idx % chunks);
   const long plane = (long)M * RTp;
   const float* src = part + m * RTp + 8 * c;
+  // the partials are loaded four splits at a time (past the last split the last one again, not
+  // added), then added in split order
   f32x4 v0 = *reinterpret_cast<const f32x4*>(src), v1 = *reinterpret_cast<const f32x4*>(src + 4);
-  for (int s = 1; s < S; ++s) {
-    v0 += *reinterpret_cast<const f32x4*>(src + s * plane);
-    v1 += *reinterpret_cast<const f32x4*>(src + s * plane + 4);
+  for (int s0 = 1; s0 < S; s0 += 4) {
+    f32x4 a0[4], a1[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const long o = (long)min(s0 + j, S - 1) * plane;
+      a0[j] = *reinterpret_cast<const f32x4*>(src + o);
+      a1[j] = *reinterpret_cast<const f32x4*>(src + o + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (s0 + j < S) {
+        v0 += a0[j];
+        v1 += a1[j];
+      }
   }
   const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
   u32x4 hi, lo;

@@ -48,3 +48,20 @@ def test_async_load_kernels_do_not_spill():
     bad = {k: v for k, v in checked.items()
            if v.get("private_segment_fixed_size", -1) != 0 or v.get("vgpr_spill_count", -1) != 0}
     assert not bad, f"kernels with in-flight asm loads spill: {bad}"
+
+
+# Kernels on the denoise step's path (every group-64 activation pass, the grouped GEMM, the
+# attention and the streaming passes around them): a spill there (a mis-sized register array, a
+# loop the compiler could not keep in registers) costs more than it saves.
+NO_SCRATCH_KERNELS = ("mid_finalize_kernel", "gate_op_kernel", "rms_norm_modulate_kernel", "head_rms_rope",
+                      "attn_fast_kernel", "attn_combine_kernel", "act_kernelILi64E", "w4a4_e3m2_siblings_kernel")
+
+
+@pytest.mark.skipif(not LIB.exists(), reason="library not built")
+def test_streaming_kernels_use_no_scratch():
+    meta = _kernel_metadata()
+    checked = {k: v for k, v in meta.items() if any(s in k for s in NO_SCRATCH_KERNELS)}
+    assert len(checked) >= 12, f"expected the kernels in the metadata, found {sorted(meta)[:5]}..."
+    bad = {k: v for k, v in checked.items()
+           if v.get("private_segment_fixed_size", -1) != 0 or v.get("vgpr_spill_count", -1) != 0}
+    assert not bad, f"kernels with scratch or spills: {bad}"
