@@ -273,7 +273,7 @@ int svdq_head_rms_rope(const void* t, int T, int heads, const void* cos, const v
  *   o[t, h, :] = sum_u softmax_u(scale * q[t, h, :] . k[u, h / (H / Hkv), :]) v[u, h / (H / Hkv), :]
  * q, o: bf16 rows of H heads x 128 with row strides ldq, ldo; k, v: bf16 rows of Hkv heads x 128
  * with row stride ldkv (elements; multiples of 8, pointers 16-byte aligned, o not overlapping the
- * inputs).  Scores and softmax statistics float32, probabilities rounded to bf16 for the product
+ * inputs; T * ldkv * 2 below 2^31 bytes).  Scores and softmax statistics float32, probabilities rounded to bf16 for the product
  * with v, o rounded to bf16 once.  workspace: svdq_attention_workspace(T, H) bytes of device memory,
  * 16-byte aligned, no initial contents (the call's kernels share it on the stream; overlapping
  * calls need separate workspaces).  No counterpart in the reference: its blocks run in diffusers

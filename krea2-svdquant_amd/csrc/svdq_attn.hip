@@ -135,46 +135,45 @@ struct AttnArgs {
 // 4 (t % 16) .. + 3 -- four keys whose V^T positions are adjacent -- at d chunk t / 16, and stores
 // each of its 8 d rows' four values as one 8-byte write: a wave's 64 lanes then cover all 64 keys
 // of 4 d rows (at most a 2-way bank conflict), where scattered 2-byte writes conflicted 8 ways.
-// Keys past T read key T - 1; the scores mask them.
+// Loads are buffer loads whose resource starts at the tile's first key and holds the keys up to
+// T: the byte offsets of a thread's rows are the same for every tile (no address arithmetic per
+// tile on the VALU), and keys past T read 0 (the hardware's range check); the scores mask them.
 struct TileStaging {
-  const uint16_t* kb;   // the KV head's K, this thread's first row and d chunk
-  const uint16_t* vb;   // the KV head's V, this thread's first row and d chunk
+  const uint16_t* k;
+  const uint16_t* v;
   long ld;
-  int T, krow, vkey, kst, vst;
+  int T, rowb;          // rowb: bytes per key row
+  int kvo, vvo;         // byte offsets of this thread's first K chunk and V chunk within a tile
+  int kst, vst;
   u32x4 kr[4], vr[4];
   __device__ __forceinline__ TileStaging(const AttnArgs& p, int kvh, int tid) {
     const int vkg = tid & 15, vc = tid >> 4;
+    const int krow = tid >> 4, vkey = 4 * vkg;
+    k = p.k;
+    v = p.v;
     ld = p.ldkv;
     T = p.T;
-    krow = tid >> 4;
-    vkey = 4 * vkg;
-    kb = p.k + (long)kvh * AD + 8 * (tid & 15) + krow * ld;
-    vb = p.v + (long)kvh * AD + 8 * vc + vkey * ld;
+    rowb = 2 * (int)p.ldkv;
+    kvo = 2 * (krow * (int)p.ldkv + kvh * AD + 8 * (tid & 15));
+    vvo = 2 * (vkey * (int)p.ldkv + kvh * AD + 8 * vc);
     kst = krow * KPITCH + 16 * (tid & 15);
     // V^T byte column of key 4 vkg: slice vkg / 4, first position of keys 4 (vkg % 4) .. + 3
     vst = 8 * vc * VPITCH + 2 * (16 * (vkg >> 2) + slice_pos(4 * (vkg & 3)));
   }
-  // rows of tile j: whole tiles step the row pointers by 64 rows (uniform offsets); the last,
-  // partial tile clamps each row to T - 1
+  // the keys j * ABN .. T - 1 of a tensor as a raw buffer (stride 0, T * ldkv * 2 < 2^31 bytes)
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t keys_from(const uint16_t* base, int j) const {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base) + (long)j * ABN * ld, (short)0,
+                                             (T - j * ABN) * rowb, 0x00020000);
+  }
   __device__ __forceinline__ void load_k(int j) {
-    if ((j + 1) * ABN <= T) {
-      const uint16_t* src = kb + (long)j * ABN * ld;
+    const __amdgpu_buffer_rsrc_t r = keys_from(k, j);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[i] = ld16(src + 16 * i * ld);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) kr[i] = ld16(kb + (long)(min(j * ABN + krow + 16 * i, T - 1) - krow) * ld);
-    }
+    for (int i = 0; i < 4; ++i) kr[i] = __builtin_amdgcn_raw_buffer_load_b128(r, kvo + 16 * i * rowb, 0, 0);
   }
   __device__ __forceinline__ void load_v(int j) {
-    if ((j + 1) * ABN <= T) {
-      const uint16_t* src = vb + (long)j * ABN * ld;
+    const __amdgpu_buffer_rsrc_t r = keys_from(v, j);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vr[i] = ld16(src + i * ld);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vr[i] = ld16(vb + (long)(min(j * ABN + vkey + i, T - 1) - vkey) * ld);
-    }
+    for (int i = 0; i < 4; ++i) vr[i] = __builtin_amdgcn_raw_buffer_load_b128(r, vvo + i * rowb, 0, 0);
   }
   __device__ __forceinline__ void store_k(uint8_t* sk) const {
 #pragma unroll

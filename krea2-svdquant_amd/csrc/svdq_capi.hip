@@ -485,6 +485,9 @@ int svdq_attention_fwd(const void* q, int64_t ldq, const void* k, const void* v,
     return fail(SVDQ_ERR_SHAPE, "attention_fwd: row strides ldq=%lld ldkv=%lld ldo=%lld below the heads' width",
                 (long long)ldq, (long long)ldkv, (long long)ldo);
   if (!(scale > 0.0f) || !(scale < 1e30f)) return fail(SVDQ_ERR_ARG, "attention_fwd: scale must be positive and finite");
+  if ((int64_t)T * ldkv * 2 > INT32_MAX)   // the kernels address K and V as buffers of 32-bit byte offsets
+    return fail(SVDQ_ERR_SHAPE, "attention_fwd: T * ldkv * 2 = %lld bytes of K or V exceed 2^31 - 1",
+                (long long)T * ldkv * 2);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || ldq % 8 || ldkv % 8 || ldo % 8)
     return fail(SVDQ_ERR_ALIGN, "attention_fwd: pointers must be 16-byte aligned and row strides multiples of 8");
   return launched(svdq::launch_attention_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
