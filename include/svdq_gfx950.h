@@ -209,9 +209,9 @@ int svdq_w4a16_gemm_epi(const void* xhat, int64_t ldxh, const void* qw, const vo
 /* Sibling linears in one launch: up to SVDQ_MAX_SIBLINGS W4A4 GEMMs over the same activation rows
  * (same M, K and group; each layer with its own operands, scales, low-rank factors, bias and
  * output), e.g. attn.to_q / to_k / to_v / to_gate or ff.gate / ff.up of one block.  The reference
- * calls such layers one after another, each through SVDQuantLinear.forward
- * (runtime/linear.py:156-161; the layer names are in README.md:41-51); each output here equals
- * svdq_w4a4_gemm's for that layer bit for bit.  With SVDQ_OPERAND_E3M2, group 64 or 128 and
+ * calls such layers one after another, each through SVDQuantLinear.forward (reference
+ * runtime/linear.py:156-161; the layer names: reference README.md:41-51); each output here
+ * equals svdq_w4a4_gemm's for that layer bit for bit.  With SVDQ_OPERAND_E3M2, group 64 or 128 and
  * K % 512 == 0 the layers' output tiles run in one launch, so that the tiles of small layers
  * and the last partial round of workgroups of each layer share the CUs; otherwise the layers are
  * launched one after another on `stream`.
