@@ -60,6 +60,9 @@ const char* svdq_version(void);
 /* Message for the most recent failing call on this host thread ("" if none). */
 const char* svdq_last_error(void);
 
+/* Most layers of one sibling call (svdq_act_quant_siblings, svdq_w4a4_gemm_siblings). */
+#define SVDQ_MAX_SIBLINGS 4
+
 /* Group sizes with kernels in this build; returns 1 if `group` is supported: any positive
  * multiple of 16 (the reference quantizer takes any group, quant/pack.py:6-23; its own test uses
  * 16, tests/test_svd_linear_cpu.py:10).  64 and 128 have the tuned kernels and every operand
@@ -112,6 +115,27 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
                    const void* lora_down, int rl, const float* lora_mult, int M, int K, int group,
                    int RTp, unsigned flags, void* qa, void* sx, void* qx, void* xhat, int64_t ldxh,
                    float* mid, int splits, hipStream_t stream);
+
+/* The activation passes of sibling layers over the same x (e.g. attn.to_q / to_k / to_v / to_gate,
+ * whose smoothing vectors differ, so each has its own codes): each layer's output equals
+ * svdq_act_quant(x, ..., layer's srs, l2, r, no LoRA, ...) bit for bit.  With flags =
+ * SVDQ_ACT_OPERAND_E3M2 | SVDQ_ACT_SX_PAIRS, group 64 or 128 and every r <= 32 the layers run as
+ * one launch and their finalize as one more; otherwise svdq_act_quant per layer, in order.  The
+ * reference quantizes each layer's input in its own forward (quant/svd.py:121-122,
+ * quant/pack.py:6-23 through runtime/linear.py:156-161).
+ *   layers[i]: srs, l2 [r, K] and r of the layer; its qa, sx (as in svdq_act_quant) and mid
+ *              workspace of svdq_act_quant_workspace(M, K, group, RTp) floats
+ *   RTp, splits: shared (one svdq_act_quant_workspace query) */
+typedef struct svdq_act_sibling {
+  const float* srs;
+  const void* l2;
+  int r;
+  void* qa;
+  void* sx;
+  float* mid;
+} svdq_act_sibling;
+int svdq_act_quant_siblings(const void* x, int64_t ldx, const svdq_act_sibling* layers, int count, int M, int K,
+                            int group, int RTp, unsigned flags, int splits, hipStream_t stream);
 
 /* Largest split-partial buffer of svdq_act_quant_noalloc, in floats (16 MiB): S * M * RTp must
  * not exceed it (S from svdq_act_quant_workspace). */
@@ -217,7 +241,6 @@ int svdq_w4a16_gemm_epi(const void* xhat, int64_t ldxh, const void* qw, const vo
  * launched one after another on `stream`.
  *   layers[i]: the per-layer arguments of svdq_w4a4_gemm (qa and sxp from that layer's own
  *              svdq_act_quant: the smoothing differs per layer), with out_f32 = 0 or 1 for all. */
-#define SVDQ_MAX_SIBLINGS 4
 typedef struct svdq_w4a4_sibling {
   const void* qa;
   const void* sxp;

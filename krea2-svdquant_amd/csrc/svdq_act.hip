@@ -98,7 +98,7 @@ __device__ __forceinline__ void smooth64_exact(const u32x4 (&xr)[8], cfloat_ptr 
 // further launches with OPER 0 and no XHAT (down projections only), each writing its own columns
 // of the split partials.
 template <int G, int NT, int OPER, bool XHAT, bool QX, bool LX>
-__global__ void __launch_bounds__(256) act_kernel(ActParams p) {
+__device__ __forceinline__ void act_tile(const ActParams& p) {
   constexpr int HB = G / 64;             // 64-column blocks per group
   constexpr bool QUANT = OPER != 0;
   __shared__ __attribute__((aligned(16))) float red[4 * 64 * 32];
@@ -335,11 +335,24 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
 
 }
 
+template <int G, int NT, int OPER, bool XHAT, bool QX, bool LX>
+__global__ void __launch_bounds__(256) act_kernel(ActParams p) {
+  act_tile<G, NT, OPER, XHAT, QX, LX>(p);
+}
+
+// Sibling layers' activation passes over the same x in one launch (blockIdx.z = the layer):
+// e3m2 codes, rank tiles of the low-rank down projection only (r <= 32), each layer with its own
+// smoothing constants, factors and outputs.
+template <int G>
+__global__ void __launch_bounds__(256) act_siblings_kernel(ActSiblings s) {
+  act_tile<G, 1, 3, false, false, false>(s.layer[blockIdx.z]);
+}
+
 // Final low-rank operand of the GEMM epilogue: the split partials summed in split order
 // (a fixed order, so the result is deterministic), then split into bf16 hi and lo planes
 // [M, 2, RTp] (the bf16 MFMA operands of mid @ l1cat^T).  One thread per 8 columns of a row.
-__global__ void __launch_bounds__(256) mid_finalize_kernel(const float* __restrict__ part, int S, int M,
-                                                           int RTp, uint16_t* __restrict__ midp) {
+__device__ __forceinline__ void mid_finalize_rows(const float* __restrict__ part, int S, int M, int RTp,
+                                                  uint16_t* __restrict__ midp) {
   const int chunks = RTp / 8;
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)M * chunks) return;
@@ -371,6 +384,17 @@ __global__ void __launch_bounds__(256) mid_finalize_kernel(const float* __restri
   uint16_t* dst = midp + m * 2 * RTp + 8 * c;
   *reinterpret_cast<u32x4*>(dst) = hi;
   *reinterpret_cast<u32x4*>(dst + RTp) = lo;
+}
+
+__global__ void __launch_bounds__(256) mid_finalize_kernel(const float* __restrict__ part, int S, int M, int RTp,
+                                                           uint16_t* __restrict__ midp) {
+  mid_finalize_rows(part, S, M, RTp, midp);
+}
+
+// The finalize of sibling layers' passes in one launch (blockIdx.y = the layer).
+__global__ void __launch_bounds__(256) mid_finalize_siblings_kernel(ActSiblings s, int S) {
+  const ActParams& p = s.layer[blockIdx.y];
+  mid_finalize_rows(p.mid, S, p.M, p.RTp, s.head[blockIdx.y]);
 }
 
 // A4 quantizer for any group size G (a multiple of 16 dividing K), from x_hat (written by the act
@@ -488,6 +512,22 @@ hipError_t launch_act(const ActParams& p, int G, int nt, int oper, bool xhat, in
   if (G == 64) return launch_act_g<64>(p, nt, oper, xhat, grid, st);
   if (G == 128) return launch_act_g<128>(p, nt, oper, xhat, grid, st);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_act_siblings(const ActSiblings& s, int G, int splits, hipStream_t st) {
+  if (s.count < 1 || s.count > MAX_SIBLINGS) return hipErrorInvalidValue;
+  for (int i = 0; i < s.count; ++i)
+    if (s.layer[i].M != s.layer[0].M || s.layer[i].K != s.layer[0].K || s.layer[i].r > 32 || s.layer[i].rl ||
+        s.layer[i].t0)
+      return hipErrorInvalidValue;
+  const dim3 grid((s.layer[0].M + 63) / 64, splits, s.count);
+  if (G == 64) act_siblings_kernel<64><<<grid, 256, 0, st>>>(s);
+  else if (G == 128) act_siblings_kernel<128><<<grid, 256, 0, st>>>(s);
+  else return hipErrorInvalidValue;
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  const long n = (long)s.layer[0].M * (s.layer[0].RTp / 8);
+  mid_finalize_siblings_kernel<<<dim3((unsigned)((n + 255) / 256), s.count), 256, 0, st>>>(s, splits);
+  return hipGetLastError();
 }
 
 hipError_t launch_mid_finalize(const float* part, int S, int M, int RTp, uint16_t* midp, hipStream_t st) {

@@ -89,7 +89,8 @@ namespace {
 int act_quant_run(const void* x, int64_t ldx, const float* srs, const void* l2, int r, const void* lora_down,
                   int rl, const float* lora_mult, int M, int K, int group, int RTp, unsigned flags, void* qa,
                   void* sx, void* qx, void* xhat, int64_t ldxh, float* head, float* part, int splits,
-                  hipStream_t stream) {
+                  hipStream_t stream, svdq::ActParams* checked = nullptr) {
+  // checked: validate only, and return the launch parameters of the first launch instead
   const unsigned known = SVDQ_ACT_PACKED | SVDQ_ACT_XHAT | SVDQ_ACT_EXACT_DIV | SVDQ_ACT_OPERAND_E4M3 |
                          SVDQ_ACT_OPERAND_I8 | SVDQ_ACT_SX_PAIRS | SVDQ_ACT_OPERAND_E3M2;
   if (flags & ~known) return fail(SVDQ_ERR_ARG, "act_quant: unknown flags 0x%x", flags);
@@ -150,6 +151,11 @@ int act_quant_run(const void* x, int64_t ldx, const float* srs, const void* l2, 
   p.gps = (ngroups + splits - 1) / splits;
   p.exact = (flags & SVDQ_ACT_EXACT_DIV) ? 1 : 0;
   p.sx_pairs = pairs ? 1 : 0;
+  if (checked) {
+    p.t0 = 0;
+    *checked = p;
+    return SVDQ_OK;
+  }
   // The first launch quantizes and computes the first 4 column tiles; each further launch adds 4
   // more tiles of the down projections (rank + LoRA rank beyond 128), into their own columns of
   // the split partials.
@@ -232,6 +238,38 @@ int svdq_act_quant(const void* x, int64_t ldx, const float* srs, const void* l2,
   float* part = mid ? mid + (int64_t)(M > 0 ? M : 0) * (RTp > 0 ? RTp : 0) : nullptr;   // partials after the head
   return act_quant_run(x, ldx, srs, l2, r, lora_down, rl, lora_mult, M, K, group, RTp, flags, qa, sx, qx, xhat,
                        ldxh, mid, part, splits, stream);
+}
+
+int svdq_act_quant_siblings(const void* x, int64_t ldx, const svdq_act_sibling* layers, int count, int M, int K,
+                            int group, int RTp, unsigned flags, int splits, hipStream_t stream) {
+  if (!layers) return fail(SVDQ_ERR_ARG, "act_quant_siblings: null layer array");
+  if (count < 1 || count > SVDQ_MAX_SIBLINGS)
+    return fail(SVDQ_ERR_ARG, "act_quant_siblings: count=%d, must be 1..%d", count, SVDQ_MAX_SIBLINGS);
+  bool one = fast_group(group) && flags == (SVDQ_ACT_OPERAND_E3M2 | SVDQ_ACT_SX_PAIRS);
+  for (int i = 0; i < count; ++i) one = one && layers[i].r >= 1 && layers[i].r <= 32;
+  if (!one) {   // other formats, flags, groups or ranks: one svdq_act_quant per layer, in order
+    for (int i = 0; i < count; ++i) {
+      const svdq_act_sibling& l = layers[i];
+      if (int e = svdq_act_quant(x, ldx, l.srs, l.l2, l.r, nullptr, 0, nullptr, M, K, group, RTp, flags, l.qa, l.sx,
+                                 nullptr, nullptr, 0, l.mid, splits, stream))
+        return e;
+    }
+    return SVDQ_OK;
+  }
+  const int expect = svdq::act_splits(M, K, group);
+  if (M > 0 && splits != expect)
+    return fail(SVDQ_ERR_ARG, "act_quant_siblings: splits=%d, workspace says %d", splits, expect);
+  svdq::ActSiblings s{};
+  s.count = count;
+  for (int i = 0; i < count; ++i) {
+    const svdq_act_sibling& l = layers[i];
+    float* part = l.mid ? l.mid + (int64_t)(M > 0 ? M : 0) * (RTp > 0 ? RTp : 0) : nullptr;
+    if (int e = act_quant_run(x, ldx, l.srs, l.l2, l.r, nullptr, 0, nullptr, M, K, group, RTp, flags, l.qa, l.sx,
+                              nullptr, nullptr, 0, l.mid, part, splits, stream, &s.layer[i]))
+      return e;
+    s.head[i] = reinterpret_cast<uint16_t*>(l.mid);
+  }
+  return launched(svdq::launch_act_siblings(s, group, splits, stream), "act_quant_siblings");
 }
 
 int svdq_act_quant_noalloc(const void* x, int64_t ldx, const float* srs, const void* l2, int r,

@@ -62,6 +62,16 @@ struct GemmSiblings {
   int tile0[MAX_SIBLINGS + 1];
 };
 
+// Activation passes of up to MAX_SIBLINGS layers over the same x (same M, K, group, RTp and
+// splits; e3m2 codes with sx pairs, rank r <= 32, no LoRA tiles) as one launch, then one finalize
+// launch: layer[i] as for launch_act (mid = the split partials), head[i] = its finalized operand.
+struct ActSiblings {
+  ActParams layer[MAX_SIBLINGS];
+  uint16_t* head[MAX_SIBLINGS];
+  int count;
+};
+hipError_t launch_act_siblings(const ActSiblings& s, int G, int splits, hipStream_t st);
+
 int act_splits(int M, int K, int G);
 // oper: 0 = no codes (x_hat only), 1 = e4m3 operand codes, 2 = int8 16*q operand codes, 3 = e3m2;
 // nt: column tiles of the down projections from p.t0 (at most 4); with p.t0 > 0 the launch computes

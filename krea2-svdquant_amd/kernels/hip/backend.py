@@ -231,8 +231,9 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
 def forward_prepared_siblings(x: Tensor, preps: Sequence[PreparedLayer], *, out_f32: bool = False,
                               exact_div: bool = False, operand: str = "e3m2") -> list[Tensor]:
     """W4A4 forwards of sibling layers (same input ``x``, same K and group size) on prepared
-    operands: one activation pass per layer (each layer has its own smoothing), then the layers'
-    GEMMs as one launch (``svdq::w4a4_gemm_siblings``).  Every output is bit-identical to
+    operands: an activation pass per layer (each layer has its own smoothing; one launch for all
+    when none has LoRA adapters, ``svdq::act_quant_siblings``), then the layers' GEMMs as one
+    launch (``svdq::w4a4_gemm_siblings``).  Every output is bit-identical to
     ``forward_prepared(x, prep)`` of its layer."""
     if not x.is_cuda:
         raise RuntimeError("HIP gfx950 backend needs a GPU tensor")
@@ -256,8 +257,14 @@ def forward_prepared_siblings(x: Tensor, preps: Sequence[PreparedLayer], *, out_
         raise ValueError(f"activation K={x2.shape[1]} exceeds packed weight K={p0.kp}")
     if x2.shape[1] != p0.kp:
         x2 = _pad_cols(x2, p0.kp)
-    acts = [ops.act_quant(x2, p.srs, p.l2, p.lora_down, p.lora_mult, p.group_size, p.rtp, opc, False, False,
-                          exact_div, True) for p in preps]
+    if opc == ops.OPERAND_E3M2 and all(p.lora_down is None and p.rtp == p0.rtp for p in preps):
+        # one activation-pass launch for the layers (each its own smoothing) and one finalize
+        flat = ops.act_quant_siblings(x2, [p.srs for p in preps], [p.l2 for p in preps], p0.group_size, p0.rtp,
+                                      exact_div)
+        acts = [(flat[3 * i], flat[3 * i + 1], None, None, flat[3 * i + 2]) for i in range(len(preps))]
+    else:
+        acts = [ops.act_quant(x2, p.srs, p.l2, p.lora_down, p.lora_mult, p.group_size, p.rtp, opc, False, False,
+                              exact_div, True) for p in preps]
     ys = ops.w4a4_gemm_siblings([a[0] for a in acts], [a[1] for a in acts], [p.weight_operand(opc) for p in preps],
                                 [p.weight_scale_pairs(opc) for p in preps], [a[4] for a in acts],
                                 [p.l1cat for p in preps], [p.bias for p in preps], p0.group_size, opc, out_f32)

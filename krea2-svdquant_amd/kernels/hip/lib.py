@@ -45,6 +45,11 @@ _L = ctypes.c_int64
 _U = ctypes.c_uint
 
 
+class ActSibling(ctypes.Structure):
+    """``svdq_act_sibling``: one layer of ``svdq_act_quant_siblings``."""
+    _fields_ = [("srs", _P), ("l2", _P), ("r", _I), ("qa", _P), ("sx", _P), ("mid", _P)]
+
+
 class W4A4Sibling(ctypes.Structure):
     """``svdq_w4a4_sibling``: one layer of ``svdq_w4a4_gemm_siblings``."""
     _fields_ = [("qa", _P), ("sxp", _P), ("qwe", _P), ("swp", _P), ("mid", _P), ("l1cat", _P), ("RTp", _I),
@@ -70,6 +75,7 @@ SIGNATURES = {
                                 _I, _P, _L, _P, _P]),
     "svdq_w4a16_gemm_epi": (_I, [_P, _L, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I,
                                  _I, _P, _L, _P, _P]),
+    "svdq_act_quant_siblings": (_I, [_P, _L, ctypes.POINTER(ActSibling), _I, _I, _I, _I, _I, _U, _I, _P]),
     "svdq_w4a4_gemm_siblings": (_I, [ctypes.POINTER(W4A4Sibling), _I, _I, _I, _I, _I, _I, _P]),
     "svdq_gate_op": (_I, [_I, _P, _P, _P, _L, _P]),
     "svdq_rms_norm_modulate": (_I, [_P, _L, _P, _P, _I, _I, ctypes.c_float, _P, _L, _P]),

@@ -184,6 +184,53 @@ def _(x, srs, l2, lora_down, lora_mult, group_size, rtp, operand, packed, want_x
 _split_cache: dict[tuple[int, int, int, int], int] = {}
 
 
+@torch.library.custom_op("svdq::act_quant_siblings", mutates_args=())
+def act_quant_siblings(x: Tensor, srs: list[Tensor], l2: list[Tensor], group_size: int, rtp: int,
+                       exact: bool) -> list[Tensor]:
+    """``act_quant(x, srs[i], l2[i], None, None, group_size, rtp, OPERAND_E3M2, False, False, exact,
+    True)`` for sibling layers i over the same x (no LoRA), as one launch when every rank is at most
+    32 and the group 64 or 128 (``svdq_act_quant_siblings``).  Returns ``[qa_0, sx_0, mid_0, qa_1,
+    ...]``, each bit-identical to that layer's ``act_quant``."""
+    _need(x.is_cuda, RuntimeError, "svdq::act_quant_siblings needs a GPU tensor")
+    count = len(srs)
+    _need(1 <= count <= lib.SVDQ_MAX_SIBLINGS and len(l2) == count, ValueError,
+          f"1..{lib.SVDQ_MAX_SIBLINGS} layers with one srs and one l2 each")
+    dev = x.device
+    _need(x.dim() == 2, ValueError, f"x must be 2-D [M, K], got {tuple(x.shape)}")
+    _check_dev("x", x, dev, torch.bfloat16)
+    m, k = x.shape
+    _need(k % group_size == 0, ValueError, f"K={k} must be a multiple of group_size={group_size}")
+    for i in range(count):
+        _check_dev(f"srs[{i}]", srs[i], dev, torch.float32)
+        _need(srs[i].numel() == 2 * k, ValueError, f"srs[{i}] has {srs[i].numel()} elements, expected {2 * k}")
+        _check_dev(f"l2[{i}]", l2[i], dev, torch.bfloat16)
+        _need(l2[i].dim() == 2 and l2[i].shape[1] == k, ValueError, f"l2[{i}] must be [r, {k}]")
+    splits = _splits(m, k, group_size, rtp)
+    outs, arr = [], (lib.ActSibling * count)()
+    for i in range(count):
+        qa = torch.empty(_operand_shape(m, k, OPERAND_E3M2), dtype=torch.uint8, device=dev)
+        sx = torch.empty((k // group_size, m), dtype=torch.int32, device=dev)
+        mid = torch.empty((splits + 1, m, rtp), dtype=torch.float32, device=dev)
+        arr[i] = lib.ActSibling(srs[i].data_ptr(), l2[i].data_ptr(), l2[i].shape[0], qa.data_ptr(), sx.data_ptr(),
+                                mid.data_ptr())
+        outs += [qa, sx, mid]
+    flags = lib.SVDQ_ACT_OPERAND_E3M2 | lib.SVDQ_ACT_SX_PAIRS | (lib.SVDQ_ACT_EXACT_DIV if exact else 0)
+    lib.call("svdq_act_quant_siblings", _vp(x), k, arr, count, m, k, group_size, rtp, flags, splits, _stream(dev))
+    return outs
+
+
+@act_quant_siblings.register_fake
+def _(x, srs, l2, group_size, rtp, exact):
+    m, k = x.shape
+    splits = _splits(m, k, group_size, rtp)
+    out = []
+    for _i in range(len(srs)):
+        out += [x.new_empty(_operand_shape(m, k, OPERAND_E3M2), dtype=torch.uint8),
+                x.new_empty((k // group_size, m), dtype=torch.int32),
+                x.new_empty((splits + 1, m, rtp), dtype=torch.float32)]
+    return out
+
+
 def _splits(m: int, k: int, group_size: int, rtp: int) -> int:
     """Number of K splits the activation pass uses for this shape (leading dim of ``mid``)."""
     key = (m, k, group_size, rtp)

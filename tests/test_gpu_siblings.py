@@ -125,3 +125,29 @@ def test_run_grouped_modules_and_standin(dev):
         b = model.denoise_step(text, latent, dt=-0.125, fused=fused, siblings="grouped")
         torch.cuda.synchronize()
         assert torch.equal(a, b), f"fused={fused}"
+
+
+@pytest.mark.parametrize("group,exact", [(64, False), (128, False), (64, True)])
+def test_act_quant_siblings_match_per_layer_passes(dev, group, exact):
+    """One launch of the siblings' activation passes (and one finalize): codes, scale pairs and the
+    whole mid workspace (finalized head and split partials) bit-identical to each layer's own pass;
+    ranks above 32 take the per-layer path inside the C-ABI, with the same results."""
+    from krea2_svdquant_amd.kernels.hip import ops
+    from krea2_svdquant_amd.runtime.krea2_standin import random_quantized_state
+    from krea2_svdquant_amd.kernels.hip.backend import prepare_layer
+    gen = torch.Generator(device=dev).manual_seed(group + exact)
+    k = 1024
+    for rank, ns in ((32, (512, 128, 256, 64)), (64, (256, 128))):
+        preps = [prepare_layer(random_quantized_state(n, k, rank=rank, group_size=group, device=dev, generator=gen))
+                 for n in ns]
+        rtp = preps[0].rtp
+        for m in (300, 64, 4352):
+            x = (torch.randn(m, k, device=dev, generator=gen) * 2).to(torch.bfloat16)
+            flat = ops.act_quant_siblings(x, [p.srs for p in preps], [p.l2 for p in preps], group, rtp, exact)
+            for i, p in enumerate(preps):
+                qa, sx, _, _, mid = ops.act_quant(x, p.srs, p.l2, None, None, group, rtp, ops.OPERAND_E3M2, False,
+                                                  False, exact, True)
+                assert torch.equal(flat[3 * i], qa), f"r={rank} m={m} layer {i}: codes"
+                assert torch.equal(flat[3 * i + 1], sx), f"r={rank} m={m} layer {i}: scale pairs"
+                assert torch.equal(flat[3 * i + 2].view(torch.int32), mid.view(torch.int32)), \
+                    f"r={rank} m={m} layer {i}: mid workspace"
