@@ -306,6 +306,16 @@ int64_t svdq_attention_workspace(int T, int H);
 int svdq_attention_fwd(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv, int T, int H,
                        int Hkv, float scale, void* o, int64_t ldo, void* workspace, hipStream_t stream);
 
+/* svdq_attention_fwd with the block's per-head RMS norm and rotary embedding of q applied on load
+ * (as svdq_head_rms_rope(q, ...) followed by svdq_attention_fwd, without the normalized copy of q;
+ * a normalized value can differ by one bf16 ulp where the float32 mean of squares, summed in
+ * another order, sits at a rounding boundary).  cos / sin: bf16 [T, ldcs] position tables
+ * (columns 0..63 read), 16-byte aligned, ldcs % 8 == 0; eps >= 0.  No counterpart in the
+ * reference (its blocks run in diffusers). */
+int svdq_attention_fwd_qnorm(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv, int T, int H,
+                             int Hkv, float scale, const void* cos, const void* sin, int64_t ldcs, float eps, void* o,
+                             int64_t ldo, void* workspace, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

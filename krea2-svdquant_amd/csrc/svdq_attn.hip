@@ -128,7 +128,58 @@ struct AttnArgs {
   float* part_o;     // [tail * split, 256, 128] unnormalized partial outputs of the pieces
   float* part_ml;    // [tail * split, 256, 2]: exponent offset (log2 units), row sum
   int* part_flag;    // [tail * split, 4]: a piece's wave past the offset limit
+  // optional per-head RMS norm + rotary embedding of q on load (null qcos: q is used as given)
+  const uint16_t* qcos;
+  const uint16_t* qsin;
+  long ldcs;
+  float qeps;
 };
+
+// Q^T fragments of query row qc for lane half h: fragment s holds d = 16 s + 8 h .. + 7.  With
+// rotary tables, the row is first normalized per head and rotated as the block's head norm does
+//   n = bf16(q * rsqrt(mean(q^2) + eps));  (n1, n2) = (n[j], n[j + 64]):
+//   o1 = bf16(fma(-n2, sin, bf16(n1 cos))),  o2 = bf16(fma(n1, sin, bf16(n2 cos)))
+// (j < 64, cos / sin of the query's position): the lane holds both members of its pairs
+// (fragments s and s + 4), and the mean of squares adds the other half's lane (lane ^ 32).  All 64
+// lanes must be active.
+__device__ __forceinline__ void load_q(const AttnArgs& p, long qc, int head, int h, u32x4 (&qf)[AD / 16]) {
+  const uint16_t* qr = p.q + qc * p.ldq + (long)head * AD + 8 * h;
+#pragma unroll
+  for (int s = 0; s < AD / 16; ++s) qf[s] = ld16(qr + 16 * s);
+  if (!p.qcos) return;   // uniform
+  float ss = 0.0f;
+#pragma unroll
+  for (int s = 0; s < AD / 16; ++s)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      ss = __builtin_fmaf(bf16lo(qf[s][d]), bf16lo(qf[s][d]), ss);
+      ss = __builtin_fmaf(bf16hi(qf[s][d]), bf16hi(qf[s][d]), ss);
+    }
+  ss += __shfl_xor(ss, 32, 64);
+  const float r = rsqrtf(ss / 128.0f + p.qeps);
+#pragma unroll
+  for (int s = 0; s < AD / 32; ++s) {
+    const u32x4 c = ld16(p.qcos + qc * p.ldcs + 16 * s + 8 * h), sn = ld16(p.qsin + qc * p.ldcs + 16 * s + 8 * h);
+    u32x4 o1, o2;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      float a1[2], a2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float x1 = e ? bf16hi(qf[s][d]) : bf16lo(qf[s][d]);
+        const float x2 = e ? bf16hi(qf[s + 4][d]) : bf16lo(qf[s + 4][d]);
+        const float cc = e ? bf16hi(c[d]) : bf16lo(c[d]), sv = e ? bf16hi(sn[d]) : bf16lo(sn[d]);
+        const float n1 = round_bf16(x1 * r), n2 = round_bf16(x2 * r);
+        a1[e] = __builtin_fmaf(-n2, sv, round_bf16(n1 * cc));
+        a2[e] = __builtin_fmaf(n1, sv, round_bf16(n2 * cc));
+      }
+      o1[d] = pack_bf16x2(a1[0], a1[1]);
+      o2[d] = pack_bf16x2(a2[0], a2[1]);
+    }
+    qf[s] = o1;
+    qf[s + 4] = o2;
+  }
+}
 
 // Global -> register -> LDS staging of a 64-key tile.  K: chunk idx = tid + 256 i (i = 0..3) is key
 // row tid / 16 + 16 i, 16-byte d chunk tid % 16, stored as is.  V: thread t takes keys
@@ -211,9 +262,7 @@ __global__ void __launch_bounds__(256, 2) attn_safe_kernel(AttnArgs p) {
   // Q^T fragments (B operand): k-step s covers d = 16 s .. 16 s + 15, lane half h d 16 s + 8 h ..
   // (rows past T read row T - 1, never stored)
   u32x4 qf[AD / 16];
-  const long qc = min(qrow, T - 1);
-#pragma unroll
-  for (int s = 0; s < AD / 16; ++s) qf[s] = ld16(p.q + qc * p.ldq + (long)head * AD + 16 * s + 8 * h);
+  load_q(p, min(qrow, T - 1), head, h, qf);
   TileStaging st(p, kvh, tid);
 
   // O^T accumulators: register r of d block db holds d = 32 db + 8 (r / 4) + 4 h + r % 4
@@ -347,11 +396,7 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
 
   u32x4 qf[QB][AD / 16];   // Q^T fragments of query block qb (queries qbase + 32 qb + lr)
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const long qc = min(qbase + 32 * qb + lr, T - 1);
-#pragma unroll
-    for (int s = 0; s < AD / 16; ++s) qf[qb][s] = ld16(p.q + qc * p.ldq + (long)head * AD + 16 * s + 8 * h);
-  }
+  for (int qb = 0; qb < QB; ++qb) load_q(p, min(qbase + 32 * qb + lr, T - 1), head, h, qf[qb]);
   TileStaging st(p, kvh, tid);
 
   f32x16 O[QB][AD / 32];
@@ -711,13 +756,15 @@ AttnWs attn_ws(int T, int H) {
 long attention_workspace_bytes(int T, int H) { return attn_ws(T, H).total; }
 
 hipError_t launch_attention_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int T, int H,
-                                int Hkv, long ldq, long ldkv, long ldo, float scale, void* workspace, hipStream_t st) {
+                                int Hkv, long ldq, long ldkv, long ldo, float scale, void* workspace, hipStream_t st,
+                                const uint16_t* qcos, const uint16_t* qsin, long ldcs, float qeps) {
   const AttnWs w = attn_ws(T, H);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const AttnPlan pl = attn_plan(T, H, ATTN_CUS);
   AttnArgs a{q, k, v, o, reinterpret_cast<int*>(ws + w.flags), pl.nq * 4, T, H, Hkv, ldq, ldkv, ldo,
              scale * 1.4426950408889634f, pl, reinterpret_cast<float*>(ws + w.part_o),
-             reinterpret_cast<float*>(ws + w.part_ml), reinterpret_cast<int*>(ws + w.part_flag)};
+             reinterpret_cast<float*>(ws + w.part_ml), reinterpret_cast<int*>(ws + w.part_flag), qcos, qsin, ldcs,
+             qeps};
   attn_fast_kernel<<<(unsigned)(pl.nmain + pl.tail * pl.split), 256, 0, st>>>(a);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   if (pl.tail) {

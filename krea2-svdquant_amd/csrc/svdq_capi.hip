@@ -513,8 +513,8 @@ int64_t svdq_attention_workspace(int T, int H) {
   return T > 0 && H > 0 ? (int64_t)svdq::attention_workspace_bytes(T, H) : 0;
 }
 
-int svdq_attention_fwd(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv, int T, int H,
-                       int Hkv, float scale, void* o, int64_t ldo, void* workspace, hipStream_t stream) {
+static int attention_checks(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv, int T, int H,
+                            int Hkv, float scale, const void* o, int64_t ldo, const void* workspace) {
   if (!q || !k || !v || !o || !workspace) return fail(SVDQ_ERR_ARG, "attention_fwd: null pointer");
   if (!aligned16(workspace)) return fail(SVDQ_ERR_ALIGN, "attention_fwd: workspace must be 16-byte aligned");
   if (T <= 0 || H <= 0 || Hkv <= 0 || H % Hkv)
@@ -528,10 +528,34 @@ int svdq_attention_fwd(const void* q, int64_t ldq, const void* k, const void* v,
                 (long long)T * ldkv * 2);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || ldq % 8 || ldkv % 8 || ldo % 8)
     return fail(SVDQ_ERR_ALIGN, "attention_fwd: pointers must be 16-byte aligned and row strides multiples of 8");
+  return SVDQ_OK;
+}
+
+int svdq_attention_fwd(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv, int T, int H,
+                       int Hkv, float scale, void* o, int64_t ldo, void* workspace, hipStream_t stream) {
+  if (int e = attention_checks(q, ldq, k, v, ldkv, T, H, Hkv, scale, o, ldo, workspace)) return e;
   return launched(svdq::launch_attention_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                                              static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), T, H, Hkv,
                                              ldq, ldkv, ldo, scale, workspace, stream),
                   "attention_fwd");
+}
+
+int svdq_attention_fwd_qnorm(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv, int T, int H,
+                             int Hkv, float scale, const void* cos, const void* sin, int64_t ldcs, float eps, void* o,
+                             int64_t ldo, void* workspace, hipStream_t stream) {
+  if (!cos || !sin) return fail(SVDQ_ERR_ARG, "attention_fwd_qnorm: null pointer");
+  if (ldcs < 64 || ldcs % 8 || !aligned16(cos) || !aligned16(sin))
+    return fail(SVDQ_ERR_ALIGN, "attention_fwd_qnorm: cos, sin 16-byte aligned, ldcs >= 64 and a multiple of 8");
+  if (!(eps >= 0.0f)) return fail(SVDQ_ERR_ARG, "attention_fwd_qnorm: eps must be >= 0");
+  if (!q || !k || !v || !o || !workspace) return fail(SVDQ_ERR_ARG, "attention_fwd_qnorm: null pointer");
+  // the remaining checks and the launch as svdq_attention_fwd, with the tables
+  if (int e = attention_checks(q, ldq, k, v, ldkv, T, H, Hkv, scale, o, ldo, workspace)) return e;
+  return launched(svdq::launch_attention_fwd(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                                             static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), T, H, Hkv,
+                                             ldq, ldkv, ldo, scale, workspace, stream,
+                                             static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin),
+                                             ldcs, eps),
+                  "attention_fwd_qnorm");
 }
 
 int svdq_w4a16_gemm(const void* xhat, int64_t ldxh, const void* qw, const void* sw, const void* mid,

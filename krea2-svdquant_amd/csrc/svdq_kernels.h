@@ -113,8 +113,12 @@ hipError_t launch_head_rms_rope(const uint16_t* t, int T, int heads, const uint1
                                 long ldcs, float eps, uint16_t* out, hipStream_t st);
 // Stand-in block attention (svdq_attn.hip): softmax(scale q k^T) v, head dimension 128, H query heads
 // over Hkv key / value heads (H % Hkv == 0); rows of q / o hold H heads, rows of k / v Hkv heads
+// qcos / qsin (optional, [T, ldcs] bf16): q is normalized per head and rotated on load (the
+// block's head norm + rotary of q), eps qeps
 hipError_t launch_attention_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int T, int H,
-                                int Hkv, long ldq, long ldkv, long ldo, float scale, void* workspace, hipStream_t st);
+                                int Hkv, long ldq, long ldkv, long ldo, float scale, void* workspace, hipStream_t st,
+                                const uint16_t* qcos = nullptr, const uint16_t* qsin = nullptr, long ldcs = 0,
+                                float qeps = 0.0f);
 long attention_workspace_bytes(int T, int H);
 
 }  // namespace svdq

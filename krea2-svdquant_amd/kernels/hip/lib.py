@@ -84,6 +84,8 @@ SIGNATURES = {
     "svdq_head_rms_rope": (_I, [_P, _I, _I, _P, _P, _L, ctypes.c_float, _P, _P]),
     "svdq_attention_workspace": (_L, [_I, _I]),
     "svdq_attention_fwd": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, ctypes.c_float, _P, _L, _P, _P]),
+    "svdq_attention_fwd_qnorm": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, ctypes.c_float, _P, _P, _L, ctypes.c_float,
+                                      _P, _L, _P, _P]),
 }
 
 _lock = threading.Lock()

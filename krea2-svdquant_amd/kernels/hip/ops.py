@@ -535,11 +535,8 @@ def _(t, cos, sin, eps):
     return torch.empty_like(t)
 
 
-@torch.library.custom_op("svdq::attention", mutates_args=())
-def attention(q: Tensor, k: Tensor, v: Tensor, scale: float) -> Tensor:
-    """Softmax attention ``softmax(scale q k^T) v`` without a mask: ``q`` [T, H, 128], ``k`` / ``v``
-    [T, Hkv, 128] (bf16, H a multiple of Hkv: query head h reads key / value head h // (H // Hkv))
-    -> [T, H, 128] bf16.  Rows may be strided (last two dimensions contiguous)."""
+def _attention(q: Tensor, k: Tensor, v: Tensor, scale: float, cos: Optional[Tensor], sin: Optional[Tensor],
+               eps: float) -> Tensor:
     _need(q.is_cuda, RuntimeError, "svdq::attention needs GPU tensors")
     dev = q.device
     for name, t in (("q", q), ("k", k), ("v", v)):
@@ -560,9 +557,44 @@ def attention(q: Tensor, k: Tensor, v: Tensor, scale: float) -> Tensor:
         k, v = k.contiguous(), v.contiguous()
     out = torch.empty((tok, heads, 128), dtype=torch.bfloat16, device=dev)
     ws = torch.empty(lib.load().svdq_attention_workspace(tok, heads), dtype=torch.uint8, device=dev)
-    lib.call("svdq_attention_fwd", _vp(q), q.stride(0), _vp(k), _vp(v), k.stride(0), tok, heads, kvh,
-             ctypes.c_float(scale), _vp(out), out.stride(0), _vp(ws), _stream(dev))
+    if cos is None:
+        lib.call("svdq_attention_fwd", _vp(q), q.stride(0), _vp(k), _vp(v), k.stride(0), tok, heads, kvh,
+                 ctypes.c_float(scale), _vp(out), out.stride(0), _vp(ws), _stream(dev))
+        return out
+    for name, t in (("cos", cos), ("sin", sin)):
+        _need(t is not None and t.device == dev and t.dtype == torch.bfloat16, TypeError,
+              f"{name} must be a bf16 tensor on {dev}")
+        _need(t.dim() == 2 and t.shape[0] >= tok and t.shape[1] >= 64, ValueError,
+              f"{name} must be [T, >= 64], got {tuple(t.shape)}")
+    cos, sin = (t if t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0 else t.contiguous()
+                for t in (cos, sin))
+    if cos.stride(0) != sin.stride(0):
+        cos, sin = cos.contiguous(), sin.contiguous()
+    lib.call("svdq_attention_fwd_qnorm", _vp(q), q.stride(0), _vp(k), _vp(v), k.stride(0), tok, heads, kvh,
+             ctypes.c_float(scale), _vp(cos), _vp(sin), cos.stride(0), ctypes.c_float(eps), _vp(out), out.stride(0),
+             _vp(ws), _stream(dev))
     return out
+
+
+@torch.library.custom_op("svdq::attention", mutates_args=())
+def attention(q: Tensor, k: Tensor, v: Tensor, scale: float) -> Tensor:
+    """Softmax attention ``softmax(scale q k^T) v`` without a mask: ``q`` [T, H, 128], ``k`` / ``v``
+    [T, Hkv, 128] (bf16, H a multiple of Hkv: query head h reads key / value head h // (H // Hkv))
+    -> [T, H, 128] bf16.  Rows may be strided (last two dimensions contiguous)."""
+    return _attention(q, k, v, scale, None, None, 0.0)
+
+
+@torch.library.custom_op("svdq::attention_qnorm", mutates_args=())
+def attention_qnorm(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, eps: float, scale: float) -> Tensor:
+    """``attention(head_rms_rope(q, cos, sin, eps), k, v, scale)`` with the per-head norm and rotary
+    embedding of q applied as the kernel loads q (no normalized copy of q; a normalized value may
+    differ by one bf16 ulp where the mean of squares sits at a rounding boundary)."""
+    return _attention(q, k, v, scale, cos, sin, eps)
+
+
+@attention_qnorm.register_fake
+def _(q, k, v, cos, sin, eps, scale):
+    return q.new_empty((q.shape[0], q.shape[1], 128))
 
 
 @attention.register_fake

@@ -187,3 +187,15 @@ def test_gate_op_and_siblings_reject_bad_arguments_before_any_launch():
     with pytest.raises(lib.SVDQError) as ei:
         lib.call("svdq_w4a4_gemm_siblings", layers, 2, 2, 256, 1024, 64, 0, None)   # null pointers
     assert ei.value.status == -1 and "null pointer" in str(ei.value)
+
+
+def test_attention_qnorm_rejects_bad_tables_before_any_launch():
+    fake = ctypes.c_void_p(0x1000)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_attention_fwd_qnorm", fake, 1536, fake, fake, 1536, 16, 12, 12, ctypes.c_float(0.1), None,
+                 fake, 64, ctypes.c_float(1e-6), fake, 1536, fake, None)
+    assert ei.value.status == -1
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_attention_fwd_qnorm", fake, 1536, fake, fake, 1536, 16, 12, 12, ctypes.c_float(0.1), fake,
+                 fake, 60, ctypes.c_float(1e-6), fake, 1536, fake, None)
+    assert ei.value.status == -3

@@ -165,3 +165,28 @@ def test_attention_rejects_bad_shapes(dev):
     q2, k2, v2 = _inputs(16, 8, 2, dev, seed=2)
     with pytest.raises(ValueError):
         ops.attention(q2, k2, v2[:8], 0.1)
+
+
+@pytest.mark.parametrize("t,heads,kvh,kscale", [(300, 4, 2, 1.0), (4352, 48, 12, 1.0), (200, 4, 2, 25.0)])
+def test_attention_qnorm_matches_head_norm_then_attention(dev, t, heads, kvh, kscale):
+    """svdq::attention_qnorm (q's per-head norm + rotary applied on load) against
+    svdq::head_rms_rope followed by svdq::attention: the normalized q may differ by one bf16 ulp
+    where the mean of squares sits at a rounding boundary, so the outputs agree to rel-L2 1e-3;
+    both against the float32 evaluation on the normalized q.  kscale 25 drives rows past the fast
+    kernel's offset limit (the running-maximum kernel normalizes q as well)."""
+    from krea2_svdquant_amd.kernels.hip import ops
+    from krea2_svdquant_amd.runtime.krea2_standin import rope_tables
+    gen = torch.Generator(device=dev).manual_seed(t + heads)
+    q = (torch.randn(t, heads, 128, device=dev, generator=gen) * 3).to(torch.bfloat16)
+    k = (torch.randn(t, kvh, 128, device=dev, generator=gen) * kscale).to(torch.bfloat16)
+    v = torch.randn(t, kvh, 128, device=dev, generator=gen).to(torch.bfloat16)
+    cos, sin = rope_tables(t, 128, dev, torch.bfloat16)
+    scale = 1.0 / math.sqrt(128)
+    qn = ops.head_rms_rope(q, cos, sin, 1e-6)
+    ref_path = ops.attention(qn, k, v, scale)
+    got = ops.attention_qnorm(q, k, v, cos, sin, 1e-6, scale)
+    torch.cuda.synchronize()
+    assert got.shape == q.shape and got.dtype == torch.bfloat16
+    assert _rel(got, ref_path.float()) <= 1e-3
+    ref = _reference(qn, k, v, scale)
+    assert _rel(got, ref) <= 4e-3 and _rel(ref_path, ref) <= 4e-3
