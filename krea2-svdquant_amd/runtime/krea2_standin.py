@@ -275,13 +275,9 @@ class Krea2StandInBlock(nn.Module):
             x, h = residual_norm_modulate(x, pending[0], pending[1], scale_a, shift_a, weight=w_a)
         q, g, k, v = siblings_of(h, "attn.to_q", "attn.to_gate", "attn.to_k", "attn.to_v")
         q, k, v = (z.view(t, -1, d.head_dim) for z in (q, k, v))
-        if q.is_cuda and ATTENTION == "hip" and NORMS == "hip":   # q's norm + rotary inside the attention
-            k = head_norm_rope(k, cos, sin)
-            a = hip_ops.attention_qnorm(q, k, v, cos, sin, 1e-6, 1.0 / math.sqrt(d.head_dim)).reshape(t, -1)
-        else:
-            q = head_norm_rope(q, cos, sin)
-            k = head_norm_rope(k, cos, sin)
-            a = attention(q, k, v)                               # [T, heads * head_dim]
+        q = head_norm_rope(q, cos, sin)
+        k = head_norm_rope(k, cos, sin)
+        a = attention(q, k, v)                                   # [T, heads * head_dim]
         a = gate_mul_sigmoid(a, g)
         x, h = residual_norm_modulate(x, gate_a, linear("attn.to_out.0", lin["attn.to_out.0"], a), scale_f, shift_f,
                                       weight=w_f)
