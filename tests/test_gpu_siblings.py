@@ -11,11 +11,11 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _layers(dev, shapes, seed, backend):
+def _layers(dev, shapes, seed, backend, group=64):
     from krea2_svdquant_amd.runtime.krea2_standin import random_quantized_state
     from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
     gen = torch.Generator(device=dev).manual_seed(seed)
-    return [SVDQuantLinear(random_quantized_state(n, k, rank=32, group_size=64, device=dev, generator=gen),
+    return [SVDQuantLinear(random_quantized_state(n, k, rank=32, group_size=group, device=dev, generator=gen),
                            backend=backend) for n, k in shapes]
 
 
@@ -69,11 +69,11 @@ def _prepared(mods, dev):
 
 
 @pytest.mark.parametrize("out_f32", [False, True])
-@pytest.mark.parametrize("k", [1024, 768])   # one launch (K % 512 == 0); one launch per layer
-def test_grouped_gemms_match_single_layer_forwards(dev, k, out_f32):
+@pytest.mark.parametrize("k,group", [(1024, 64), (768, 64), (1024, 128)])   # one launch (K % 512 == 0); per layer
+def test_grouped_gemms_match_single_layer_forwards(dev, k, group, out_f32):
     from krea2_svdquant_amd.kernels.hip.backend import forward_prepared, forward_prepared_siblings
     # partial column tiles (160, 96), a LoRA adapter that widens one layer's rank tiles (RTp 96)
-    mods = _layers(dev, [(640, k), (160, k), (384, k), (96, k)], seed=31, backend="hip_gfx950")
+    mods = _layers(dev, [(640, k), (160, k), (384, k), (96, k)], seed=31, backend="hip_gfx950", group=group)
     gen_l = torch.Generator(device=dev).manual_seed(6)
     mods[1].add_lora_adapter((torch.randn(48, k, device=dev, generator=gen_l) * 0.05).to(torch.bfloat16),
                              (torch.randn(160, 48, device=dev, generator=gen_l) * 0.05).to(torch.bfloat16),
