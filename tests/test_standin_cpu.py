@@ -99,3 +99,38 @@ def test_block_siblings_flag_keeps_the_call_set_and_result():
     y1, s1 = run(True)
     assert sorted(s0) == sorted(ks.LINEAR_NAMES) and s0 == s1
     assert torch.equal(y0, y1)
+
+
+def test_grouped_siblings_and_deferred_residual_off_the_gpu():
+    """siblings="grouped" (the default) with a custom linear runs the siblings one after another
+    (no side streams), and the transformer's deferred residuals (each block's last gated residual
+    formed with the next block's first norm) give the block-by-block result exactly on the CPU."""
+    from krea2_svdquant_amd.runtime.siblings import _groupable, run_grouped
+    dims = ks.Krea2Dims(layers=2, hidden=256, heads=2, kv_heads=1, head_dim=128, mlp=512)
+    model = ks.Krea2StandInTransformer.random(dims, device="cpu", seed=3)
+    gen = torch.Generator().manual_seed(0)
+    w = {n: torch.randn(o, i, generator=gen) / math.sqrt(i) for n, (o, i) in dims.linear_shapes().items()}
+    seen = []
+
+    def lin(name, mod, x):
+        seen.append(name)
+        return x @ w[name].T
+    x = torch.randn(24, 256, generator=torch.Generator().manual_seed(1))
+    for blk in model.transformer_blocks:          # float modulation for the float CPU evaluation
+        blk.modulation = blk.modulation.float()
+    y_grouped = model(x, linear=lin)
+    calls = list(seen)
+    seen.clear()
+    y_seq = model(x, linear=lin, siblings=False)
+    assert calls == seen and len(calls) == 8 * dims.layers
+    assert torch.equal(y_grouped, y_seq)
+    cos, sin = ks.rope_tables(24, 128, "cpu", torch.float32)
+    y_blocks = x
+    for blk in model.transformer_blocks:          # the blocks one by one, each with its own residual
+        y_blocks = blk(y_blocks, cos, sin, lin, siblings=False)
+    assert torch.equal(y_seq, y_blocks)
+    # off the GPU nothing is grouped: run_grouped calls the modules in order
+    mods = [torch.nn.Identity(), torch.nn.Identity()]
+    assert not _groupable(x, mods)
+    outs = run_grouped(x, mods)
+    assert len(outs) == 2 and all(torch.equal(o, x) for o in outs)
