@@ -1,0 +1,122 @@
+"""The stand-in Krea-2 block at BASELINE config 3's full size: hidden 6144, 48 query heads over 12
+KV heads of 128, MLP 16384, T = 4352 tokens (256 text + 4096 latent, one 1024px image).
+
+Same two-part check as ``test_gpu_standin.py``, at the shapes the denoise step runs:
+
+* every quantized linear is recorded with its own bf16 input and held, on a row sample, to the
+  float64 W4A4 oracle of that input (rel-L2 <= 1e-3 against bf16(oracle)); the activation codes
+  of those rows are checked bit for bit on the way (``sim.quantize_activations``);
+* the glue between the linears (adaptive RMS norms, per-head norm + rotary embedding, GQA
+  attention over all 4352 keys, sigmoid gate, SwiGLU product, gated residuals) is replayed on the
+  CPU in float32 for the sampled rows, from the recorded linear outputs, and each linear's
+  recorded input and the block output are compared with it (bf16 intermediates on the GPU:
+  rel-L2 <= 1e-2 per stage).
+
+The recorded forward runs the linears one by one; the default forward (sibling GEMMs grouped in
+one launch each) must give the same block output bit for bit.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import numerics as nm
+from oracle import sim
+from tests.gpu_util import from_device_state, rel_l2
+
+pytestmark = pytest.mark.gpu
+T_TEXT, T_LATENT = 256, 4096
+
+
+def _cpu_norm(x, scale, shift, eps=1e-6):
+    return F.rms_norm(x, (x.shape[-1],), eps=eps) * (1 + scale) + shift
+
+
+def _cpu_head_norm_rope(t, cos, sin, eps=1e-6):
+    t = F.rms_norm(t, (t.shape[-1],), eps=eps)
+    d = t.shape[-1] // 2
+    t1, t2 = t[..., :d], t[..., d:]
+    c, s = cos[:, None, :d], sin[:, None, :d]
+    return torch.cat([t1 * c - t2 * s, t2 * c + t1 * s], dim=-1)
+
+
+def test_standin_block_full_size(dev):
+    from krea2_svdquant_amd.runtime import krea2_standin as ks
+    dims = ks.Krea2Dims(layers=1)
+    print(f"full-size stand-in block: hidden {dims.hidden}, heads {dims.heads}/{dims.kv_heads}, "
+          f"T={T_TEXT + T_LATENT}", flush=True)
+    model = ks.Krea2StandInTransformer.random(dims, rank=32, group_size=64, device=dev, seed=23)
+    blk = model.transformer_blocks[0]
+    gen = torch.Generator(device=dev).manual_seed(29)
+    tokens = torch.randn(T_TEXT + T_LATENT, dims.hidden, device=dev, generator=gen).to(torch.bfloat16)
+    t = tokens.shape[0]
+
+    calls = {}
+
+    def record(name, mod, x):
+        y = mod(x)
+        calls[name] = (mod, x.detach().clone(), y.detach().clone())
+        return y
+
+    out_rec = model(tokens, linear=record)
+    out_grp = model(tokens)              # sibling GEMMs grouped, the default
+    torch.cuda.synchronize()
+    assert set(calls) == set(ks.LINEAR_NAMES)
+    assert torch.isfinite(out_rec.float()).all()
+    assert torch.equal(out_rec, out_grp), "grouped-sibling block output differs from the linear-by-linear one"
+
+    rng = np.random.default_rng(31)
+    rows = np.unique(np.concatenate([[0, T_TEXT - 1, T_TEXT, t - 1], rng.choice(t, 20, replace=False)]))
+    ridx = torch.from_numpy(rows).to(dev)
+
+    # (1) every linear on its recorded input, sampled rows, against the float64 oracle
+    for name in ks.LINEAR_NAMES:
+        mod, x, y = calls[name]
+        st = from_device_state(mod.state)
+        xr = x[ridx].float().cpu().numpy()
+        ref = sim.w4a4_eval(xr, st)["y"]
+        err = rel_l2(y[ridx].float().cpu().numpy(), nm.bf16(ref.astype(np.float32)))
+        print(f"  {name} {tuple(st.shape)}: {len(rows)} rows, rel_l2 {err:.3e}", flush=True)
+        assert err < 1e-3, f"{name}: rel_l2 {err}"
+        del st
+
+    # (2) the glue on the sampled rows, in float32 from the recorded linear outputs
+    f32 = lambda z: z.float().cpu()  # noqa: E731
+    rows_t = torch.from_numpy(rows)
+    mod = blk.modulation.float().cpu()
+    shift_a, scale_a, gate_a, shift_f, scale_f, gate_f = mod
+    cos, sin = ks.rope_tables(t, dims.head_dim, "cpu", torch.float32)
+    out = {n: f32(calls[n][2]) for n in ks.LINEAR_NAMES}
+    inp = {n: f32(calls[n][1][ridx]) for n in ks.LINEAR_NAMES}
+
+    def stage(tag, got, want):
+        err = rel_l2(got.numpy(), want.numpy())
+        print(f"  glue {tag}: rel_l2 {err:.3e}", flush=True)
+        assert err < 1e-2, f"glue {tag}: rel_l2 {err}"
+
+    x0 = f32(tokens)[rows_t]
+    h = _cpu_norm(x0, scale_a, shift_a)
+    for n in ("attn.to_q", "attn.to_k", "attn.to_v", "attn.to_gate"):
+        stage(f"{n} input", inp[n], h)
+
+    hd, hq, hk = dims.head_dim, dims.heads, dims.kv_heads
+    q = _cpu_head_norm_rope(out["attn.to_q"][rows_t].view(len(rows), hq, hd), cos[rows_t], sin[rows_t])
+    k = _cpu_head_norm_rope(out["attn.to_k"].view(t, hk, hd), cos, sin)
+    v = out["attn.to_v"].view(t, hk, hd)
+    rep = hq // hk
+    k = k.repeat_interleave(rep, dim=1).transpose(0, 1)          # [H, T, d]
+    v = v.repeat_interleave(rep, dim=1).transpose(0, 1)
+    s = torch.matmul(q.transpose(0, 1), k.transpose(1, 2)) / math.sqrt(hd)   # [H, R, T]
+    a = torch.matmul(torch.softmax(s, dim=-1), v).transpose(0, 1).reshape(len(rows), hq * hd)
+    a = a * torch.sigmoid(out["attn.to_gate"][rows_t])
+    stage("attn.to_out.0 input", inp["attn.to_out.0"], a)
+
+    x1 = x0 + gate_a * out["attn.to_out.0"][rows_t]
+    h2 = _cpu_norm(x1, scale_f, shift_f)
+    for n in ("ff.gate", "ff.up"):
+        stage(f"{n} input", inp[n], h2)
+    f = F.silu(out["ff.gate"][rows_t]) * out["ff.up"][rows_t]
+    stage("ff.down input", inp["ff.down"], f)
+    stage("block output", f32(out_rec)[rows_t], x1 + gate_f * out["ff.down"][rows_t])
