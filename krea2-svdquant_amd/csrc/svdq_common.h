@@ -70,6 +70,14 @@ __device__ __forceinline__ f32x16 mfma_bf16_32x32x16(u32x4 a, u32x4 b, f32x16 c)
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// K = 8 form of the bf16 MFMA (same 8 passes as K = 16 on gfx950, half the operand registers):
+// lane l holds row / column l % 32, k = 4 (l / 32) .. + 3, as two bf16 pairs.
+__device__ __forceinline__ f32x16 mfma_bf16_32x32x8(u32x2 a, u32x2 b, f32x16 c) {
+  typedef short i16x4 __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0,
+                                                  0, 0);
+}
+
 __device__ __forceinline__ f32x16 mfma_fp8_32x32x64(const u32x4 (&a)[2], const u32x4 (&b)[2], f32x16 c) {
   typedef int i32x8 __attribute__((ext_vector_type(8)));
   const i32x8 av = {(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3],

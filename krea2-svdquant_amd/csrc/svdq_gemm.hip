@@ -14,6 +14,8 @@
 // INT4 nibbles; the activation operand is written in the same order, so the permutation
 // cancels in every dot product.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "svdq_common.h"
@@ -1024,6 +1026,272 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_siblings_kernel(GemmSiblings
   w4a4_e3m2_tile<G, OUT_F32, true>(p, bm, bn);
 }
 
+// W4A4 GEMM, wide tiles (group 64, K a multiple of 256): block tile 256 x 256, 8 waves in a
+// 2 x 4 grid, wave tile 128 x 64 = 4 x 2 sub-tiles of 32 x 32.  Same arithmetic as
+// w4a4_e3m2_tile (FP6 product MFMA, bf16 scale MFMA, acc += P * S per group), same planar
+// operands and epilogue; what changes is the reuse per byte staged: each A fragment read from
+// LDS feeds 2 MFMAs and each B fragment 4 (2 and 2 in the 256 x 128 tile), and each byte the DMA
+// brings in feeds 256 output columns instead of 128.  Per 32 x 32 x 64 block that is a third fewer
+// DMA and a quarter fewer LDS read instructions, and the tile's fixed cost (first stage,
+// epilogue) is spread over twice the work.
+//
+// Stage = 128 columns of K (2 groups), two LDS buffers of 53312 bytes:
+//   A Q planes [k-step][half][256 rows][16 B], A P planes [k-step][half][256 rows][8 B], then B
+//   the same with 256 columns, then the scale words: (sx, sx) pairs [group][256 + 4] and
+//   (hi, lo) weight-scale pairs [group][256 + 4] (the last 4 words of each zero).
+// Wave w moves, per stage: rows 128 (w & 1) .. + 127 of plane w >> 1 of each operand (2 + 1 DMA
+// each for A and B) and 64 words of the scale tiles (group w >> 2, words 64 (w & 3) ..): 8 DMA
+// instructions, issued 2 per step over the stage's first 4 steps and waited for before the
+// barrier that ends the stage.
+// Steps: (group gi, row sub-tile i), 8 per stage; a step issues the row sub-tile's two product
+// and two scale MFMAs against both column sub-tiles, then its 32 rescale FMAs.  A fragments and
+// the sx operand of the next step are read at the top of the step into the other register set;
+// the B fragments and weight-scale operands of the next group are read in the group's last step,
+// after its MFMAs have taken the current ones (one set).
+template <bool OUT_F32>
+__device__ __forceinline__ void w4a4_e3m2_wide_tile(const GemmParams& p, int bm, int bn) {
+  constexpr int TBM = 256, TBN = 256, KT = 2, GPS = 2, HPS = 8;
+  constexpr int PQ = TBM * 16, PP = TBM * 8;             // bytes of one Q / P plane
+  constexpr int AQ = 0, AP = AQ + KT * 2 * PQ, BQ = AP + KT * 2 * PP, BP = BQ + KT * 2 * PQ;
+  constexpr int XS = TBM + 36;                            // scale words per group (the last 36 zero)
+  constexpr int XO = BP + KT * 2 * PP, WO = XO + GPS * XS * 4, BUF = WO + GPS * XS * 4;
+  constexpr int NDMA = 8, PER = 2;
+  static_assert(TBN == TBM, "scale tiles share one word count");
+  __shared__ __attribute__((aligned(1024))) uint8_t sm[2 * BUF];
+
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int m0 = bm * TBM, n0 = bn * TBN;
+  const int M = p.M, N = p.N, K = p.K, nkt = K / 64, nstages = K / 128;
+  const uint32_t lds0 = lds_offset(sm);
+
+  // DMA (M and N multiples of 256: no row is clamped).  Wave w moves plane pa = w >> 1 of the
+  // stage's 4 planes (k-step pa >> 1, half pa & 1), rows 128 (w & 1) ..; per-lane offsets are
+  // lane x 16 bytes (one Q row, or two 8-byte P rows) and lane x 4 (one scale word), everything
+  // else goes into the wave-uniform source and LDS addresses.
+  const int pa = wave >> 1, rh = (wave & 1) * 128, sj = wave >> 2, sr = (wave & 3) * 64;
+  const uint32_t o16 = (uint32_t)lane * 16u, o4 = (uint32_t)lane * 4u;
+  const long aP0 = (long)nkt * 2 * M * 16, bP0 = (long)nkt * 2 * N * 16;   // P region offsets
+  const uint32_t lAQ = lds0 + AQ + pa * PQ + rh * 16, lAP = lds0 + AP + pa * PP + rh * 8;
+  const uint32_t lBQ = lds0 + BQ + pa * PQ + rh * 16, lBP = lds0 + BP + pa * PP + rh * 8;
+  const uint32_t lX = lds0 + XO + 4 * (sj * XS + sr), lW = lds0 + WO + 4 * (sj * XS + sr);
+  // sources of stage 0 (advanced one stage at a time)
+  const uint8_t* gAQ = p.qa + (long)pa * M * 16 + (long)(m0 + rh) * 16;
+  const uint8_t* gAP = p.qa + aP0 + (long)pa * M * 8 + (long)(m0 + rh) * 8;
+  const uint8_t* gBQ = p.qwe + (long)pa * N * 16 + (long)(n0 + rh) * 16;
+  const uint8_t* gBP = p.qwe + bP0 + (long)pa * N * 8 + (long)(n0 + rh) * 8;
+  const uint32_t* gX = p.sxp + (long)sj * M + m0 + sr;
+  const uint32_t* gW = p.swp + (long)sj * N + n0 + sr;
+  const long stA = 4L * M, stB = 4L * N;   // plane rows per stage
+  auto dma_next = [&](int nb, int d) {
+    const uint32_t o = (uint32_t)(nb * BUF);
+    if (d < 2) dma16(gAQ + 64 * d * 16, o16, lAQ + o + 64 * d * 16);
+    else if (d == 2) dma16(gAP, o16, lAP + o);
+    else if (d < 5) dma16(gBQ + 64 * (d - 3) * 16, o16, lBQ + o + 64 * (d - 3) * 16);
+    else if (d == 5) dma16(gBP, o16, lBP + o);
+    else if (d == 6) dma4(gX, o4, lX + o);
+    else dma4(gW, o4, lW + o);
+  };
+  auto advance = [&]() {
+    gAQ += stA * 16;
+    gAP += stA * 8;
+    gBQ += stB * 16;
+    gBP += stB * 8;
+    gX += (long)GPS * M;
+    gW += (long)GPS * N;
+  };
+  // the zero words after each scale tile, both buffers (2 x 2 x 2 x 36)
+  for (int t = tid; t < 2 * 2 * GPS * 36; t += 512) {
+    const int b = t / (2 * GPS * 36), r = t % (2 * GPS * 36), w = r / (GPS * 36), g = (r / 36) % GPS, e = r % 36;
+    *reinterpret_cast<uint32_t*>(sm + b * BUF + (w ? WO : XO) + 4 * (g * XS + TBM + e)) = 0u;
+  }
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  // Per-lane LDS read bases; every read adds a compile-time offset (buffer, plane, sub-tile).
+  typedef const __attribute__((address_space(3))) uint8_t* lds_u8;
+  typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
+  typedef const __attribute__((address_space(3))) u32x2* lds_u32x2;
+  typedef const __attribute__((address_space(3))) uint32_t* lds_u32;
+  lds_u8 rAQ = (lds_u8)&sm[AQ + h * PQ + (128 * wm + lr) * 16];
+  lds_u8 rAP = (lds_u8)&sm[AP + h * PP + (128 * wm + lr) * 8];
+  lds_u8 rBQ = (lds_u8)&sm[BQ + h * PQ + (64 * wn + lr) * 16];
+  lds_u8 rBP = (lds_u8)&sm[BP + h * PP + (64 * wn + lr) * 8], rBP1 = rBP + 32 * 8;
+  lds_u8 rX = (lds_u8)&sm[XO + 4 * (128 * wm + scale_row_perm(lr))];   // rows permuted: see rescale_acc
+  // weight scales: lanes 32-63 read zero words (B rows 8-15 of the scale MFMA)
+  lds_u8 rW = (lds_u8)&sm[WO + 4 * (h ? TBN : 64 * wn + lr)];
+
+  // One register set: the next step's A fragments and sx operand are read after this step's
+  // MFMAs have taken the current ones, the next group's B fragments and weight-scale operands in
+  // the group's last step.  The scale MFMA is the K = 8 bf16 form (two-register operands): word 0
+  // loaded from LDS, word 1 stays zero.
+  u32x4 faq, fbq[2];
+  u32x2 fap, fbp[2], xop = u32x2{}, wop[2] = {u32x2{}, u32x2{}};
+  auto read_a = [&](int buf, int gi, int i) {
+    faq = *(lds_u32x4)(rAQ + buf * BUF + gi * 2 * PQ + 32 * i * 16);
+    fap = *(lds_u32x2)(rAP + buf * BUF + gi * 2 * PP + 32 * i * 8);
+    xop[0] = *(lds_u32)(rX + buf * BUF + 4 * gi * XS + 128 * i);
+  };
+  auto read_b = [&](int buf, int gi) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      fbq[j] = *(lds_u32x4)(rBQ + buf * BUF + gi * 2 * PQ + 32 * j * 16);
+      fbp[j] = *(lds_u32x2)((j ? rBP1 : rBP) + buf * BUF + gi * 2 * PP);
+      wop[j][0] = *(lds_u32)(rW + buf * BUF + 4 * gi * XS + 128 * j);
+    }
+  };
+  // last stage, RTp == 32: the epilogue's low-rank operands -> the free buffer (256 mid rows of
+  // 128 bytes, then 256 l1cat rows of 64 bytes), swizzled for the epilogue's reads
+  const bool epi_lds = p.RTp == 32;
+  auto epi_prefetch = [&](int fbuf) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = (4 * wave + c) * 64 + lane, r = idx >> 3, ch = (idx & 7) ^ ((r >> 1) & 7);
+      dma16(p.midp, (uint32_t)(m0 + r) * 128u + 16u * ch, lds0 + fbuf * BUF + (4 * wave + c) * 1024);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int idx = (2 * wave + c) * 64 + lane, r = idx >> 2, ch = (idx & 3) ^ ((r >> 2) & 3);
+      dma16(p.l1cat, (uint32_t)(n0 + r) * 64u + 16u * ch, lds0 + fbuf * BUF + 32768 + (2 * wave + c) * 1024);
+    }
+  };
+
+  // Stage 0 landed everywhere; stage s + 1 goes out during stage s.
+#pragma unroll
+  for (int d = 0; d < NDMA; ++d) dma_next(0, d);
+  advance();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  read_a(0, 0, 0);
+  read_b(0, 0);
+
+  auto stage = [&](auto buf_c, auto last_c) {
+    constexpr int buf = decltype(buf_c)::value, nbuf = buf ^ 1;
+    constexpr bool LASTST = decltype(last_c)::value;
+    asm volatile("" : "+v"(rAQ), "+v"(rAP), "+v"(rBQ), "+v"(rBP), "+v"(rBP1), "+v"(rX), "+v"(rW));
+#pragma unroll
+    for (int hh = 0; hh < HPS; ++hh) {
+      const int gi = hh >> 2, i = hh & 3;
+      const bool last = hh == HPS - 1;
+      if (LASTST && hh == 0 && epi_lds) epi_prefetch(nbuf);   // ahead of the step's MFMA results
+      // this step's fragments in place, the previous step's rescale issued
+      asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(acc[2][0]),
+                   "+v"(acc[2][1]), "+v"(acc[3][0]), "+v"(acc[3][1])::"memory");
+      asm volatile("" : "+v"(faq), "+v"(fap), "+v"(xop), "+v"(fbq[0]), "+v"(fbq[1]), "+v"(fbp[0]), "+v"(fbp[1]),
+                   "+v"(wop[0]), "+v"(wop[1])::"memory");
+      f32x16 P[2], S[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        P[j] = mfma_fp6_32x32x64(faq, fap, fbq[j], fbp[j], f32x16{});
+        S[j] = mfma_bf16_32x32x8(xop, wop[j], f32x16{});
+      }
+      if (!LASTST && hh < NDMA / PER) {
+#pragma unroll
+        for (int d = hh * PER; d < (hh + 1) * PER; ++d) dma_next(nbuf, d);
+      }
+      // the MFMAs have their operands; the next fragments go into the same registers
+      asm volatile("" : "+v"(P[0]), "+v"(P[1]), "+v"(S[0]), "+v"(S[1])::"memory");
+      if (!last) {
+        read_a(buf, (hh + 1) >> 2, (hh + 1) & 3);
+        if (i == 3) read_b(buf, gi + 1);
+      } else if (!LASTST) {
+        // stage s + 1 landed everywhere and every wave's reads of this stage are complete
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+        read_a(nbuf, 0, 0);
+        read_b(nbuf, 0);
+      }
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) rescale_acc(acc[i][j], P[j], S[j]);
+      __builtin_amdgcn_s_setprio(0);
+    }
+    if (!LASTST) advance();
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  using NO = std::integral_constant<bool, false>;
+  using YES = std::integral_constant<bool, true>;
+  for (int s = 0; s + 2 < nstages; s += 2) {
+    stage(B0{}, NO{});
+    stage(B1{}, NO{});
+  }
+  stage(B0{}, NO{});
+  stage(B1{}, YES{});
+  __builtin_amdgcn_sched_barrier(0);   // nothing of the epilogue moves up into the last steps
+  // Only the epilogue operands' DMA can be in flight; once every wave is past its last reads,
+  // the last stage's buffer (buffer 1: K / 128 stages, an even count) holds the output staging
+  // regions (4 KB per wave).
+  if (epi_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  uint8_t* stg = sm + BUF + wave * 4096;
+  const uint8_t* lmid = epi_lds ? sm : nullptr;
+  const uint8_t* ll1 = epi_lds ? sm + 32768 : nullptr;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    f32x16(&a2)[2][2] = *reinterpret_cast<f32x16(*)[2][2]>(&acc[2 * u][0]);
+    unrotate_acc(a2);
+    epilogue<OUT_F32>(p, a2, m0 + 128 * wm + 64 * u, n0 + 64 * wn, lr, h, stg, lmid, ll1, 128 * wm + 64 * u, 64 * wn);
+  }
+}
+
+// Tile choice for the group-64 e3m2 GEMM.  The wide tiles need M, N multiples of 256 and K of 256,
+// and take a shape when their rounds of tiles over the 256 CUs times the tile's work, at the 10%
+// lower time per block measured for them (ff.up: 393 against 439 us), is no more than the 256 x
+// 128 tiles': ff.up at M = 4096 (4 rounds of 256 x 256 against 8 of 256 x 128) and the config-3
+// sibling groups take them, N = 6144 at M = 4096 (2 rounds against 3) does not.
+// SVDQ_W4A4_TILES=256x128 or 256x256 in the environment overrides the choice (the second only
+// where the wide tiles apply); it exists so that tests can run both tilings on one shape.
+int tile_override() {
+  const char* e = getenv("SVDQ_W4A4_TILES");
+  if (!e) return 0;
+  if (!strcmp(e, "256x128")) return 1;
+  if (!strcmp(e, "256x256")) return 2;
+  return 0;
+}
+bool wide_tiles_apply(int M, int N, int K) { return K % 256 == 0 && K >= 256 && M % 256 == 0 && N % 256 == 0; }
+bool wide_tiles_pay(long tiles_wide, long tiles_narrow) {
+  const long wide = (tiles_wide + 255) / 256, narrow = (tiles_narrow + 255) / 256;
+  return 2 * wide * 9 <= narrow * 10;
+}
+bool use_wide_tiles(int M, int N, int K) {
+  if (!wide_tiles_apply(M, N, K)) return false;
+  const int o = tile_override();
+  if (o) return o == 2;
+  const long bm = M / 256;
+  return wide_tiles_pay(bm * (N / 256), bm * (N / 128));
+}
+
+template <bool OUT_F32>
+__global__ void __launch_bounds__(512, 1) w4a4_e3m2_wide_kernel(GemmParams p) {
+  const int nbm = (p.M + 255) / 256, nbn = (p.N + 255) / 256;
+  int bm, bn;
+  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
+  w4a4_e3m2_wide_tile<OUT_F32>(p, bm, bn);
+}
+
+// Sibling layers on the wide tiles: as w4a4_e3m2_siblings_kernel with 256 x 256 tiles (tile0 counts
+// them); every output is bit-identical to a launch per layer.
+template <bool OUT_F32>
+__global__ void __launch_bounds__(512, 1) w4a4_e3m2_wide_siblings_kernel(GemmSiblings gs) {
+  const int total = gs.tile0[gs.count];
+  int lin = blockIdx.x;
+  if (total % 8 == 0) lin = (lin % 8) * (total / 8) + lin / 8;
+  int i = 0;
+#pragma unroll
+  for (int c = 1; c < MAX_SIBLINGS; ++c) i += (c < gs.count && lin >= gs.tile0[c]) ? 1 : 0;
+  i = __builtin_amdgcn_readfirstlane(i);
+  const GemmParams& p = gs.layer[i];
+  int bm, bn;
+  tile_of_linear(lin - gs.tile0[i], p.M / 256, p.N / 256, 4, bm, bn);
+  w4a4_e3m2_wide_tile<OUT_F32>(p, bm, bn);
+}
+
 // Weight operand of the W4A4 GEMM, once per layer: each packed dword (8 nibbles, k0 in the
 // low nibble) becomes 8 operand bytes [k0 k2 k4 k6 k1 k3 k5 k7].
 // The sigmoid gate and SwiGLU product as their own pass over contiguous bf16 tensors (the same op
@@ -1594,6 +1862,12 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
   SVDQ_W4A4(128, 1)
 #undef SVDQ_W4A4
   if (mode == 2) {
+    if (G == 64 && !p.epi && use_wide_tiles(p.M, p.N, p.K)) {
+      const dim3 wgrid((unsigned)(((p.M + 255) / 256) * ((p.N + 255) / 256)));
+      if (out_f32) w4a4_e3m2_wide_kernel<true><<<wgrid, 512, 0, st>>>(p);
+      else w4a4_e3m2_wide_kernel<false><<<wgrid, 512, 0, st>>>(p);
+      return hipGetLastError();
+    }
     const bool full = p.K % 512 == 0;   // two full 256-column stages per main-loop iteration
 #define SVDQ_E3M2(GG)                                                                  \
   if (G == GG) {                                                                       \
@@ -1625,6 +1899,28 @@ hipError_t launch_w4a4_siblings(const GemmSiblings& gs, int G, bool out_f32, hip
     tiles += ((p.M + 255) / 256) * ((p.N + 127) / 128);
   }
   if (gs.tile0[gs.count] != tiles || K % 512) return hipErrorInvalidValue;
+  if (G == 64) {
+    // the wide tiles when every layer takes them and they pay over the whole launch
+    bool apply = true;
+    long wide = 0;
+    for (int i = 0; i < gs.count; ++i) {
+      apply = apply && wide_tiles_apply(M, gs.layer[i].N, K);
+      wide += (long)(M / 256) * (gs.layer[i].N / 256);
+    }
+    const int o = tile_override();
+    if (apply && (o ? o == 2 : wide_tiles_pay(wide, tiles))) {
+      GemmSiblings w = gs;
+      int t = 0;
+      for (int i = 0; i < gs.count; ++i) {
+        w.tile0[i] = t;
+        t += (M / 256) * (gs.layer[i].N / 256);
+      }
+      w.tile0[gs.count] = t;
+      if (out_f32) w4a4_e3m2_wide_siblings_kernel<true><<<dim3((unsigned)t), 512, 0, st>>>(w);
+      else w4a4_e3m2_wide_siblings_kernel<false><<<dim3((unsigned)t), 512, 0, st>>>(w);
+      return hipGetLastError();
+    }
+  }
   const dim3 grid((unsigned)tiles);
   if (G == 64) {
     if (out_f32) w4a4_e3m2_siblings_kernel<64, true><<<grid, 512, 0, st>>>(gs);
