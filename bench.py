@@ -46,7 +46,8 @@ INT8_PEAK_TOPS = 5000.0
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 MFMA_NAME = {"e3m2": "FP6", "e4m3": "FP8", "i8": "INT8"}
-KERNEL_NAME = {"e3m2": "w4a4_e3m2_kernel<64,false> (FP6 MFMA on exact INT4 codes)",
+KERNEL_NAME = {"e3m2": "w4a4_e3m2_kernel<64,false> (256x128 tiles; FP6 MFMA on exact INT4 codes)",
+               "e3m2_wide": "w4a4_e3m2_wide_kernel<false> (256x256 tiles; FP6 MFMA on exact INT4 codes)",
                "e4m3": "w4a4_kernel<64,0,false> (FP8 MFMA on exact INT4 codes)",
                "i8": "w4a4_kernel<64,1,false> (INT8 MFMA on 16*q)"}
 TRAFFIC_SUMMARY = ROOT / "profiles" / "w4a4_gemm_ffup_traffic.md"
@@ -71,8 +72,8 @@ def parse():
     ap.add_argument("--cpu-reps", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-block", action="store_true", help="skip the config 1-4 extra lines")
-    ap.add_argument("--lines", default="block,w4a16,lora,denoise,attention",
-                    help="extra lines to run (comma list of block, w4a16, lora, denoise, attention)")
+    ap.add_argument("--lines", default="config0,block,w4a16,lora,denoise,attention",
+                    help="extra lines to run (comma list of config0, block, w4a16, lora, denoise, attention)")
     ap.add_argument("--pmc-pass", nargs="?", const="w4a4", default=None,
                     choices=["w4a4", "w4a16", "attention", "denoise"],
                     help="counter pass for rocprofv3: one copy kernel of known size, then 3 launches of the "
@@ -262,13 +263,58 @@ def block_layers(args, dev, m: int, mode: str, seed0: int) -> dict:
             "grp": ms_grp}
 
 
+def peak_fracs(tops: float) -> dict:
+    """An effective rate against the dense INT8 peak the north star names and the FP6 peak of the
+    MFMA the W4A4 GEMM issues."""
+    return {"int8_dense_peak_frac": round(tops / INT8_PEAK_TOPS, 4),
+            "fp6_dense_peak_frac": round(tops / MFMA_PEAK_TFLOPS["e3m2"], 4)}
+
+
+def config0_line(args, dev) -> dict:
+    """one to_q-shaped layer, M=256, K=N=6144 (rank 32, group 64): the GPU
+    forward and, on the host, the restated reference pytorch_sim forward at the same shape."""
+    import torch
+    from krea2_svdquant_amd.kernels.hip import backend
+    from oracle import sim
+    m, n, k = 256, 6144, 6144
+    x, ds, prep = make_layer(n, k, m, args.rank, args.group, dev, seed=500)
+    fwd = lambda: backend.forward_prepared(x, prep, mode="w4a4")  # noqa: E731
+    for _ in range(10):
+        fwd()
+    ms = time_avg(fwd, 200)
+    tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    torch.set_num_threads(os.cpu_count() or 1)
+    f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    st = sim.LayerState(smooth=f(ds.smooth_scale), qweight=ds.qweight.cpu().numpy(),
+                        weight_scales=f(ds.weight_scales), l1=f(ds.l1), l2=f(ds.l2), bias=None,
+                        group_size=ds.group_size, shape=tuple(ds.original_shape))
+    xc = x.cpu()
+    sim.sim_forward_torch(xc[:16], st)
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        sim.sim_forward_torch(xc, st)
+        times.append(time.perf_counter() - t0)
+    t_cpu = statistics.median(times)
+    del x, ds, prep
+    torch.cuda.empty_cache()
+    return {"ms": round(ms, 4), "eff_TOPS": round(tops, 1), **peak_fracs(tops),
+            "cpu_pytorch_sim_ms": round(t_cpu * 1e3, 2), "cpu_threads": torch.get_num_threads(),
+            "cpu_eff_TOPS": round(2.0 * m * n * k / t_cpu / 1e12, 4),
+            "note": "W4A4 forward (activation pass + GEMM with the low-rank epilogue) at M=256 K=N=6144, "
+                    "HIP events over 200 back-to-back calls; CPU: the oracle's restatement of the reference "
+                    "pytorch_sim forward (bf16 CPU torch, all host threads), median of 5. At this size the "
+                    "GEMM is one row of 48 tiles of 256 x 128 over the 256 CUs"}
+
+
 def block_line(args, dev) -> dict:
     """ms per block of the 8 W4A4 linears of config 1 at M=4096 (each timed alone, summed; and
     the block in order, siblings sequential / concurrent)."""
     b = block_layers(args, dev, args.m, "w4a4", 100)
     total = b["total"]
+    tops = b["ops"] / (total * 1e-3) / 1e12
     return {"ms_per_layer": b["per"], "ms_per_block_linears": round(total, 4),
-            "eff_TOPS": round(b["ops"] / (total * 1e-3) / 1e12, 2),
+            "eff_TOPS": round(tops, 2), **peak_fracs(tops),
             "linears_ms_per_denoise_step_28_blocks": round(28 * total, 3),
             "ms_per_block_in_order": round(b["seq"], 4),
             "ms_per_block_in_order_concurrent_siblings": round(b["conc"], 4),
@@ -312,7 +358,8 @@ def lora_line(args, dev) -> dict:
         for _ in range(3):
             backend.forward_prepared(x, prep, mode="w4a4")
         ms = time_avg(lambda: backend.forward_prepared(x, prep, mode="w4a4"), 10)
-        out[name] = {"ms": round(ms, 4), "eff_TOPS": round(2.0 * 16384 * n * k / (ms * 1e-3) / 1e12, 1)}
+        tops = 2.0 * 16384 * n * k / (ms * 1e-3) / 1e12
+        out[name] = {"ms": round(ms, 4), "eff_TOPS": round(tops, 1), **peak_fracs(tops)}
         del x, ds, prep
         torch.cuda.empty_cache()
     return {"layers": out, "note": "W4A4 + rank-32 SVD branch + rank-64 LoRA fused (down in the activation pass, "
@@ -383,7 +430,10 @@ def denoise_line(args, dev) -> dict:
     hbm_gb = torch.cuda.max_memory_allocated(dev) / 1e9
     del model
     torch.cuda.empty_cache()
+    lin_ops = 28 * 2.0 * 4352 * sum(n * k for _, n, k in BLOCK_SHAPES)
     return {"ms_per_denoise_step": round(ms, 3), "ms_8_steps": round(ms * steps, 2),
+            "linears_eff_TOPS": round(lin_ops / (lin_ms * 1e-3) / 1e12, 1),
+            **{"linears_" + key: val for key, val in peak_fracs(lin_ops / (lin_ms * 1e-3) / 1e12).items()},
             "ms_per_denoise_step_fused_epilogues": round(ms_fused, 3),
             "ms_per_denoise_step_concurrent_siblings": round(ms_sib, 3),
             "ms_per_denoise_step_fused_epilogues_concurrent_siblings": round(ms_fused_sib, 3),
@@ -611,6 +661,9 @@ def main() -> int:
     act_bytes = (2 * m * k + 8 * k + 2 * r * k + ops.operand_bytes(m, k, opc) + 4 * m * (k // g)
                  + 2 * 4 * m * prep.rtp * splits + 4 * m * prep.rtp)
     gemm_tflops = flops / (ms_gemm * 1e-3) / 1e12
+    from krea2_svdquant_amd.kernels.hip import lib as svdq_lib
+    wide = args.operand == "e3m2" and svdq_lib.w4a4_tile_cols(m, n, k, g, ops.OPERAND_E3M2) == 256
+    kernel_name = KERNEL_NAME["e3m2_wide" if wide else args.operand]
     traffic = read_traffic()
     result = {
         "metric": METRIC,
@@ -644,12 +697,15 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": MFMA_PEAK_TFLOPS[args.operand],
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / MFMA_PEAK_TFLOPS[args.operand], 4),
                      "traffic": traffic if args.operand == "e3m2" else None,
-                     "kernel": KERNEL_NAME[args.operand], "algorithmic_ops_per_launch": flops,
+                     "kernel": kernel_name, "algorithmic_ops_per_launch": flops,
                      "int8_dense_peak_frac": round(gemm_tflops / INT8_PEAK_TOPS, 4)},
     }
     if not args.no_block:
         lines = set(args.lines.split(","))
         del qa, sx, mid
+        if "config0" in lines:
+            log("config 0: M=256 K=N=6144 (GPU and CPU pytorch_sim)")
+            result["config0"] = config0_line(args, dev)
         if "block" in lines:
             log("block line: 8 linears of config 1")
             result["block_config1"] = block_line(args, dev)

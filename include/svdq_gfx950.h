@@ -195,6 +195,14 @@ int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe
                    const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,
                    void* y, int64_t ldy, int out_f32, hipStream_t stream);
 
+/* Block tile of the W4A4 GEMM svdq_w4a4_gemm runs for a shape (no fused op): returns the tile's
+ * column count, 256 (256 x 256 tiles, wave tile 128 x 64) or 128 (256 x 128 tiles), or 0 when the
+ * shape takes another kernel (other operand formats and group sizes).  Both tilings give
+ * bit-identical outputs; the environment variable SVDQ_W4A4_TILES=256x128 or 256x256 overrides
+ * the choice (the second only where M, N and K are multiples of 256).  No reference counterpart:
+ * a host-side query for callers that report which kernel ran (bench.py, tests). */
+int svdq_w4a4_gemm_tile_cols(int M, int N, int K, int group, int operand);
+
 /* W4A16 GEMM with fused epilogue: the reference pytorch_sim math (quant/svd.py:119-163;
  * dequantization pack.py:26-44 in bf16) and kernels/triton/generic_int4.py:18-133.
  *   xhat : bf16 [M, ldxh] (from svdq_act_quant with SVDQ_ACT_XHAT); other arguments as in

@@ -374,6 +374,11 @@ int svdq_w4a4_gemm(const void* qa, int operand, const void* sxp, const void* qwe
                             SVDQ_EPI_NONE, nullptr, 0, nullptr, stream);
 }
 
+int svdq_w4a4_gemm_tile_cols(int M, int N, int K, int group, int operand) {
+  if (operand != SVDQ_OPERAND_E3M2 || !fast_group(group) || M <= 0 || N <= 0 || K <= 0 || K % group) return 0;
+  return group == 64 && svdq::use_wide_tiles(M, N, K) ? 256 : 128;
+}
+
 // Checks of one W4A4 layer's arguments and its kernel parameters (no fused op yet).
 static int w4a4_layer(const char* who, const void* qa, int operand, const void* sxp, const void* qwe, const void* swp,
                       const void* mid, const void* l1cat, int RTp, const void* bias, int M, int N, int K, int group,

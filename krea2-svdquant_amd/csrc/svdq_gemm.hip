@@ -1259,13 +1259,6 @@ bool wide_tiles_pay(long tiles_wide, long tiles_narrow) {
   const long wide = (tiles_wide + 255) / 256, narrow = (tiles_narrow + 255) / 256;
   return 2 * wide * 9 <= narrow * 10;
 }
-bool use_wide_tiles(int M, int N, int K) {
-  if (!wide_tiles_apply(M, N, K)) return false;
-  const int o = tile_override();
-  if (o) return o == 2;
-  const long bm = M / 256;
-  return wide_tiles_pay(bm * (N / 256), bm * (N / 128));
-}
 
 template <bool OUT_F32>
 __global__ void __launch_bounds__(512, 1) w4a4_e3m2_wide_kernel(GemmParams p) {
@@ -1837,6 +1830,14 @@ __global__ void __launch_bounds__(256, 2) w4a4_any_group_kernel(GemmParams p, in
 }
 
 }  // namespace
+
+bool use_wide_tiles(int M, int N, int K) {
+  if (!wide_tiles_apply(M, N, K)) return false;
+  const int o = tile_override();
+  if (o) return o == 2;
+  const long bm = M / 256;
+  return wide_tiles_pay(bm * (N / 256), bm * (N / 128));
+}
 
 hipError_t launch_w4a4_any_group(const GemmParams& p, int G, bool out_f32, hipStream_t st) {
   if (G <= 0 || G % 16 || p.K % G || p.K % 64) return hipErrorInvalidValue;

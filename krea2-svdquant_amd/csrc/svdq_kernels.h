@@ -88,6 +88,8 @@ hipError_t launch_quant_any_group(const uint16_t* xhat, long ldxh, int M, int K,
 // mode: 0 = e4m3 operands on the FP8 MFMA, 1 = int8 operands on the INT8 MFMA, 2 = e3m2 planar
 // operands on the FP6 MFMA
 hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipStream_t st);
+// whether launch_w4a4 (e3m2, group 64, no fused op) runs the 256 x 256 tiles for this shape
+bool use_wide_tiles(int M, int N, int K);
 // e3m2 operands, G = 64 or 128, K % 512 == 0, every layer without fused store ops
 hipError_t launch_w4a4_siblings(const GemmSiblings& gs, int G, bool out_f32, hipStream_t st);
 // out = op(y, aux) elementwise over n contiguous bf16 values (op 1 mul_sigmoid, 2 silu_mul; the

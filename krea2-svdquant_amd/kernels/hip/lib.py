@@ -71,6 +71,7 @@ SIGNATURES = {
     "svdq_prepare_weight_operand": (_I, [_P, _P, _I, _I, _I, _P]),
     "svdq_w4a4_gemm": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
     "svdq_w4a16_gemm": (_I, [_P, _L, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I, _P]),
+    "svdq_w4a4_gemm_tile_cols": (_I, [_I, _I, _I, _I, _I]),
     "svdq_w4a4_gemm_epi": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I,
                                 _I, _P, _L, _P, _P]),
     "svdq_w4a16_gemm_epi": (_I, [_P, _L, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _L, _I,
@@ -130,3 +131,9 @@ def call(name: str, *args) -> None:
 
 def version() -> str:
     return load().svdq_version().decode()
+
+
+def w4a4_tile_cols(m: int, n: int, k: int, group: int, operand: int) -> int:
+    """Columns of the block tile ``svdq_w4a4_gemm`` runs for this shape (256 or 128), 0 when the
+    shape takes another kernel (``svdq_w4a4_gemm_tile_cols``)."""
+    return int(load().svdq_w4a4_gemm_tile_cols(m, n, k, group, operand))

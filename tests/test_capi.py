@@ -199,3 +199,32 @@ def test_attention_qnorm_rejects_bad_tables_before_any_launch():
         lib.call("svdq_attention_fwd_qnorm", fake, 1536, fake, fake, 1536, 16, 12, 12, ctypes.c_float(0.1), fake,
                  fake, 60, ctypes.c_float(1e-6), fake, 1536, fake, None)
     assert ei.value.status == -3
+
+
+def test_w4a4_tile_choice():
+    """The host-side tiling rule: the 256 x 256 tiles where they need no more rounds of work per CU
+    (at their measured 10% lower time per block), the 256 x 128 tiles elsewhere; 0 for shapes that
+    take another kernel.  SVDQ_W4A4_TILES overrides (the wide tiles only where they apply)."""
+    import os
+    e3m2, i8 = 2, 1
+    t = lib.w4a4_tile_cols
+    assert t(4096, 16384, 6144, 64, e3m2) == 256      # config 1 ff.up: 4 rounds of 256 x 256, 8 of 256 x 128
+    assert t(4096, 6144, 16384, 64, e3m2) == 128      # ff.down: 2 rounds x 2 against 3
+    assert t(4096, 1536, 6144, 64, e3m2) == 128       # to_k: one round either way
+    assert t(16384, 16384, 6144, 64, e3m2) == 256     # config 4 ff.up
+    assert t(16384, 6144, 16384, 64, e3m2) == 256     # config 4 ff.down: 6 rounds x 2 x 0.9 < 12
+    assert t(4352, 6144, 6144, 64, e3m2) == 256       # config 3 (4352 = 17 x 256)
+    assert t(4000, 16384, 6144, 64, e3m2) == 128      # M not a multiple of 256
+    assert t(4096, 16384, 6144, 128, e3m2) == 128     # group 128
+    assert t(4096, 16384, 6144, 64, i8) == 0 and t(4096, 16384, 6144, 32, e3m2) == 0
+    old = os.environ.get("SVDQ_W4A4_TILES")
+    try:
+        os.environ["SVDQ_W4A4_TILES"] = "256x128"
+        assert t(4096, 16384, 6144, 64, e3m2) == 128
+        os.environ["SVDQ_W4A4_TILES"] = "256x256"
+        assert t(256, 256, 256, 64, e3m2) == 256 and t(300, 256, 256, 64, e3m2) == 128
+    finally:
+        if old is None:
+            os.environ.pop("SVDQ_W4A4_TILES", None)
+        else:
+            os.environ["SVDQ_W4A4_TILES"] = old
