@@ -75,7 +75,7 @@ def parse():
     ap.add_argument("--lines", default="config0,block,w4a16,lora,denoise,attention",
                     help="extra lines to run (comma list of config0, block, w4a16, lora, denoise, attention)")
     ap.add_argument("--pmc-pass", nargs="?", const="w4a4", default=None,
-                    choices=["w4a4", "w4a16", "attention", "denoise"],
+                    choices=["w4a4", "w4a16", "attention", "denoise", "lora"],
                     help="counter pass for rocprofv3: one copy kernel of known size, then 3 launches of the "
                          "config 1 ff.up W4A4 GEMM and 3 activation passes (w4a4), or of the config 2 ff.up "
                          "W4A16 GEMM at M=2304 (w4a16); attention: 3 calls of the config 3 block attention")
@@ -528,6 +528,29 @@ def pmc_pass_attention(args, dev) -> int:
     return 0
 
 
+def pmc_pass_lora(args, dev) -> int:
+    """Counter / trace pass of config 4: ff.up and ff.down at M=16384 with the rank-64 LoRA of the
+    lora line, 3 forwards each (activation pass, finalize and GEMM per forward)."""
+    import torch
+    from krea2_svdquant_amd.kernels.hip import backend
+    for i, (name, n, k) in enumerate([("ff.up", 16384, 6144), ("ff.down", 6144, 16384)]):
+        x, ds, _ = make_layer(n, k, 16384, args.rank, args.group, dev, seed=300 + 10 * i)
+        gen = torch.Generator(device=dev).manual_seed(4 + i)
+
+        class _Ad:
+            down_weight = (torch.randn(64, k, device=dev, generator=gen) * 0.01).to(torch.bfloat16)
+            up_weight = (torch.randn(n, 64, device=dev, generator=gen) * 0.01).to(torch.bfloat16)
+            multiplier = 0.8
+        prep = backend.prepare_layer(ds, [_Ad()], dev)
+        for _ in range(3):
+            backend.forward_prepared(x, prep, mode="w4a4")
+        torch.cuda.synchronize()
+        del x, ds, prep
+        torch.cuda.empty_cache()
+    log("pmc pass done: 3 forwards each of config 4 ff.up and ff.down (M=16384, LoRA r64)")
+    return 0
+
+
 def pmc_pass_denoise(args, dev) -> int:
     """Trace pass of config 3: one warm-up and 3 default denoise steps of the stand-in model."""
     import torch
@@ -567,6 +590,8 @@ def main() -> int:
         return pmc_pass_attention(args, dev)
     if args.pmc_pass == "denoise":
         return pmc_pass_denoise(args, dev)
+    if args.pmc_pass == "lora":
+        return pmc_pass_lora(args, dev)
     log(f"device {torch.cuda.get_device_name(dev)}; building state M={m} K={k} N={n} r={r} g={g}")
     x, ds, prep = make_layer(n, k, m, r, g, dev, seed=1)
     opc = ops.OPERAND_NAMES[args.operand]
