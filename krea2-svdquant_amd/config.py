@@ -4,9 +4,10 @@
 string valid for the reference parses here too, and adds the two gfx950 backends of this
 package:
 
-* ``hip_gfx950``       -- W4A4: smoothing + dynamic per-group INT4 activations, INT8-MFMA
-  GEMM with the low-rank / LoRA / bias epilogue fused (the path the reference plans in
-  ``README.md:188-195``);
+* ``hip_gfx950``       -- W4A4: smoothing + dynamic per-group INT4 activations, and a GEMM of
+  exact INT4-code group sums on the FP6 MFMA (every INT4 code is an e3m2 value; FP8 and INT8
+  operand kernels stay selectable) with the low-rank / LoRA / bias epilogue fused (the path the
+  reference plans in ``README.md:188-195``);
 * ``hip_gfx950_w4a16`` -- W4A16: bf16 activations, INT4 weights dequantized in registers,
   BF16-MFMA GEMM; numerically the reference ``pytorch_sim`` math.
 

@@ -646,9 +646,12 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
     over |= !(l[qb] <= ROWSUM_LIMIT);   // also catches inf / NaN
   }
   if (piece >= 0) {
-    // a piece: its unnormalized output, offset and row sum for the combine (rows past T too)
-    const bool mark = __any(over);
-    if (lane == 0) p.part_flag[piece * 4 + wave] = mark ? 1 : 0;
+    // a piece: its unnormalized output, offset and row sum for the combine (rows past T too).  Its
+    // wave is also marked when an accumulator is not finite (p v past the f32 range: |v| above
+    // about 2^64 with the fixed offset), as a whole item's normalized output is; the values are
+    // checked as they go out (0 x inf and 0 x NaN are NaN, 0 x finite is 0).  Rows past T (q read
+    // as 0) are checked too: a mark there only sends the wave to the running-maximum kernel.
+    float nf = 0.0f;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const long row = (long)piece * 256 + 64 * wave + 32 * qb + lr;
@@ -657,10 +660,15 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
 #pragma unroll
       for (int db = 0; db < AD / 32; ++db)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<f32x4*>(orow + 32 * db + 8 * g + 4 * h) =
-              f32x4{O[qb][db][4 * g], O[qb][db][4 * g + 1], O[qb][db][4 * g + 2], O[qb][db][4 * g + 3]};
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 o4 = {O[qb][db][4 * g], O[qb][db][4 * g + 1], O[qb][db][4 * g + 2], O[qb][db][4 * g + 3]};
+          *reinterpret_cast<f32x4*>(orow + 32 * db + 8 * g + 4 * h) = o4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) nf = __builtin_fmaf(o4[e], 0.0f, nf);
+        }
     }
+    const bool mark = __any(over || nf != 0.0f);   // NaN != 0
+    if (lane == 0) p.part_flag[piece * 4 + wave] = mark ? 1 : 0;
     return;
   }
   // normalize (lanes l and l ^ 32 hold the same query), checking every value first

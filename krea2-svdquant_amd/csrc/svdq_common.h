@@ -52,7 +52,9 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
 
 // ---- division ---------------------------------------------------------------
 // Correctly rounded float32 quotient x / s given rs = RN(1/s) (one multiply and two
-// FMAs).  Exhaustively verified for every pair of bf16-representable operands whose
+// FMAs): Markstein's correction step (P. Markstein, "Computation of elementary functions on
+// the IBM RISC System/6000 processor", IBM J. Res. Dev. 34(1), 1990) -- the residual
+// r = x - q0 s is exact in an FMA and q0 + r rs rounds to the correctly rounded quotient.  Exhaustively verified for every pair of bf16-representable operands whose
 // quotient is a normal float32 (tests/test_division_exact.py); callers guarantee that
 // range and use the IEEE division otherwise.
 __device__ __forceinline__ float div_rcp(float x, float s, float rs) {

@@ -18,6 +18,8 @@ Nothing falls back to another implementation.
 """
 from __future__ import annotations
 
+import math
+
 import weakref
 from dataclasses import dataclass
 from typing import Optional, Sequence
@@ -106,6 +108,18 @@ def prepare_layer(state: SVDQuantLinearState, adapters: Sequence = (),
     scales = state.weight_scales.to(dev)
     if scales.dtype != torch.float16:
         raise TypeError(f"weight_scales must be float16 (checkpoint layout), got {scales.dtype}")
+    if tuple(scales.shape) != (n, kp // g):
+        raise ValueError(f"weight_scales must be [{n}, {kp // g}], got {tuple(scales.shape)}")
+    if g not in FAST_GROUPS and kp % 64:
+        # The generic-group kernels step K by 64 columns; the reference pads K only to a multiple of
+        # the group (quant/pack.py:12-16).  Pad further, to a multiple of lcm(group, 64): zero
+        # activation columns (smoothing 1), weight codes 0 (nibble 8) with scale 1, zero low-rank
+        # and LoRA down columns.  The added groups' products are exactly zero, so every output is
+        # the unpadded layer's.
+        kq = -(-kp // math.lcm(g, 64)) * math.lcm(g, 64)
+        qweight = _pad_cols(qweight, kq // 2, 0x88)
+        scales = _pad_cols(scales, kq // g, 1.0)
+        kp = kq
     smooth = _pad_cols(state.smooth_scale.to(dev, torch.bfloat16), kp, 1.0)
     l1 = state.l1.to(dev, torch.bfloat16)
     l2 = _pad_cols(state.l2.to(dev, torch.bfloat16), kp)

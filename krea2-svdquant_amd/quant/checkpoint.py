@@ -115,18 +115,18 @@ def convert_transformer(transformer: nn.Module, out_dir: str | Path, *,
     tensors: dict[str, torch.Tensor] = {}
     for name, mod in targets:
         if max_layers and len(meta["layers"]) >= max_layers:
-            say(f"reached max_layers={max_layers}; stopping")
+            say(f"{len(meta['layers'])} layers written (max_layers); the remaining targets stay dense")
             break
         b = block_index(name)
         if b is not None and b in skipped_blocks:
-            say(f"skip {name}: block {b} kept dense")
+            say(f"{name}: left dense (block {b} falls under skip_first_blocks / skip_last_blocks)")
             continue
         if skip_qk and name.endswith(("attn.to_q", "attn.to_k")):
-            say(f"skip {name}: skip_qk")
+            say(f"{name}: left dense (skip_qk)")
             continue
         calibrated = name in absmax
         if require_calib and not calibrated:
-            say(f"skip {name}: no calibration statistics")
+            say(f"{name}: left dense (require_calib, and no activation statistics for it)")
             continue
         r = rank_for(name, rank, attn_rank, mlp_rank)
         dev = torch.device(svd_device) if svd_device is not None else mod.weight.device
@@ -144,11 +144,12 @@ def convert_transformer(transformer: nn.Module, out_dir: str | Path, *,
             tensors[f"{key}.bias"] = st.bias.cpu()
         meta["layers"][name] = {"rank": r, "group_size": group_size, "shape": [int(v) for v in w.shape],
                                 "calibrated": calibrated}
-        say(f"converted {name} rank={r} shape={tuple(w.shape)} calibrated={calibrated}")
+        say(f"{name}: {tuple(w.shape)} -> INT4 group {group_size} + rank {r}, "
+            f"{'calibrated' if calibrated else 'uncalibrated'} smoothing")
     save_file(tensors, str(out / TENSORS_NAME))
     (out / CONFIG_NAME).write_text(json.dumps(meta, indent=2))
     save_transformer_checkpoint_readme(out, base_model)
-    say(f"converted {len(meta['layers'])} layers; saved to {out}")
+    say(f"{len(meta['layers'])} quantized layers written to {out}")
     return meta
 
 

@@ -130,6 +130,27 @@ def test_attention_scores_far_above_the_first_keys(dev):
     assert torch.equal(out2, out)
 
 
+def test_attention_tail_pieces_hand_over_overflowing_products(dev):
+    """T=300 at 48 query heads: 96 items, all in the last, partly filled round, so every item runs
+    as key pieces merged by the combine kernel.  Keys 32.. score 56 log2 units above the first 32
+    keys (the fixed exponent offset), so a probability reaches 2^56 while the row sum stays below
+    2^64, and every v is 2^73: p v passes the f32 range in the first piece.  Those waves must hand
+    their queries to the running-maximum kernel (as whole items do through their normalized
+    output), and the output is the average of equal values, 2^73, exactly."""
+    t, heads, kvh = 300, 48, 12
+    q = torch.ones(t, heads, 128, device=dev, dtype=torch.bfloat16)
+    s56 = 56.0 * math.log(2.0) * math.sqrt(128) / 128   # per-element k: q . k / sqrt(128) = 56 ln 2
+    k = torch.full((t, kvh, 128), s56, device=dev)
+    k[:32] = 0.0
+    k = k.to(torch.bfloat16)
+    v = torch.full((t, kvh, 128), 2.0 ** 73, device=dev, dtype=torch.bfloat16)
+    out, flags = _fast_flags(q, k, v, 1.0 / math.sqrt(128))
+    live = flags[:, : (t + 63) // 64]
+    assert bool((live == 1).all()), flags
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(out, torch.full_like(out, 2.0 ** 73))
+
+
 def test_attention_random_inputs_stay_on_the_fast_kernel(dev):
     """N(0, 1) inputs at the config-3 head counts: no fast wave hands its queries over."""
     q, k, v = _inputs(1000, 48, 12, dev, seed=21)

@@ -1,5 +1,6 @@
 """GPU parity for group sizes other than 64 / 128 (the generic kernels): any multiple of 16 that
-divides K, with K % 64 == 0.
+divides K; a layer whose K is not a multiple of 64 is padded by prepare_layer to a multiple of
+lcm(group, 64) with zero groups, which leaves every output unchanged.
 
 The reference quantizer takes any group (quant/pack.py:6-23; its own test uses g16,
 tests/test_svd_linear_cpu.py:10) and the group size is per-layer checkpoint metadata
@@ -46,6 +47,9 @@ def test_any_group_codes_bit_exact(dev, m, k, g):
     (200, 333, 1024, 16, 64, False),    # N % 8 != 0, LoRA
     (130, 384, 1536, 192, 32, True),    # a group spans three 64-column stages
     (257, 128, 6144, 32, 0, False),     # partial tiles, long K
+    (50, 96, 80, 16, 0, True),          # K % 64 != 0: prepare_layer pads K to 128 (lcm(16, 64))
+    (33, 160, 96, 32, 16, False),       # K = 96 -> 128, with LoRA
+    (20, 64, 144, 48, 0, False),        # K = 144 -> 192 (lcm(48, 64))
 ])
 @pytest.mark.parametrize("mode", ["w4a4", "w4a16"])
 def test_any_group_layer_matches_oracle(dev, m, n, k, g, rl, bias, mode):

@@ -79,7 +79,8 @@ def test_noalloc_matches_workspace_entry_point_twice_then_smaller(dev):
 
 
 def test_noalloc_config1_ffup_rows(dev):
-    """The BASELINE layer size (M=4096, K=6144, rank 32): 8 splits of 4096 x 32 partials (4 MiB)."""
+    """The BASELINE layer size (M=4096, K=6144, rank 32): the activation pass's K splits of 4096 x 32
+    f32 partials (7 at this size, 3.5 MiB) in the file-scope array."""
     from krea2_svdquant_amd.kernels.hip import backend
     x = synth.make_activation(4096, 6144, seed=71)
     st = synth.make_layer(512, 6144, x[:256], rank=32, group_size=64, seed=72)
