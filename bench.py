@@ -685,6 +685,9 @@ def main() -> int:
     # hi / lo operand written by the finalize kernel
     act_bytes = (2 * m * k + 8 * k + 2 * r * k + ops.operand_bytes(m, k, opc) + 4 * m * (k // g)
                  + 2 * 4 * m * prep.rtp * splits + 4 * m * prep.rtp)
+    # the same pass counted with the reference's formats: x and s read (bf16), L2 read, 4-bit
+    # packed codes and bf16 scales written, r float partials per split written
+    act_bytes_packed = (2 * m * k + 2 * k + 2 * r * k + m * k // 2 + 2 * m * (k // g) + 4 * m * r * splits)
     gemm_tflops = flops / (ms_gemm * 1e-3) / 1e12
     from krea2_svdquant_amd.kernels.hip import lib as svdq_lib
     wide = args.operand == "e3m2" and svdq_lib.w4a4_tile_cols(m, n, k, g, ops.OPERAND_E3M2) == 256
@@ -718,6 +721,9 @@ def main() -> int:
                     "step_minus_kernels_us": round((ms - ms_act_step - ms_gemm) * 1e3, 1),
                     "act_quant_GBps": round(act_bytes / (ms_act * 1e-3) / 1e9, 1),
                     "act_quant_hbm_frac": round(act_bytes / (ms_act * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "act_quant_bytes": act_bytes, "act_quant_bytes_packed_formats": act_bytes_packed,
+                    "act_quant_hbm_frac_packed_formats": round(act_bytes_packed / (ms_act * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                                               4),
                     "step_host_wall_ms": round(wall, 4)},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": MFMA_PEAK_TFLOPS[args.operand],
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / MFMA_PEAK_TFLOPS[args.operand], 4),
