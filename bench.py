@@ -73,7 +73,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-block", action="store_true", help="skip the config 1-4 extra lines")
     ap.add_argument("--lines", default="config0,block,w4a16,lora,denoise,attention",
-                    help="extra lines to run (comma list of config0, block, w4a16, lora, denoise, attention)")
+                    help="extra lines to run (comma list of config0, block, w4a16, lora, denoise, attention, "
+                         "siblings)")
     ap.add_argument("--pmc-pass", nargs="?", const="w4a4", default=None,
                     choices=["w4a4", "w4a16", "attention", "denoise", "lora"],
                     help="counter pass for rocprofv3: one copy kernel of known size, then 3 launches of the "
@@ -364,6 +365,75 @@ def lora_line(args, dev) -> dict:
         torch.cuda.empty_cache()
     return {"layers": out, "note": "W4A4 + rank-32 SVD branch + rank-64 LoRA fused (down in the activation pass, "
                                    "up in the GEMM epilogue), M=16384"}
+
+
+def sibling_options_line(args, dev) -> dict:
+    """The two sibling fusions that the default block path does not take, measured against it at
+    config 3's shapes (M = 4352, hidden 6144, mlp 16384), outputs compared bit for bit:
+    the activation passes of the four attention inputs and of ff.gate + ff.up with x read once
+    for all layers (``SVDQ_ACT_SIBLINGS=shared_x``) against one workgroup per layer (default); and
+    the SwiGLU product in ff.up's GEMM store (ff.gate, then ff.up with the ``silu_mul`` epilogue)
+    against the grouped ff.gate + ff.up launch followed by the SwiGLU pass (default)."""
+    import os
+    import torch
+    from krea2_svdquant_amd.kernels.hip import backend
+    from krea2_svdquant_amd.kernels.hip import ops as hip_ops
+    m, k = 4352, 6144
+    out = {}
+    layers = {}
+    for i, (name, n) in enumerate([("attn.to_q", 6144), ("attn.to_gate", 6144), ("attn.to_k", 1536),
+                                   ("attn.to_v", 1536), ("ff.up", 16384), ("ff.gate", 16384)]):
+        x, _, prep = make_layer(n, k, m, args.rank, args.group, dev, seed=700 + 10 * i)
+        layers[name] = prep   # x: the last layer's synthetic activations serve every layer
+
+    def act(names):
+        preps = [layers[nm] for nm in names]
+        return lambda: hip_ops.act_quant_siblings(x, [p.srs for p in preps], [p.l2 for p in preps], args.group,
+                                                  preps[0].rtp, False)
+    old = os.environ.get("SVDQ_ACT_SIBLINGS")
+    try:
+        for key, names in (("attention_inputs", ("attn.to_q", "attn.to_gate", "attn.to_k", "attn.to_v")),
+                           ("ff_gate_up", ("ff.up", "ff.gate"))):
+            res = {}
+            for mode in ("per_layer", "shared_x"):
+                os.environ["SVDQ_ACT_SIBLINGS"] = mode
+                f = act(names)
+                for _ in range(3):
+                    f()
+                res[mode] = (round(time_avg(f, 20) * 1e3, 1), [t.clone() for t in f()])
+            same = all(torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+                       for a, b in zip(res["per_layer"][1], res["shared_x"][1]))
+            out[f"act_{key}_us"] = {"per_layer": res["per_layer"][0], "shared_x": res["shared_x"][0],
+                                    "bit_identical": same}
+    finally:
+        if old is None:
+            os.environ.pop("SVDQ_ACT_SIBLINGS", None)
+        else:
+            os.environ["SVDQ_ACT_SIBLINGS"] = old
+
+    up, gate = layers["ff.up"], layers["ff.gate"]
+
+    def swiglu_pass():
+        u, g = backend.forward_prepared_siblings(x, [up, gate])
+        return hip_ops.gate_op(u, g, hip_ops.EPILOGUES["silu_mul"])
+
+    def swiglu_store():
+        g = backend.forward_prepared(x, gate)
+        return backend.forward_prepared(x, up, epilogue="silu_mul", aux=g)
+    for f in (swiglu_pass, swiglu_store):
+        for _ in range(3):
+            f()
+    a, b = swiglu_pass(), swiglu_store()
+    torch.cuda.synchronize()
+    out["ff_swiglu_ms"] = {"grouped_then_pass": round(time_avg(swiglu_pass, 10), 4),
+                           "gate_then_up_with_store_op": round(time_avg(swiglu_store, 10), 4),
+                           "bit_identical": bool(torch.equal(a, b))}
+    del layers, up, gate, a, b
+    torch.cuda.empty_cache()
+    out["note"] = ("config 3 shapes (M=4352, K=6144): act_* = the siblings' activation passes (one launch + "
+                   "finalize) with one workgroup per layer vs x read once; ff_swiglu = silu(ff.gate(h)) * ff.up(h) "
+                   "as the grouped GEMM launch + the SwiGLU pass vs ff.gate then ff.up with the product in its store")
+    return out
 
 
 def denoise_line(args, dev) -> dict:
@@ -752,6 +822,9 @@ def main() -> int:
         if "attention" in lines:
             log("config 3: the block's attention")
             result["attention_config3"] = attention_line(args, dev)
+        if "siblings" in lines:
+            log("config 3: sibling fusion options")
+            result["sibling_options_config3"] = sibling_options_line(args, dev)
     if not args.no_cpu_baseline:
         log("cpu baseline (whole layer)")
         result["cpu_baseline"] = cpu_baseline(ds, x, args.cpu_reps)

@@ -19,6 +19,9 @@
 //
 // Codes never need the reference's clamp: |x_hat| <= amax and sx >= (amax/7)(1 - 2^-9), so
 // |x_hat / sx| < 7.02 rounds into [-7, 7].
+#include <cstdlib>
+#include <cstring>
+
 #include "svdq_common.h"
 #include "svdq_kernels.h"
 
@@ -97,11 +100,18 @@ __device__ __forceinline__ void smooth64_exact(const u32x4 (&xr)[8], cfloat_ptr 
 // may be LoRA tiles (the raw x is then kept as an MFMA operand too).  Ranks beyond 4 tiles take
 // further launches with OPER 0 and no XHAT (down projections only), each writing its own columns
 // of the split partials.
-template <int G, int NT, int OPER, bool XHAT, bool QX, bool LX>
-__device__ __forceinline__ void act_tile(const ActParams& p) {
+// NL > 1: the passes of NL sibling layers over the same x (lp[0 .. NL-1], same M, K, splits; one
+// rank tile each, NT = 1, no LoRA): each group of x is loaded once and smoothed, quantized and
+// down-projected once per layer, in layer order, so that every layer's codes, scales and split
+// partials are bit-identical to its own pass (the same groups per wave, the same MFMA and
+// reduction order).
+template <int G, int NT, int OPER, bool XHAT, bool QX, bool LX, int NL = 1>
+__device__ __forceinline__ void act_tile(const ActParams* lp) {
   constexpr int HB = G / 64;             // 64-column blocks per group
   constexpr bool QUANT = OPER != 0;
+  static_assert(NL == 1 || (NT == 1 && !LX && !XHAT && !QX), "shared-x passes: one rank tile, codes only");
   __shared__ __attribute__((aligned(16))) float red[4 * 64 * 32];
+  const ActParams& p = lp[0];            // M, K, x and the split are the same for every layer
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, lr = lane & 31, h = lane >> 5;
@@ -114,15 +124,14 @@ __device__ __forceinline__ void act_tile(const ActParams& p) {
   const int ngroups = K / G;
   const int gb = blockIdx.y * p.gps;
   const int ge = min(ngroups, gb + p.gps);
-  const int TR = (p.r + 31) >> 5;
-  const cfloat_ptr sv = (cfloat_ptr)p.srs;
-  const cfloat_ptr rv = (cfloat_ptr)(p.srs + K);
 
-  f32x16 acc[2][NT];
+  f32x16 acc[NL][2][NT];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int l = 0; l < NL; ++l)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[a][t] = f32x16{};
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[l][a][t] = f32x16{};
 
   // Without LoRA, x of the wave's next group is loaded into xr as soon as the current group's xr
   // is dead (after the smoothing and its exact fallback): the loads overlap the quantization, the
@@ -138,8 +147,14 @@ __device__ __forceinline__ void act_tile(const ActParams& p) {
   };
   if (!LORA && gb + wave < ge) load_x(gb + wave);
   for (int g = gb + wave; g < ge; g += 4) {
-    u32x4 xh[HB][8];
     if (LORA) load_x(g);
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+    const ActParams& p = lp[l];
+    const int TR = (p.r + 31) >> 5;
+    const cfloat_ptr sv = (cfloat_ptr)p.srs;
+    const cfloat_ptr rv = (cfloat_ptr)(p.srs + K);
+    u32x4 xh[HB][8];
 
     u16x2 amx = {0, 0}, xmx = {0, 0}, xmn = {0xFFFF, 0xFFFF};
 #pragma unroll
@@ -174,7 +189,7 @@ __device__ __forceinline__ void act_tile(const ActParams& p) {
 #pragma unroll
       for (int b = 0; b < HB; ++b) smooth64_exact(xr[b], sv + g * G + 64 * b, xh[b], am);
     }
-    if (!LORA && g + 4 < ge) load_x(g + 4);
+    if (l == NL - 1 && !LORA && g + 4 < ge) load_x(g + 4);
 
     if (QUANT) {
       const float sc = round_bf16(div_rcp(fmaxf(am, kBf16OneEMinus8), 7.0f, kRcp7));
@@ -292,13 +307,18 @@ __device__ __forceinline__ void act_tile(const ActParams& p) {
           if (!nok) bf = u32x4{};
 #pragma unroll
           for (int i = 0; i < 2; ++i)
-            acc[i][t] = mfma_bf16_32x32x16(is_l2 ? fa[i][c] : fx[i][c], bf, acc[i][t]);
+            acc[l][i][t] = mfma_bf16_32x32x16(is_l2 ? fa[i][c] : fx[i][c], bf, acc[l][i][t]);
         }
       }
     }
+    }   // layers
   }
 
-  // ---- reduce the 4 waves (fixed order) and write this split's partial ----
+  // ---- reduce the 4 waves (fixed order) and write this split's partial, layer by layer ----
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+  const ActParams& p = lp[l];
+  const int TR = (p.r + 31) >> 5;
   const int RTp = p.RTp;
   float* dst = p.mid + (long)blockIdx.y * p.M * RTp;
   const int nval = p.r + p.rl;
@@ -308,7 +328,7 @@ __device__ __forceinline__ void act_tile(const ActParams& p) {
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        red[wave * 2048 + (32 * a + 8 * (i >> 2) + 4 * h + (i & 3)) * 32 + lr] = acc[a][t][i];
+        red[wave * 2048 + (32 * a + 8 * (i >> 2) + 4 * h + (i & 3)) * 32 + lr] = acc[l][a][t][i];
     __syncthreads();
     const int T = p.t0 + t;
     const bool is_l2 = T < TR;
@@ -332,12 +352,13 @@ __device__ __forceinline__ void act_tile(const ActParams& p) {
     const int grow = m0 + idx / npad;
     if (grow < p.M) dst[(long)grow * RTp + nval + idx % npad] = 0.0f;
   }
+  }   // layers
 
 }
 
 template <int G, int NT, int OPER, bool XHAT, bool QX, bool LX>
 __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
-  act_tile<G, NT, OPER, XHAT, QX, LX>(p);
+  act_tile<G, NT, OPER, XHAT, QX, LX>(&p);
 }
 
 // Sibling layers' activation passes over the same x in one launch (blockIdx.z = the layer):
@@ -345,7 +366,13 @@ __global__ void __launch_bounds__(256) act_kernel(ActParams p) {
 // smoothing constants, factors and outputs.
 template <int G>
 __global__ void __launch_bounds__(256) act_siblings_kernel(ActSiblings s) {
-  act_tile<G, 1, 3, false, false, false>(s.layer[blockIdx.z]);
+  act_tile<G, 1, 3, false, false, false>(&s.layer[blockIdx.z]);
+}
+
+// The same passes with x read once: each workgroup runs all NL layers of its row block and split.
+template <int G, int NL>
+__global__ void __launch_bounds__(256) act_shared_x_kernel(ActSiblings s) {
+  act_tile<G, 1, 3, false, false, false, NL>(s.layer);
 }
 
 // Final low-rank operand of the GEMM epilogue: the split partials summed in split order
@@ -520,10 +547,29 @@ hipError_t launch_act_siblings(const ActSiblings& s, int G, int splits, hipStrea
     if (s.layer[i].M != s.layer[0].M || s.layer[i].K != s.layer[0].K || s.layer[i].r > 32 || s.layer[i].rl ||
         s.layer[i].t0)
       return hipErrorInvalidValue;
-  const dim3 grid((s.layer[0].M + 63) / 64, splits, s.count);
-  if (G == 64) act_siblings_kernel<64><<<grid, 256, 0, st>>>(s);
-  else if (G == 128) act_siblings_kernel<128><<<grid, 256, 0, st>>>(s);
-  else return hipErrorInvalidValue;
+  if (G != 64 && G != 128) return hipErrorInvalidValue;
+  // One workgroup per layer, row block and split (blockIdx.z = the layer), or with
+  // SVDQ_ACT_SIBLINGS=shared_x x read once for all layers (act_shared_x_kernel; same results, but
+  // one wave per SIMD and a quarter of the workgroups: 119 against 79 us for the four attention
+  // inputs at M = 4352, 60 against 44 us for ff.gate / ff.up).  Group 128 with three or four
+  // layers would spill: per layer.
+  const char* e = getenv("SVDQ_ACT_SIBLINGS");
+  if (s.count >= 2 && (G == 64 || s.count == 2) && e && !strcmp(e, "shared_x")) {
+    const dim3 grid((s.layer[0].M + 63) / 64, splits);
+#define SVDQ_SHARED_X(NL)                                                            \
+  if (s.count == NL) {                                                               \
+    if (G == 64) act_shared_x_kernel<64, NL><<<grid, 256, 0, st>>>(s);               \
+    else if (NL == 2) act_shared_x_kernel<128, 2><<<grid, 256, 0, st>>>(s);          \
+  }
+    SVDQ_SHARED_X(2)
+    SVDQ_SHARED_X(3)
+    SVDQ_SHARED_X(4)
+#undef SVDQ_SHARED_X
+  } else {
+    const dim3 grid((s.layer[0].M + 63) / 64, splits, s.count);
+    if (G == 64) act_siblings_kernel<64><<<grid, 256, 0, st>>>(s);
+    else act_siblings_kernel<128><<<grid, 256, 0, st>>>(s);
+  }
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   const long n = (long)s.layer[0].M * (s.layer[0].RTp / 8);
   mid_finalize_siblings_kernel<<<dim3((unsigned)((n + 255) / 256), s.count), 256, 0, st>>>(s, splits);

@@ -127,17 +127,20 @@ def test_run_grouped_modules_and_standin(dev):
         assert torch.equal(a, b), f"fused={fused}"
 
 
+@pytest.mark.parametrize("mode", ["per_layer", "shared_x"])
 @pytest.mark.parametrize("group,exact", [(64, False), (128, False), (64, True)])
-def test_act_quant_siblings_match_per_layer_passes(dev, group, exact):
+def test_act_quant_siblings_match_per_layer_passes(dev, group, exact, mode, monkeypatch):
     """One launch of the siblings' activation passes (and one finalize): codes, scale pairs and the
     whole mid workspace (finalized head and split partials) bit-identical to each layer's own pass;
-    ranks above 32 take the per-layer path inside the C-ABI, with the same results."""
+    ranks above 32 take the per-layer path inside the C-ABI, with the same results.  shared_x: one
+    workgroup runs every layer's pass over one read of x (SVDQ_ACT_SIBLINGS)."""
+    monkeypatch.setenv("SVDQ_ACT_SIBLINGS", mode)
     from krea2_svdquant_amd.kernels.hip import ops
     from krea2_svdquant_amd.runtime.krea2_standin import random_quantized_state
     from krea2_svdquant_amd.kernels.hip.backend import prepare_layer
     gen = torch.Generator(device=dev).manual_seed(group + exact)
     k = 1024
-    for rank, ns in ((32, (512, 128, 256, 64)), (64, (256, 128))):
+    for rank, ns in ((32, (512, 128, 256, 64)), (32, (384, 256)), (64, (256, 128))):
         preps = [prepare_layer(random_quantized_state(n, k, rank=rank, group_size=group, device=dev, generator=gen))
                  for n in ns]
         rtp = preps[0].rtp

@@ -55,7 +55,7 @@ def test_async_load_kernels_do_not_spill():
 # loop the compiler could not keep in registers) costs more than it saves.
 NO_SCRATCH_KERNELS = ("mid_finalize_kernel", "gate_op_kernel", "rms_norm_modulate_kernel", "head_rms_rope",
                       "attn_fast_kernel", "attn_combine_kernel", "act_kernelILi64E", "w4a4_e3m2_siblings_kernel",
-                      "act_siblings_kernel", "mid_finalize_siblings_kernel")
+                      "act_siblings_kernel", "act_shared_x_kernel", "mid_finalize_siblings_kernel")
 
 
 @pytest.mark.skipif(not LIB.exists(), reason="library not built")
