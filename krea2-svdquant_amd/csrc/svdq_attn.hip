@@ -77,10 +77,16 @@ __device__ __forceinline__ float half_sum(float v) {
 //  * the probabilities (VALU-written B operands) are read at least one phase later, behind such a
 //    fence;
 //  * a source fragment's registers are not rewritten until two more MFMAs have issued;
-//  * no VALU work sits between two adjacent MFMAs that read the same fragment (a layout rule kept
-//    because a layout that broke it gave wrong results, cause unknown);
-//  * the output is read after out_fence (2 x 16 wait states).
-// (tests/test_attn_mfma_order.py checks the last two rules on the built library.)
+//  * no VALU work sits between two adjacent MFMAs that read the same fragment;
+//  * the output is read after out_fence (2 x 16 wait states);
+//  * a VALU write of an MFMA's source register (A, B or C) comes at least 2 wait states before the
+//    MFMA (the ISA's VALU-write -> MFMA-read rule).  The compiler moves the output accumulators
+//    between AGPRs and VGPRs around the rescale with v_accvgpr_write, and may place the last of
+//    those writes right before an output MFMA, which then reads the old value of that register:
+//    mfma_out starts with s_nop 1.  (A layout with softmax work between the two MFMAs of a fragment
+//    gave wrong results for the second MFMA of every pair; its build has v_accvgpr_write of that
+//    MFMA's srcC 0 and 1 wait states before it.)
+// (tests/test_attn_mfma_order.py checks the last four rules on the built library.)
 __device__ __forceinline__ void mfma_score0(f32x16& acc, u32x4 a, u32x4 b) {
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
 }
@@ -88,7 +94,7 @@ __device__ __forceinline__ void mfma_score(f32x16& acc, u32x4 a, u32x4 b) {
   asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
 }
 __device__ __forceinline__ void mfma_out(f32x16& acc, u32x4 a, u32x4 b) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
 // Work of the fast kernel: items (head, block of 256 queries), item = head * nq + block.  The
@@ -418,12 +424,12 @@ __global__ void __launch_bounds__(256, 1) attn_fast_kernel(AttnArgs p) {
   //  * with one kind, the two MFMAs of a fragment back to back (16 slots), the softmax parts
   //    before the first of each pair.
   // (An earlier layout that put softmax work between the two adjacent MFMAs of a fragment gave
-  // wrong results for the second of every pair, deterministically; the cause was not found -- the
-  // same instruction sequence in a standalone probe is exact -- so the kernel keeps to layouts
-  // that test exact: no VALU work between two adjacent MFMAs that read the same fragment.  One
-  // wave per SIMD stalls in order behind an MFMA that waits for the matrix pipe, so VALU work
-  // placed between MFMAs of different fragments hides under twice as much MFMA time as work
-  // placed only between pairs.)
+  // wrong results for the second of every pair, deterministically: rebuilt, its code writes the
+  // last accumulator AGPRs of that MFMA (v_accvgpr_write after the rescale) 0 and 1 wait states
+  // before it, under the ISA's 2 -- see mfma_out.  The kernel keeps the layouts that test exact:
+  // no VALU work between two adjacent MFMAs that read the same fragment.  One wave per SIMD stalls
+  // in order behind an MFMA that waits for the matrix pipe, so VALU work placed between MFMAs of
+  // different fragments hides under twice as much MFMA time as work placed only between pairs.)
   // A fragment is read from LDS LEAD slots before its first use; the ones used earlier than that
   // come from pre, read during the phase before (or by prefetch after a barrier).
   constexpr int LEAD = 6;
