@@ -1737,6 +1737,209 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
   }
 }
 
+// W4A16 GEMM with specialized waves (group 64 or 128, no fused op; the 192-row tiles of
+// w4a16_wide_kernel, with the same per-output arithmetic, so bit-identical outputs).  In one wave
+// the dequantization's VALU work and the MFMAs share the issue slots badly; here waves 0-3 only read
+// fragments and issue MFMAs (wave tile 96 x 128 of the 192 x 256 block tile, as in
+// w4a16_wide_kernel) and waves 4-7 only stage the next k-step block: x_hat by DMA into a swizzled
+// A tile (16-byte chunk c of row r at c ^ ((r >> 1) & 7), so a ds_read_b128 phase of 16 rows hits
+// 16 distinct bank groups), the weight codes loaded two stages ahead and dequantized into the B
+// tile (rows of 144 bytes).  One wave of each kind per SIMD; one barrier per 64-column stage.
+// The low-rank term runs as RTp / 32 more stages through the same MFMAs (A = the mid planes
+// [hi_2e | lo_2e | hi_2e+1 | lo_2e+1], B = [l1_2e | l1_2e | l1_2e+1 | l1_2e+1]), so each accumulator
+// takes hi_k then lo_k as in the epilogue's low-rank MFMAs, and the epilogue only adds the bias and
+// stores (the 192 accumulators leave no room for its operands).
+template <int G, bool OUT_F32>
+__global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
+  constexpr int NT = 256, TBM = 192, TBN = 256, KB = 64, RI = TBM / 64;
+  constexpr int PITCH = 2 * KB + 16;
+  constexpr int ALD = TBM * 8 / NT;            // x_hat DMA instructions per producer wave and stage
+  constexpr int D = 2;                         // register sets of weight codes (stages in flight)
+  constexpr int ABUF = TBM * 128;
+  __shared__ __attribute__((aligned(1024))) uint8_t sA[2][ABUF];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[2][TBN * PITCH];
+
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
+  int bm, bn;
+  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
+  const int m0 = bm * TBM, n0 = bn * TBN;
+  const int K = p.K, ngroups = K / G, kp = K / 2, nst = K / KB;
+  // the low-rank term mid @ l1cat^T as RTp / 32 more stages: A rows [hi_2e | lo_2e | hi_2e+1 |
+  // lo_2e+1] (16 columns each) of the mid planes, B rows [l1_2e | l1_2e | l1_2e+1 | l1_2e+1], so each
+  // accumulator takes hi_k then lo_k for k = 0, 1, .. as in the epilogue's low-rank MFMAs
+  const int RTp = p.RTp, nall = nst + RTp / 32;
+  using Q0 = std::integral_constant<int, 0>;
+  using Q1 = std::integral_constant<int, 1>;
+
+  if (wave >= 4) {
+    // ---- producer ----
+    const int ptid = tid - NT, pw = wave - 4;
+    // x_hat DMA: instruction t (6 per wave: t = 6 pw + i) moves rows 8 t .. 8 t + 7; lane -> row
+    // 8 t + lane / 8, LDS position lane % 8 holding chunk (lane % 8) ^ ((row >> 1) & 7)
+    const int rr = lane >> 3, jj = lane & 7;
+    const long ldb = p.ldxh * 2;
+    uint32_t aoffs[ALD];
+#pragma unroll
+    for (int i = 0; i < ALD; ++i) {
+      const int row = 8 * (ALD * pw + i) + rr;
+      aoffs[i] = (uint32_t)(min(m0 + row, p.M - 1) * ldb + 16 * (jj ^ ((row >> 1) & 7)));
+    }
+    const uint32_t ldsA0 = lds_offset(&sA[0][0]);
+    const uint8_t* xb = reinterpret_cast<const uint8_t*>(p.xhat);
+    auto dma_a = [&](int st, int buf) {
+#pragma unroll
+      for (int i = 0; i < ALD; ++i) dma16(xb + 2 * st * KB, aoffs[i], ldsA0 + buf * ABUF + (ALD * pw + i) * 1024);
+    };
+    const int nrow = min(n0 + ptid, p.N - 1);
+    const uint8_t* brow = p.qw + (long)nrow * kp;
+    const uint16_t* bsc = p.sw + (long)nrow * ngroups;
+    const int boff = ptid * PITCH;
+    u32x4 rb[D][2];
+    uint32_t rs[D];
+    auto gload_set = [&](int st, u32x4 (&db)[2], uint32_t& ds) {
+      const int k0 = st * KB;
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(db[0]) : "v"(brow + k0 / 2) : "memory");
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(db[1]) : "v"(brow + k0 / 2 + 16) : "memory");
+      asm volatile("global_load_ushort %0, %1, off" : "=v"(ds) : "v"(bsc + k0 / G) : "memory");
+    };
+    auto gload = [&](int st, auto q_c) {
+      constexpr int q = decltype(q_c)::value;
+      gload_set(st, rb[q], rs[q]);
+    };
+    auto mark_regs = [&](u32x4 (&db)[2], uint32_t& ds) { asm volatile("" : "+v"(db[0]), "+v"(db[1]), "+v"(ds)); };
+    auto mark_set = [&](auto q_c) {
+      constexpr int q = decltype(q_c)::value;
+      mark_regs(rb[q], rs[q]);
+    };
+    auto lstore_part = [&](int buf, auto q_c, int pt) {
+      constexpr int q = decltype(q_c)::value;
+      const float sc = round_bf16(half_bits_to_float((uint16_t)rs[q])), ns8 = -8.0f * sc;
+      const u32x4 w = rb[q][pt >> 1];
+      uint32_t o[8];
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const uint32_t v = w[2 * (pt & 1) + d];
+        uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+        asm("" : "+v"(lo), "+v"(hi));
+        o[4 * d + 0] = pack_bf16x2(__builtin_fmaf(ubyte_f32<0>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<0>(hi), sc, ns8));
+        o[4 * d + 1] = pack_bf16x2(__builtin_fmaf(ubyte_f32<1>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<1>(hi), sc, ns8));
+        o[4 * d + 2] = pack_bf16x2(__builtin_fmaf(ubyte_f32<2>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<2>(hi), sc, ns8));
+        o[4 * d + 3] = pack_bf16x2(__builtin_fmaf(ubyte_f32<3>(lo), sc, ns8), __builtin_fmaf(ubyte_f32<3>(hi), sc, ns8));
+      }
+      *reinterpret_cast<u32x4*>(&sB[buf][boff + 32 * pt]) = u32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<u32x4*>(&sB[buf][boff + 32 * pt + 16]) = u32x4{o[4], o[5], o[6], o[7]};
+    };
+    dma_a(0, 0);
+    gload(0, Q0{});
+    gload(min(1, nst - 1), Q1{});
+    asm volatile("s_waitcnt vmcnt(3)" ::: "memory");   // x_hat and codes of stage 0
+    mark_set(Q0{});
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) lstore_part(0, Q0{}, pt);
+    __syncthreads();
+    auto xstage = [&](int e, int buf) {
+      const uint8_t* mb = reinterpret_cast<const uint8_t*>(p.midp);
+#pragma unroll
+      for (int i = 0; i < ALD; ++i) {
+        const int row = 8 * (ALD * pw + i) + rr, c = jj ^ ((row >> 1) & 7), s4 = c >> 1;
+        const int col = 16 * (2 * e + (s4 >> 1)) + 8 * (c & 1);
+        const uint32_t off = (uint32_t)((long)min(m0 + row, p.M - 1) * (4 * RTp) + (s4 & 1) * (2 * RTp) + 2 * col);
+        dma16(mb, off, ldsA0 + buf * ABUF + (ALD * pw + i) * 1024);
+      }
+      u32x4 vb[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        vb[q] = *reinterpret_cast<const u32x4*>(p.l1cat + (long)nrow * RTp + 16 * (2 * e + (q >> 1)) + 8 * (q & 1));
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) {
+        *reinterpret_cast<u32x4*>(&sB[buf][boff + 32 * pt]) = vb[2 * (pt >> 1)];
+        *reinterpret_cast<u32x4*>(&sB[buf][boff + 32 * pt + 16]) = vb[2 * (pt >> 1) + 1];
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    auto pstage = [&](int st, auto q_c) {
+      using QN = std::integral_constant<int, (decltype(q_c)::value + 1) % D>;
+      const int buf = st & 1;
+      if (st + 1 < nst) {
+        // stage st + 1: x_hat by DMA, codes from set q + 1 (loaded during stage st - 1); stage
+        // st + 2's codes into set q
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        mark_set(QN{});
+        dma_a(st + 1, buf ^ 1);
+        gload(min(st + D, nst - 1), q_c);
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) lstore_part(buf ^ 1, QN{}, pt);
+        asm volatile("s_waitcnt vmcnt(3)" ::: "memory");   // the x_hat DMA landed
+      } else if (st + 1 < nall) {
+        xstage(st + 1 - nst, buf ^ 1);
+      }
+      __syncthreads();
+    };
+    int st = 0;
+    for (; st + D <= nall; st += D) {
+      pstage(st, Q0{});
+      pstage(st + 1, Q1{});
+    }
+    if (st < nall) pstage(st, Q0{});
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < D; ++q) asm volatile("" ::"v"(rb[q][0]), "v"(rb[q][1]), "v"(rs[q]));
+    return;
+  }
+
+  // ---- consumer (issues ahead of the producer on its SIMD) ----
+  __builtin_amdgcn_s_setprio(1);
+  const int wm = wave >> 1, wn = wave & 1;
+  f32x16 acc[RI][4];
+#pragma unroll
+  for (int i = 0; i < RI; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  const int r0 = (TBM / 2) * wm + lr, swz = (r0 >> 1) & 7;
+  const int rb0 = (128 * wn + lr) * PITCH + 16 * h;
+  __syncthreads();
+  auto cstage = [&](int st) {
+    const int buf = st & 1;
+    // units u = 4 ks + j: the 3 MFMAs of B fragment j of k-step ks (one B register set in use, so
+    // the 192 accumulators fit); the next unit's B fragment and the next k-step's A fragments are
+    // read while a unit's MFMAs run
+    u32x4 a[2][RI], b[2];
+    auto read_a = [&](int ks, u32x4 (&fa)[RI]) {
+#pragma unroll
+      for (int i = 0; i < RI; ++i) fa[i] = *reinterpret_cast<const u32x4*>(&sA[buf][r0 * 128 + 4096 * i + 16 * ((2 * ks + h) ^ swz)]);
+    };
+    auto read_b = [&](int u, u32x4& fb) {
+      fb = *reinterpret_cast<const u32x4*>(&sB[buf][rb0 + 32 * (u & 3) * PITCH + 32 * (u >> 2)]);
+    };
+    read_a(0, a[0]);
+    read_b(0, b[0]);
+#pragma unroll
+    for (int u = 0; u < 4 * (KB / 16); ++u) {
+      const int ks = u >> 2, j = u & 3;
+      if (u + 1 < 4 * (KB / 16)) read_b(u + 1, b[(u + 1) & 1]);
+      if (j == 0 && ks + 1 < KB / 16) read_a(ks + 1, a[(ks + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < RI; ++i) acc[i][j] = mfma_bf16_32x32x16(a[ks & 1][i], b[u & 1], acc[i][j]);
+    }
+    __syncthreads();
+  };
+  for (int st = 0; st < nall; ++st) cstage(st);
+  GemmParams pe = p;   // the low-rank term is in the accumulators: bias and store only
+  pe.RTp = 0;
+  const int wrow = m0 + (TBM / 2) * wm, wend = wrow + TBM / 2;
+#pragma unroll
+  for (int qi = 0; qi < (RI + 1) / 2; ++qi)
+#pragma unroll
+    for (int qj = 0; qj < 2; ++qj) {
+      const int i1 = 2 * qi + 1 < RI ? 2 * qi + 1 : 2 * qi;
+      f32x16 part[2][2] = {{acc[2 * qi][2 * qj], acc[2 * qi][2 * qj + 1]}, {acc[i1][2 * qj], acc[i1][2 * qj + 1]}};
+      epilogue<OUT_F32>(pe, part, wrow + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096,
+                        nullptr, nullptr, 0, 0, wend);
+    }
+}
+
 // W4A4 GEMM for group sizes other than 64 / 128 (any multiple of 16 dividing K): the generic path.
 // Operands are the int8 codes 16 q (SVDQ_OPERAND_I8 layout: within each chunk of 8 columns the even
 // columns, then the odd ones, identically for activations and weights, so the order cancels).  K
@@ -1994,6 +2197,21 @@ hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st
     else w4a16_wide_kernel<GG, false, false, TT><<<grid, 256, 0, st>>>(p);                  \
     return hipGetLastError();                                                               \
   }
+    // the 192-row tiles on specialized waves (w4a16_ws_kernel) unless SVDQ_W4A16_KERNEL=wide
+    const char* ke = getenv("SVDQ_W4A16_KERNEL");
+    if (t192 && !p.epi && !(ke && !strcmp(ke, "wide"))) {
+      const dim3 grid((unsigned)tiles192);
+      if (G == 64) {
+        if (out_f32) w4a16_ws_kernel<64, true><<<grid, 512, 0, st>>>(p);
+        else w4a16_ws_kernel<64, false><<<grid, 512, 0, st>>>(p);
+        return hipGetLastError();
+      }
+      if (G == 128) {
+        if (out_f32) w4a16_ws_kernel<128, true><<<grid, 512, 0, st>>>(p);
+        else w4a16_ws_kernel<128, false><<<grid, 512, 0, st>>>(p);
+        return hipGetLastError();
+      }
+    }
     if (t192) {
       SVDQ_W4A16W(64, 192)
       SVDQ_W4A16W(128, 192)

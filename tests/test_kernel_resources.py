@@ -17,7 +17,7 @@ import pytest
 from tests.test_dma_hazards import LIB, _gfx950_code_objects
 
 READOBJ = "/opt/rocm/llvm/bin/llvm-readobj"
-ASYNC_VGPR_LOAD_KERNELS = ("w4a16_kernel", "w4a16_wide_kernel")
+ASYNC_VGPR_LOAD_KERNELS = ("w4a16_kernel", "w4a16_wide_kernel", "w4a16_ws_kernel")
 
 
 def _kernel_metadata() -> dict[str, dict[str, int]]:
