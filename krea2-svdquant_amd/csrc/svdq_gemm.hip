@@ -2197,9 +2197,11 @@ hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st
     else w4a16_wide_kernel<GG, false, false, TT><<<grid, 256, 0, st>>>(p);                  \
     return hipGetLastError();                                                               \
   }
-    // the 192-row tiles on specialized waves (w4a16_ws_kernel) unless SVDQ_W4A16_KERNEL=wide
+    // the 192-row tiles on specialized waves (w4a16_ws_kernel; its x_hat DMA moves 16-byte chunks:
+    // rows 16-byte aligned) unless SVDQ_W4A16_KERNEL=wide
     const char* ke = getenv("SVDQ_W4A16_KERNEL");
-    if (t192 && !p.epi && !(ke && !strcmp(ke, "wide"))) {
+    const bool xa = (reinterpret_cast<uintptr_t>(p.xhat) & 15) == 0 && p.ldxh % 8 == 0;
+    if (t192 && !p.epi && xa && !(ke && !strcmp(ke, "wide"))) {
       const dim3 grid((unsigned)tiles192);
       if (G == 64) {
         if (out_f32) w4a16_ws_kernel<64, true><<<grid, 512, 0, st>>>(p);
