@@ -1773,6 +1773,8 @@ __global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
   using Q0 = std::integral_constant<int, 0>;
   using Q1 = std::integral_constant<int, 1>;
 
+  // The role is wave-uniform, and both roles pass the same barriers: one after the first stage is
+  // staged, then one per stage (the staging waves leave after the last; the epilogue has none).
   if (wave >= 4) {
     // ---- producer ----
     const int ptid = tid - NT, pw = wave - 4;
@@ -1798,6 +1800,7 @@ __global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
     const int boff = ptid * PITCH;
     u32x4 rb[D][2];
     uint32_t rs[D];
+    constexpr int CL = 3;   // loads per set: two 16-byte code loads and the scale
     auto gload_set = [&](int st, u32x4 (&db)[2], uint32_t& ds) {
       const int k0 = st * KB;
       asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(db[0]) : "v"(brow + k0 / 2) : "memory");
@@ -1834,7 +1837,7 @@ __global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
     dma_a(0, 0);
     gload(0, Q0{});
     gload(min(1, nst - 1), Q1{});
-    asm volatile("s_waitcnt vmcnt(3)" ::: "memory");   // x_hat and codes of stage 0
+    asm volatile("s_waitcnt vmcnt(%c0)" ::"i"(CL) : "memory");   // x_hat and codes of stage 0
     mark_set(Q0{});
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) lstore_part(0, Q0{}, pt);
@@ -1871,7 +1874,7 @@ __global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
         gload(min(st + D, nst - 1), q_c);
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) lstore_part(buf ^ 1, QN{}, pt);
-        asm volatile("s_waitcnt vmcnt(3)" ::: "memory");   // the x_hat DMA landed
+        asm volatile("s_waitcnt vmcnt(%c0)" ::"i"(CL) : "memory");   // the x_hat DMA landed
       } else if (st + 1 < nall) {
         xstage(st + 1 - nst, buf ^ 1);
       }
