@@ -1779,7 +1779,9 @@ __global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
     // ---- producer ----
     const int ptid = tid - NT, pw = wave - 4;
     // x_hat DMA: instruction t (6 per wave: t = 6 pw + i) moves rows 8 t .. 8 t + 7; lane -> row
-    // 8 t + lane / 8, LDS position lane % 8 holding chunk (lane % 8) ^ ((row >> 1) & 7)
+    // 8 t + lane / 8, LDS position lane % 8 holding chunk (lane % 8) ^ ((row >> 1) & 7).  The
+    // per-lane offsets are 32-bit: the launcher takes this kernel only where (M - 1) * ldxh * 2
+    // and M * 4 * RTp (the mid planes of the low-rank stages) stay below 2^32.
     const int rr = lane >> 3, jj = lane & 7;
     const long ldb = p.ldxh * 2;
     uint32_t aoffs[ALD];
@@ -2201,10 +2203,13 @@ hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st
     return hipGetLastError();                                                               \
   }
     // the 192-row tiles on specialized waves (w4a16_ws_kernel; its x_hat DMA moves 16-byte chunks:
-    // rows 16-byte aligned) unless SVDQ_W4A16_KERNEL=wide
+    // rows 16-byte aligned) unless SVDQ_W4A16_KERNEL=wide.  Its DMA addresses a row by a 32-bit
+    // byte offset from the x_hat base (row * ldxh * 2) and from the mid planes' (row * 4 * RTp):
+    // larger operands take the register-staged kernel, which addresses rows in 64 bits.
     const char* ke = getenv("SVDQ_W4A16_KERNEL");
     const bool xa = (reinterpret_cast<uintptr_t>(p.xhat) & 15) == 0 && p.ldxh % 8 == 0;
-    if (t192 && !p.epi && xa && !(ke && !strcmp(ke, "wide"))) {
+    const bool off32 = ((long)p.M - 1) * p.ldxh * 2 + 128 <= 0xFFFFFFFFL && (long)p.M * 4 * p.RTp <= 0xFFFFFFFFL;
+    if (t192 && !p.epi && xa && off32 && !(ke && !strcmp(ke, "wide"))) {
       const dim3 grid((unsigned)tiles192);
       if (G == 64) {
         if (out_f32) w4a16_ws_kernel<64, true><<<grid, 512, 0, st>>>(p);
