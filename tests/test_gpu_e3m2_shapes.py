@@ -1,6 +1,7 @@
 """GPU parity of the production W4A4 path (e3m2 operands on the FP6 MFMA, the default) at the
 BASELINE shapes: config 0, the config 1 shapes at M=4096 (ff.up, ff.down with K=16384, to_k with
-N=1536) and config 4 (M=16384, ff.up and ff.down with a rank-64 LoRA on the rank-32 branch).
+N=1536) and config 4 (M=16384, ff.up and ff.down with a rank-64 LoRA on the rank-32 branch); and an
+activation operand of more than 2^31 elements on both tilings (M=131200 / 131328, K=16384).
 
 Bars: the e3m2 activation operand (decoded through the format definition, independently of the
 encoder) and the sx pairs bit-exact against the oracle quantizer; layer outputs in float32 mode
@@ -118,6 +119,25 @@ def test_config4_lora_e3m2(dev, name, n, k):
     _check_codes(dev, x, prep, st, rows)
     y = _check_rows(dev, x, prep, st, rows, f"config4 {name} e3m2 + LoRA r64")
     _check_homogeneity(dev, x, prep, y, None)    # the LoRA branch (on raw x) is linear in x too
+
+
+@pytest.mark.parametrize("m,n", [(131200, 256), (131328, 512)])
+def test_large_rows_e3m2(dev, m, n):
+    """An activation operand of more than 2^31 elements (K=16384): the e3m2 codes, sx pairs and
+    outputs of sampled rows, the last ones included, against the oracle (M=131200 takes the
+    256 x 128 tiles, M=131328 with N=512 the 256 x 256 tiles)."""
+    from krea2_svdquant_amd.kernels.hip import backend, lib, ops
+    k = 16384
+    assert m * k > 2 ** 31
+    cols = lib.w4a4_tile_cols(m, n, k, 64, ops.OPERAND_E3M2)
+    print(f"e3m2 with M*K > 2^31: M={m} K={k} N={n}, tile columns {cols}", flush=True)
+    assert cols == (256 if m % 256 == 0 else 128)
+    x, ds = _gpu_layer(dev, m, k, n, seed=m + n)
+    prep = backend.prepare_layer(ds, (), dev)
+    st = from_device_state(ds)
+    rows = np.unique(np.concatenate([_rows(m, 16, 5), np.arange(m - 8, m)]))
+    _check_codes(dev, x, prep, st, rows)
+    _check_rows(dev, x, prep, st, rows, f"M={m} e3m2")
 
 
 @pytest.mark.parametrize("m,k,g", [(1, 64, 64), (5, 448, 64), (64, 1024, 64), (100, 768, 128), (257, 1536, 64),
