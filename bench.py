@@ -330,16 +330,35 @@ def block_line(args, dev) -> dict:
 def w4a16_line(args, dev) -> dict:
     """the 8 block shapes, W4A16 at M=2304 (768x768 latent), each timed alone
     (and the block in order, siblings sequential / concurrent)."""
+    import torch
+    from krea2_svdquant_amd.kernels.hip import ops as hip_ops
     b = block_layers(args, dev, 2304, "w4a16", 200)
     total = b["total"]
     tflops = b["ops"] / (total * 1e-3) / 1e12
+    # ff.up's GEMM alone: x_hat and the low-rank operand computed once, then the W4A16 GEMM (with its
+    # low-rank epilogue) over and over
+    m, n, k = 2304, 16384, 6144
+    x, _, prep = make_layer(n, k, m, args.rank, args.group, dev, seed=900)
+    _, _, _, xhat, mid = hip_ops.act_quant(x, prep.srs, prep.l2, prep.lora_down, prep.lora_mult, prep.group_size,
+                                           prep.rtp, hip_ops.OPERAND_NONE, False, True, False)
+    gemm = lambda: hip_ops.w4a16_gemm(xhat, prep.qweight, prep.weight_scales, mid, prep.l1cat, prep.bias,  # noqa: E731
+                                      prep.group_size, False)
+    for _ in range(5):
+        gemm()
+    ms_gemm = time_avg(gemm, 50)
+    tf_gemm = 2.0 * m * n * k / (ms_gemm * 1e-3) / 1e12
+    del x, prep, xhat, mid
+    torch.cuda.empty_cache()
     return {"ms_per_layer": b["per"], "ms_per_block_linears": round(total, 4), "TFLOPs": round(tflops, 1),
             "bf16_peak_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
             "ms_per_block_in_order": round(b["seq"], 4),
             "ms_per_block_in_order_concurrent_siblings": round(b["conc"], 4),
+            "ffup_gemm_ms": round(ms_gemm, 4), "ffup_gemm_TFLOPs": round(tf_gemm, 1),
+            "ffup_gemm_bf16_peak_frac": round(tf_gemm / BF16_PEAK_TFLOPS, 4),
             "note": "W4A16 (bf16 x_hat x in-register dequantized INT4 weights, bf16 MFMA), M=2304, layer = "
                     "x_hat pass + GEMM with low-rank epilogue; ms_per_block_linears = each layer timed alone, "
-                    "summed; *_in_order as in block_config1"}
+                    "summed; *_in_order as in block_config1; ffup_gemm_* = ff.up's GEMM alone (HIP events over "
+                    "50 back-to-back calls on one x_hat; the specialized-wave kernel at this shape)"}
 
 
 def lora_line(args, dev) -> dict:
