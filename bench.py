@@ -1,6 +1,6 @@
-"""Benchmark of the W4A4 SVDQuantLinear forward on one MI355X (the BASELINE metric).
+"""Benchmark of the W4A4 SVDQuantLinear forward on one MI355X (the headline metric).
 
-Workload (the shape the metric is quoted on): the ff.up linear of a
+Workload (benchmark config 1, the shape the metric is quoted on): the ff.up linear of a
 Krea-2 block, M=4096 tokens (1024x1024 latent), K=6144 -> N=16384, rank 32, group 64, W4A4.
 Synthetic inputs: X bf16 ~ N(0,1) with 1% outlier channels x20; W fp32 ~ N(0, 0.02) quantized
 on the GPU by the package converter (smoothing, rank-32 SVD, INT4 residual), random init.
@@ -11,7 +11,7 @@ with its inputs resident in HBM.  ``value`` = effective TOPS = 2*M*N*K / step ti
 ``roofline`` prices the dominant kernel, the W4A4 GEMM, against the MI355X dense peak of the
 MFMA it issues: the FP6 MFMA (10.1 PFLOP/s; every INT4 code is an exact e3m2 value) by default,
 the FP8 one (5.0) with ``--operand e4m3``; ``int8_dense_peak_frac`` restates the achieved rate
-against the dense INT8 peak (5.0 POP/s) the BASELINE north star names.  Its average launch
+against the dense INT8 peak (5.0 POP/s) the north star names.  Its average launch
 duration is measured here with HIP events on the stream the kernel is launched on (torch's
 current stream, which the custom ops use).  ``traffic`` (HBM bytes per launch) comes from the
 rocprofv3 FETCH_SIZE / WRITE_SIZE passes committed in profiles/w4a4_gemm_ffup_traffic.md
@@ -51,7 +51,7 @@ KERNEL_NAME = {"e3m2": "w4a4_e3m2_kernel<64,false> (256x128 tiles; FP6 MFMA on e
                "e4m3": "w4a4_kernel<64,0,false> (FP8 MFMA on exact INT4 codes)",
                "i8": "w4a4_kernel<64,1,false> (INT8 MFMA on 16*q)"}
 TRAFFIC_SUMMARY = ROOT / "profiles" / "w4a4_gemm_ffup_traffic.md"
-# (name, N, K) of the 8 quantized linears of one Krea-2 block
+# (name, N, K) of the 8 quantized linears of one Krea-2 block (benchmark config 1)
 BLOCK_SHAPES = [("to_q", 6144, 6144), ("to_gate", 6144, 6144), ("to_k", 1536, 6144), ("to_v", 1536, 6144),
                 ("to_out.0", 6144, 6144), ("ff.gate", 16384, 6144), ("ff.up", 16384, 6144),
                 ("ff.down", 6144, 16384)]
@@ -149,7 +149,7 @@ def cpu_model() -> str:
 
 
 def make_layer(n: int, k: int, m: int, r: int, g: int, dev, seed: int):
-    """Synthetic BASELINE layer: X with outlier channels, W ~ N(0, 0.02), converted on the GPU."""
+    """Synthetic benchmark layer: X with outlier channels, W ~ N(0, 0.02), converted on the GPU."""
     import torch
     from krea2_svdquant_amd.kernels.hip import backend
     from krea2_svdquant_amd.quant.convert import convert_linear
@@ -272,7 +272,7 @@ def peak_fracs(tops: float) -> dict:
 
 
 def config0_line(args, dev) -> dict:
-    """one to_q-shaped layer, M=256, K=N=6144 (rank 32, group 64): the GPU
+    """benchmark config 0: one to_q-shaped layer, M=256, K=N=6144 (rank 32, group 64): the GPU
     forward and, on the host, the restated reference pytorch_sim forward at the same shape."""
     import torch
     from krea2_svdquant_amd.kernels.hip import backend
@@ -328,7 +328,7 @@ def block_line(args, dev) -> dict:
 
 
 def w4a16_line(args, dev) -> dict:
-    """the 8 block shapes, W4A16 at M=2304 (768x768 latent), each timed alone
+    """benchmark config 2: the 8 block shapes, W4A16 at M=2304 (768x768 latent), each timed alone
     (and the block in order, siblings sequential / concurrent)."""
     import torch
     from krea2_svdquant_amd.kernels.hip import ops as hip_ops
@@ -362,7 +362,7 @@ def w4a16_line(args, dev) -> dict:
 
 
 def lora_line(args, dev) -> dict:
-    """batch-4 1024px (M=16384) ff.up and ff.down, W4A4, fused LoRA rank 64."""
+    """benchmark config 4: batch-4 1024px (M=16384) ff.up and ff.down, W4A4, fused LoRA rank 64."""
     import torch
     from krea2_svdquant_amd.kernels.hip import backend
     out = {}
@@ -456,7 +456,7 @@ def sibling_options_line(args, dev) -> dict:
 
 
 def denoise_line(args, dev) -> dict:
-    """the 28-block stand-in Krea-2 denoiser, 1024px (4096 latent + 256 text
+    """benchmark config 3: the 28-block stand-in Krea-2 denoiser, 1024px (4096 latent + 256 text
     tokens, one stream of M=4352), batch 1, 8 Euler steps, every block resident in HBM."""
     import torch
     from krea2_svdquant_amd.runtime.krea2_standin import Krea2Dims, Krea2StandInTransformer
@@ -489,7 +489,7 @@ def denoise_line(args, dev) -> dict:
     same_sib = bool(torch.equal(lat, lat_sib))
     same_seq = bool(torch.equal(lat, lat_seq))
     # the same steps with the attention on PyTorch's fused SDPA kernels, and with the norms and
-    # gate ops in torch as well (config 3 as BASELINE states it: everything but the linears in
+    # gate ops in torch as well (config 3 as the benchmark defines it: everything but the linears in
     # PyTorch-ROCm)
     from krea2_svdquant_amd.runtime import krea2_standin as ks
     try:
@@ -540,7 +540,7 @@ def denoise_line(args, dev) -> dict:
                     "SwiGLU product (svdq::gate_op) on gfx950 kernels, gated residuals as torch.addcmul "
                     "(ms_per_denoise_step). Variants: *_sdpa_attention: the attention on PyTorch's fused SDPA "
                     "kernels; *_torch_attention_norms_gates: attention, norms and gate ops in PyTorch-ROCm (the "
-                    "configuration as BASELINE states it); *_fused_epilogues: sigmoid gate, SwiGLU product and "
+                    "configuration as the benchmark defines it); *_fused_epilogues: sigmoid gate, SwiGLU product and "
                     "gated residuals fused into the stores of to_gate, ff.up, to_out.0 and ff.down; "
                     "*_sequential_siblings: the sibling linears one after another, *_concurrent_siblings: on "
                     "side streams. Random-init quantized weights, N(0,1) tokens; HIP events around 8 Euler "

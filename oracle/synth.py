@@ -86,7 +86,7 @@ def make_layer(n: int, k: int, x_sample: np.ndarray, *, rank: int = 32, group_si
 
 def make_adapter(n: int, k: int, rank: int = 64, std: float = 0.01, scale: float = 0.8,
                  network_alpha: float | None = None, seed: int = 4) -> Adapter:
-    """LoRA rank ``rank`` with A, B ~ N(0, std) stored in bf16."""
+    """LoRA rank ``rank`` with A, B ~ N(0, std) stored in bf16 (benchmark config 4)."""
     rng = np.random.default_rng(seed)
     down = bf16(rng.standard_normal((rank, k), dtype=np.float32) * np.float32(std))
     up = bf16(rng.standard_normal((n, rank), dtype=np.float32) * np.float32(std))

@@ -1,4 +1,4 @@
-"""GPU parity of the W4A16 path at BASELINE config 2's own shapes: M=2304 (768x768 latent), the
+"""GPU parity of the W4A16 path at benchmark config 2's own shapes: M=2304 (768x768 latent), the
 four distinct (N, K) shapes of a Krea-2 block's eight linears (to_q / to_gate / to_out.0
 6144->6144, to_k / to_v 6144->1536, ff.gate / ff.up 6144->16384, ff.down 16384->6144), rank 32,
 group 64, outlier activations, layers converted on the GPU as bench.py builds them.

@@ -1,5 +1,5 @@
 """GPU parity of the production W4A4 path (e3m2 operands on the FP6 MFMA, the default) at the
-BASELINE shapes: config 0, the config 1 shapes at M=4096 (ff.up, ff.down with K=16384, to_k with
+benchmark shapes: config 0, the config 1 shapes at M=4096 (ff.up, ff.down with K=16384, to_k with
 N=1536) and config 4 (M=16384, ff.up and ff.down with a rank-64 LoRA on the rank-32 branch); and an
 activation operand of more than 2^31 elements on both tilings (M=131200 / 131328, K=16384).
 

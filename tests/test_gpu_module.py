@@ -1,4 +1,4 @@
-"""GPU tests of the module boundary (SVDQuantLinear) and BASELINE-sized layers."""
+"""GPU tests of the module boundary (SVDQuantLinear) and benchmark-sized layers."""
 import numpy as np
 import pytest
 import torch
@@ -61,7 +61,7 @@ def test_w4a16_module_matches_sim_math(dev):
 
 
 def test_config0_layer(dev):
-    """BASELINE config 0 shape: M=256, K=N=6144, rank 32, group 64, outlier channels."""
+    """benchmark config 0 shape: M=256, K=N=6144, rank 32, group 64, outlier channels."""
     from krea2_svdquant_amd.kernels.hip import backend
     x = synth.make_activation(256, 6144, seed=0)
     st = synth.make_layer(6144, 6144, x, rank=32, group_size=64, seed=1)

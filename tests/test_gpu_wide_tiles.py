@@ -3,7 +3,7 @@
 Both run the same per-output arithmetic (group sums on the FP6 MFMA, scale products on the bf16
 MFMA, the rescale FMAs in group order, the same epilogue), so a shape run on either tiling must give
 bit-identical outputs.  ``SVDQ_W4A4_TILES`` forces one tiling; the wide tiles need M, N and K
-multiples of 256.  The automatic choice at the BASELINE shapes (ff.up takes the wide tiles) is
+multiples of 256.  The automatic choice at the benchmark shapes (ff.up takes the wide tiles) is
 covered against the oracle by ``test_gpu_e3m2_shapes.py``.
 """
 import os

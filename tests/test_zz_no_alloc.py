@@ -79,7 +79,7 @@ def test_noalloc_matches_workspace_entry_point_twice_then_smaller(dev):
 
 
 def test_noalloc_config1_ffup_rows(dev):
-    """The BASELINE layer size (M=4096, K=6144, rank 32): the activation pass's K splits of 4096 x 32
+    """The benchmark layer size (M=4096, K=6144, rank 32): the activation pass's K splits of 4096 x 32
     f32 partials (7 at this size, 3.5 MiB) in the file-scope array."""
     from krea2_svdquant_amd.kernels.hip import backend
     x = synth.make_activation(4096, 6144, seed=71)
