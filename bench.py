@@ -11,7 +11,7 @@ with its inputs resident in HBM.  ``value`` = effective TOPS = 2*M*N*K / step ti
 ``roofline`` prices the dominant kernel, the W4A4 GEMM, against the MI355X dense peak of the
 MFMA it issues: the FP6 MFMA (10.1 PFLOP/s; every INT4 code is an exact e3m2 value) by default,
 the FP8 one (5.0) with ``--operand e4m3``; ``int8_dense_peak_frac`` restates the achieved rate
-against the dense INT8 peak (5.0 POP/s) the north star names.  Its average launch
+against the dense INT8 peak (5.0 POP/s), the peak the performance target is stated against.  Its average launch
 duration is measured here with HIP events on the stream the kernel is launched on (torch's
 current stream, which the custom ops use).  ``traffic`` (HBM bytes per launch) comes from the
 rocprofv3 FETCH_SIZE / WRITE_SIZE passes committed in profiles/w4a4_gemm_ffup_traffic.md
@@ -265,7 +265,7 @@ def block_layers(args, dev, m: int, mode: str, seed0: int) -> dict:
 
 
 def peak_fracs(tops: float) -> dict:
-    """An effective rate against the dense INT8 peak the north star names and the FP6 peak of the
+    """An effective rate against the dense INT8 peak the performance target is stated against and the FP6 peak of the
     MFMA the W4A4 GEMM issues."""
     return {"int8_dense_peak_frac": round(tops / INT8_PEAK_TOPS, 4),
             "fp6_dense_peak_frac": round(tops / MFMA_PEAK_TFLOPS["e3m2"], 4)}

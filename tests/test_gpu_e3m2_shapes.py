@@ -6,7 +6,7 @@ activation operand of more than 2^31 elements on both tilings (M=131200 / 131328
 Bars: the e3m2 activation operand (decoded through the format definition, independently of the
 encoder) and the sx pairs bit-exact against the oracle quantizer; layer outputs in float32 mode
 within relative L2 1e-4 of the float64 evaluation of the quantized math, bf16 outputs within 1e-3
-of bf16(oracle) (the north star allows 1e-3 for both); and, over whole outputs, the exact
+of bf16(oracle) (1e-3 is the tolerance allowed for both); and, over whole outputs, the exact
 power-of-two homogeneity y(2x) - b = 2 (y(x) - b).  Large layers are built on the GPU by the
 package converter and checked on a row sample (every row of x is quantized and multiplied
 independently).

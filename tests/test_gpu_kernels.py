@@ -1,6 +1,6 @@
 """GPU parity of the gfx950 kernels against the CPU oracle (through the C-ABI custom ops).
 
-Bars (north star): activation codes, scales and x_hat bit-exact; GEMM / layer outputs within
+Bars: activation codes, scales and x_hat bit-exact; GEMM / layer outputs within
 relative L2 1e-3 of the float64 evaluation of the same quantized math -- in float32-output mode
 directly, in bf16-output mode against bf16(oracle) (a bf16 store alone costs ~1.7e-3 against
 float32, so the bf16 output is compared with the rounded reference).  Float32 mode is also
