@@ -1048,7 +1048,44 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_siblings_kernel(GemmSiblings
 // the sx operand of the next step are read at the top of the step into the other register set;
 // the B fragments and weight-scale operands of the next group are read in the group's last step,
 // after its MFMAs have taken the current ones (one set).
-template <bool OUT_F32>
+// The low-rank term mid @ l1cat^T of one 64 x 64 output block with its operands in LDS, 32 ranks:
+// the tile's mid rows (128 bytes: hi plane, lo plane; 16-byte chunk c of row r at
+// c ^ ((r >> 1) & 7)) and l1cat rows (64 bytes; chunk c of row r at c ^ ((r >> 2) & 3)); wr / wc =
+// the block's first row / column in the tile.  Each accumulator takes hi_k then lo_k for the two
+// 16-rank steps, as in epilogue().
+__device__ __forceinline__ void lowrank_lds(f32x16 (&acc)[2][2], int lr, int h, const uint8_t* lmid,
+                                            const uint8_t* ll1, int wr, int wc) {
+  u32x4 ahi[2][2], alo[2][2], b[2][2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = wr + 32 * i + lr, sw = (r >> 1) & 7;
+      ahi[u][i] = ld16(lmid + r * 128 + 16 * ((2 * u + h) ^ sw));
+      alo[u][i] = ld16(lmid + r * 128 + 16 * ((4 + 2 * u + h) ^ sw));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = wc + 32 * j + lr;
+      b[u][j] = ld16(ll1 + c * 64 + 16 * ((2 * u + h) ^ ((c >> 2) & 3)));
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        acc[i][j] = mfma_bf16_32x32x16(ahi[u][i], b[u][j], acc[i][j]);
+        acc[i][j] = mfma_bf16_32x32x16(alo[u][i], b[u][j], acc[i][j]);
+      }
+}
+
+// CH: RTp of 64 .. 256 (a multiple of 32), the low-rank term streamed through the two LDS buffers
+// in chunks of 32 ranks after the main loop (chunk 0 prefetched by the last stage as for RTp = 32,
+// chunk c + 1's DMA under chunk c's MFMAs); without it those ranks read their operands from global
+// memory in the epilogue.  A separate build, so that the RTp = 32 kernel keeps its code.
+template <bool OUT_F32, bool CH = false>
 __device__ __forceinline__ void w4a4_e3m2_wide_tile(const GemmParams& p, int bm, int bn) {
   constexpr int TBM = 256, TBN = 256, KT = 2, GPS = 2, HPS = 8;
   constexpr int PQ = TBM * 16, PP = TBM * 8;             // bytes of one Q / P plane
@@ -1147,17 +1184,30 @@ __device__ __forceinline__ void w4a4_e3m2_wide_tile(const GemmParams& p, int bm,
   };
   // last stage, RTp == 32: the epilogue's low-rank operands -> the free buffer (256 mid rows of
   // 128 bytes, then 256 l1cat rows of 64 bytes), swizzled for the epilogue's reads
-  const bool epi_lds = p.RTp == 32;
-  auto epi_prefetch = [&](int fbuf) {
+  // CH: chunk cc = ranks 32 cc .. 32 cc + 31, 64 bytes of the hi plane and 64 of the lo plane per
+  // mid row (rows of 4 RTp bytes), 64 bytes per l1cat row (2 RTp bytes), in the RTp = 32 layout
+  const int nch = p.RTp / 32;
+  const bool epi_lds = CH || p.RTp == 32;
+  auto epi_prefetch = [&](int fbuf, int cc) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int idx = (4 * wave + c) * 64 + lane, r = idx >> 3, ch = (idx & 7) ^ ((r >> 1) & 7);
-      dma16(p.midp, (uint32_t)(m0 + r) * 128u + 16u * ch, lds0 + fbuf * BUF + (4 * wave + c) * 1024);
+      if constexpr (CH) {
+        const uint32_t src = (uint32_t)(m0 + r) * (uint32_t)(4 * p.RTp) + (uint32_t)((ch & 4) ? 2 * p.RTp : 0) +
+                             64u * cc + 16u * (ch & 3);
+        dma16(p.midp, src, lds0 + fbuf * BUF + (4 * wave + c) * 1024);
+      } else {
+        dma16(p.midp, (uint32_t)(m0 + r) * 128u + 16u * ch, lds0 + fbuf * BUF + (4 * wave + c) * 1024);
+      }
     }
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const int idx = (2 * wave + c) * 64 + lane, r = idx >> 2, ch = (idx & 3) ^ ((r >> 2) & 3);
-      dma16(p.l1cat, (uint32_t)(n0 + r) * 64u + 16u * ch, lds0 + fbuf * BUF + 32768 + (2 * wave + c) * 1024);
+      if constexpr (CH)
+        dma16(p.l1cat, (uint32_t)(n0 + r) * (uint32_t)(2 * p.RTp) + 64u * cc + 16u * ch,
+              lds0 + fbuf * BUF + 32768 + (2 * wave + c) * 1024);
+      else
+        dma16(p.l1cat, (uint32_t)(n0 + r) * 64u + 16u * ch, lds0 + fbuf * BUF + 32768 + (2 * wave + c) * 1024);
     }
   };
 
@@ -1178,7 +1228,7 @@ __device__ __forceinline__ void w4a4_e3m2_wide_tile(const GemmParams& p, int bm,
     for (int hh = 0; hh < HPS; ++hh) {
       const int gi = hh >> 2, i = hh & 3;
       const bool last = hh == HPS - 1;
-      if (LASTST && hh == 0 && epi_lds) epi_prefetch(nbuf);   // ahead of the step's MFMA results
+      if (LASTST && hh == 0 && epi_lds) epi_prefetch(nbuf, 0);   // ahead of the step's MFMA results
       // this step's fragments in place, the previous step's rescale issued
       asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(acc[2][0]),
                    "+v"(acc[2][1]), "+v"(acc[3][0]), "+v"(acc[3][1])::"memory");
@@ -1230,13 +1280,38 @@ __device__ __forceinline__ void w4a4_e3m2_wide_tile(const GemmParams& p, int bm,
   if (epi_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   uint8_t* stg = sm + BUF + wave * 4096;
-  const uint8_t* lmid = epi_lds ? sm : nullptr;
-  const uint8_t* ll1 = epi_lds ? sm + 32768 : nullptr;
+  if constexpr (CH) {
+    // chunk cc from buffer cc & 1, chunk cc + 1's DMA into the other while its MFMAs run (buffer 1
+    // is free once every wave is past the barrier above); each accumulator takes hi_k then lo_k for
+    // k = 0, 16, .. as in epilogue(); then bias, staging (buffer 1) and stores
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    f32x16(&a2)[2][2] = *reinterpret_cast<f32x16(*)[2][2]>(&acc[2 * u][0]);
-    unrotate_acc(a2);
-    epilogue<OUT_F32>(p, a2, m0 + 128 * wm + 64 * u, n0 + 64 * wn, lr, h, stg, lmid, ll1, 128 * wm + 64 * u, 64 * wn);
+    for (int u = 0; u < 2; ++u) unrotate_acc(*reinterpret_cast<f32x16(*)[2][2]>(&acc[2 * u][0]));
+    for (int cc = 0; cc < nch; ++cc) {
+      const int cb = cc & 1;
+      if (cc + 1 < nch) epi_prefetch(cb ^ 1, cc + 1);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        lowrank_lds(*reinterpret_cast<f32x16(*)[2][2]>(&acc[2 * u][0]), lr, h, sm + cb * BUF, sm + cb * BUF + 32768,
+                    128 * wm + 64 * u, 64 * wn);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // chunk cc + 1 landed
+      __syncthreads();                                     // and every wave is done with chunk cc
+    }
+    GemmParams pe = p;
+    pe.RTp = 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      epilogue<OUT_F32>(pe, *reinterpret_cast<f32x16(*)[2][2]>(&acc[2 * u][0]), m0 + 128 * wm + 64 * u,
+                        n0 + 64 * wn, lr, h, stg);
+  } else {
+    const uint8_t* lmid = epi_lds ? sm : nullptr;
+    const uint8_t* ll1 = epi_lds ? sm + 32768 : nullptr;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      f32x16(&a2)[2][2] = *reinterpret_cast<f32x16(*)[2][2]>(&acc[2 * u][0]);
+      unrotate_acc(a2);
+      epilogue<OUT_F32>(p, a2, m0 + 128 * wm + 64 * u, n0 + 64 * wn, lr, h, stg, lmid, ll1, 128 * wm + 64 * u,
+                        64 * wn);
+    }
   }
 }
 
@@ -1260,12 +1335,12 @@ bool wide_tiles_pay(long tiles_wide, long tiles_narrow) {
   return 2 * wide * 9 <= narrow * 10;
 }
 
-template <bool OUT_F32>
+template <bool OUT_F32, bool CH = false>
 __global__ void __launch_bounds__(512, 1) w4a4_e3m2_wide_kernel(GemmParams p) {
   const int nbm = (p.M + 255) / 256, nbn = (p.N + 255) / 256;
   int bm, bn;
   tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
-  w4a4_e3m2_wide_tile<OUT_F32>(p, bm, bn);
+  w4a4_e3m2_wide_tile<OUT_F32, CH>(p, bm, bn);
 }
 
 // Sibling layers on the wide tiles: as w4a4_e3m2_siblings_kernel with 256 x 256 tiles (tile0 counts
@@ -2073,8 +2148,15 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
   if (mode == 2) {
     if (G == 64 && !p.epi && use_wide_tiles(p.M, p.N, p.K)) {
       const dim3 wgrid((unsigned)(((p.M + 255) / 256) * ((p.N + 255) / 256)));
-      if (out_f32) w4a4_e3m2_wide_kernel<true><<<wgrid, 512, 0, st>>>(p);
-      else w4a4_e3m2_wide_kernel<false><<<wgrid, 512, 0, st>>>(p);
+      // ranks 64 .. 256 (LoRA adapters, larger SVD ranks): the low-rank term in LDS chunks
+      const bool ch = p.RTp > 32 && p.RTp <= 256 && p.RTp % 32 == 0;
+      if (ch) {
+        if (out_f32) w4a4_e3m2_wide_kernel<true, true><<<wgrid, 512, 0, st>>>(p);
+        else w4a4_e3m2_wide_kernel<false, true><<<wgrid, 512, 0, st>>>(p);
+      } else {
+        if (out_f32) w4a4_e3m2_wide_kernel<true><<<wgrid, 512, 0, st>>>(p);
+        else w4a4_e3m2_wide_kernel<false><<<wgrid, 512, 0, st>>>(p);
+      }
       return hipGetLastError();
     }
     const bool full = p.K % 512 == 0;   // two full 256-column stages per main-loop iteration
