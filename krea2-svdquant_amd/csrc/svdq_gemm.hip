@@ -609,6 +609,40 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
   epilogue<OUT_F32, EPI>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, sA + wave * 4096);
 }
 
+// The low-rank term mid @ l1cat^T of one 64 x 64 output block with its operands in LDS, 32 ranks:
+// the tile's mid rows (128 bytes: hi plane, lo plane; 16-byte chunk c of row r at
+// c ^ ((r >> 1) & 7)) and l1cat rows (64 bytes; chunk c of row r at c ^ ((r >> 2) & 3)); wr / wc =
+// the block's first row / column in the tile.  Each accumulator takes hi_k then lo_k for the two
+// 16-rank steps, as in epilogue().
+__device__ __forceinline__ void lowrank_lds(f32x16 (&acc)[2][2], int lr, int h, const uint8_t* lmid,
+                                            const uint8_t* ll1, int wr, int wc) {
+  u32x4 ahi[2][2], alo[2][2], b[2][2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = wr + 32 * i + lr, sw = (r >> 1) & 7;
+      ahi[u][i] = ld16(lmid + r * 128 + 16 * ((2 * u + h) ^ sw));
+      alo[u][i] = ld16(lmid + r * 128 + 16 * ((4 + 2 * u + h) ^ sw));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = wc + 32 * j + lr;
+      b[u][j] = ld16(ll1 + c * 64 + 16 * ((2 * u + h) ^ ((c >> 2) & 3)));
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        acc[i][j] = mfma_bf16_32x32x16(ahi[u][i], b[u][j], acc[i][j]);
+        acc[i][j] = mfma_bf16_32x32x16(alo[u][i], b[u][j], acc[i][j]);
+      }
+}
+
+
 // W4A4 GEMM on the FP6 MFMA (e3m2 operands, v_mfma_scale_f32_32x32x64_f8f6f4 with format 3 on
 // both sides): the INT4 codes are exact e3m2 values and the FP6 MFMA runs at twice the FP8 rate.
 // The arithmetic (exact group sums P, scale products S on the bf16 MFMA, acc += P * S), the wave
@@ -630,7 +664,10 @@ __global__ void __launch_bounds__(512, 1) w4a4_kernel(GemmParams p) {
 // offsets fold into the read and DMA instructions), no step carries a bound check, the last
 // stage is peeled (no DMA, the epilogue's prefetch), and the DMA sources are wave-uniform
 // pointers advanced one stage at a time.  Other K take the general loop.
-template <int G, bool OUT_F32, bool FULL, bool EPI = false>
+// CH: RTp of 64 .. 256 (a multiple of 32, no store ops), the low-rank term streamed through the
+// two LDS buffers in chunks of 32 ranks after the main loop (chunk 0 prefetched by the last stage
+// as for RTp = 32); a separate build, so that the other kernels keep their code.
+template <int G, bool OUT_F32, bool FULL, bool EPI = false, bool CH = false>
 __device__ __forceinline__ void w4a4_e3m2_tile(const GemmParams& p, int bm, int bn) {
   constexpr int TBM = 256, TBN = 128, NBUF = 2;
   constexpr int KB = 256;                     // K columns per pipeline stage
@@ -670,7 +707,8 @@ __device__ __forceinline__ void w4a4_e3m2_tile(const GemmParams& p, int bm, int 
   for (int c = 0; c < 2; ++c) bq_o[c] = (uint32_t)min(n0 + 64 * c + lane, p.N - 1) * 16u;
   const uint32_t bp_o = (uint32_t)min(n0 + 2 * lane, Np - 2) * 8u;
   const long aP0 = (long)nkt * 2 * Mp * 16, bP0 = (long)nkt * 2 * Np * 16;   // P region offsets
-  const bool epi_lds = p.RTp == 32;   // the epilogue's mid / l1cat rows fit the free buffer
+  const bool epi_lds = CH || p.RTp == 32;   // the epilogue's mid / l1cat rows fit the free buffer
+  const int nch = p.RTp / 32;                // CH: chunks of 32 ranks
   if (tid < NBUF * GPS * 4) {
     sX[tid / (4 * GPS)][(tid / 4) % GPS][TBM + tid % 4] = 0u;
     sW[tid / (4 * GPS)][(tid / 4) % GPS][TBN + tid % 4] = 0u;
@@ -769,14 +807,26 @@ __device__ __forceinline__ void w4a4_e3m2_tile(const GemmParams& p, int bm, int 
   // last stage, RTp == 32: the epilogue's low-rank operands -> the free buffer (its A Q area:
   // 256 mid rows of 128 bytes; its B Q area: 128 l1cat rows of 64 bytes), swizzled for the
   // epilogue's reads
-  auto epi_prefetch = [&](int fbuf) {
+  // (CH: chunk cc = ranks 32 cc .. 32 cc + 31 of mid rows of 4 RTp bytes and l1cat rows of 2 RTp
+  // bytes, in the same LDS layout)
+  auto epi_prefetch = [&](int fbuf, int cc) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int idx = (4 * wave + c) * 64 + lane, r = idx >> 3, ch = (idx & 7) ^ ((r >> 1) & 7);
-      dma16<EPI>(p.midp, (uint32_t)min(m0 + r, p.M - 1) * 128u + 16u * ch, ldsAQ + fbuf * AQ + (4 * wave + c) * 1024);
+      if constexpr (CH) {
+        const uint32_t src = (uint32_t)min(m0 + r, p.M - 1) * (uint32_t)(4 * p.RTp) +
+                             (uint32_t)((ch & 4) ? 2 * p.RTp : 0) + 64u * cc + 16u * (ch & 3);
+        dma16<EPI>(p.midp, src, ldsAQ + fbuf * AQ + (4 * wave + c) * 1024);
+      } else {
+        dma16<EPI>(p.midp, (uint32_t)min(m0 + r, p.M - 1) * 128u + 16u * ch, ldsAQ + fbuf * AQ + (4 * wave + c) * 1024);
+      }
     }
     const int idx = wave * 64 + lane, r = idx >> 2, ch = (idx & 3) ^ ((r >> 2) & 3);
-    dma16<EPI>(p.l1cat, (uint32_t)min(n0 + r, p.N - 1) * 64u + 16u * ch, ldsBQ + fbuf * BQ + wave * 1024);
+    if constexpr (CH)
+      dma16<EPI>(p.l1cat, (uint32_t)min(n0 + r, p.N - 1) * (uint32_t)(2 * p.RTp) + 64u * cc + 16u * ch,
+                 ldsBQ + fbuf * BQ + wave * 1024);
+    else
+      dma16<EPI>(p.l1cat, (uint32_t)min(n0 + r, p.N - 1) * 64u + 16u * ch, ldsBQ + fbuf * BQ + wave * 1024);
   };
   // This step's fragments in place and the previous step's rescale issued before the next reads
   // go out (keeps one register set live per step).
@@ -894,7 +944,7 @@ __device__ __forceinline__ void w4a4_e3m2_tile(const GemmParams& p, int bm, int 
           for (int d = hh * PER; d < (hh + 1) * PER; ++d)
             if (d < NDMA) dma_next(nbuf, d);
         }
-        if (LASTST && hh == 0 && epi_lds) epi_prefetch(nbuf);
+        if (LASTST && hh == 0 && epi_lds) epi_prefetch(nbuf, 0);
         if (!RM) {
           if (!last) {
             read_half_full(buf, (hh + 1) >> 1, (hh + 1) & 1, 0, 0);
@@ -968,7 +1018,7 @@ __device__ __forceinline__ void w4a4_e3m2_tile(const GemmParams& p, int bm, int 
         for (int d = hh * PER; d < (hh + 1) * PER; ++d)
           if (d < NDMA) dma(s + 1, nbuf, d);
       }
-      if (!more && epi_lds && hh == 0) epi_prefetch(nbuf);
+      if (!more && epi_lds && hh == 0) epi_prefetch(nbuf, 0);
       if (!RM) {
         if (!last) {
           if (hg + 1 < H) read_half(buf, (hh + 1) >> 1, (hh + 1) & 1, 0, 0);
@@ -993,16 +1043,34 @@ __device__ __forceinline__ void w4a4_e3m2_tile(const GemmParams& p, int bm, int 
   if (epi_lds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   unrotate_acc(acc);
-  epilogue<OUT_F32, EPI>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[lbuf][0] + wave * 4096,
-                    epi_lds ? &sAQ[lbuf ^ 1][0] : nullptr, epi_lds ? &sBQ[lbuf ^ 1][0] : nullptr, 64 * wm, 64 * wn);
+  if constexpr (CH) {
+    // the low-rank term in chunks of 32 ranks: chunk cc in buffer lbuf ^ 1 ^ (cc & 1), chunk cc + 1's
+    // DMA into the other while chunk cc's MFMAs run (the last stage's buffer is free past the
+    // barrier above); each accumulator takes hi_k then lo_k for k = 0, 16, .. as in epilogue();
+    // then bias, staging (the last stage's A planes) and stores
+    for (int cc = 0; cc < nch; ++cc) {
+      const int cb = lbuf ^ 1 ^ (cc & 1);
+      if (cc + 1 < nch) epi_prefetch(cb ^ 1, cc + 1);
+      lowrank_lds(acc, lr, h, &sAQ[cb][0], &sBQ[cb][0], 64 * wm, 64 * wn);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // chunk cc + 1 landed
+      __syncthreads();                                     // and every wave is done with chunk cc
+    }
+    GemmParams pe = p;
+    pe.RTp = 0;
+    epilogue<OUT_F32, EPI>(pe, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[lbuf][0] + wave * 4096);
+  } else {
+    epilogue<OUT_F32, EPI>(p, acc, m0 + 64 * wm, n0 + 64 * wn, lr, h, &sAQ[lbuf][0] + wave * 4096,
+                           epi_lds ? &sAQ[lbuf ^ 1][0] : nullptr, epi_lds ? &sBQ[lbuf ^ 1][0] : nullptr, 64 * wm,
+                           64 * wn);
+  }
 }
 
-template <int G, bool OUT_F32, bool FULL, bool EPI = false>
+template <int G, bool OUT_F32, bool FULL, bool EPI = false, bool CH = false>
 __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
   const int nbm = (p.M + 255) / 256, nbn = (p.N + 127) / 128;
   int bm, bn;
   tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
-  w4a4_e3m2_tile<G, OUT_F32, FULL, EPI>(p, bm, bn);
+  w4a4_e3m2_tile<G, OUT_F32, FULL, EPI, CH>(p, bm, bn);
 }
 
 // Sibling layers (same rows M, same K and group) in one launch: the layers' 256 x 128 tiles are
@@ -1048,39 +1116,6 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_siblings_kernel(GemmSiblings
 // the sx operand of the next step are read at the top of the step into the other register set;
 // the B fragments and weight-scale operands of the next group are read in the group's last step,
 // after its MFMAs have taken the current ones (one set).
-// The low-rank term mid @ l1cat^T of one 64 x 64 output block with its operands in LDS, 32 ranks:
-// the tile's mid rows (128 bytes: hi plane, lo plane; 16-byte chunk c of row r at
-// c ^ ((r >> 1) & 7)) and l1cat rows (64 bytes; chunk c of row r at c ^ ((r >> 2) & 3)); wr / wc =
-// the block's first row / column in the tile.  Each accumulator takes hi_k then lo_k for the two
-// 16-rank steps, as in epilogue().
-__device__ __forceinline__ void lowrank_lds(f32x16 (&acc)[2][2], int lr, int h, const uint8_t* lmid,
-                                            const uint8_t* ll1, int wr, int wc) {
-  u32x4 ahi[2][2], alo[2][2], b[2][2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = wr + 32 * i + lr, sw = (r >> 1) & 7;
-      ahi[u][i] = ld16(lmid + r * 128 + 16 * ((2 * u + h) ^ sw));
-      alo[u][i] = ld16(lmid + r * 128 + 16 * ((4 + 2 * u + h) ^ sw));
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int c = wc + 32 * j + lr;
-      b[u][j] = ld16(ll1 + c * 64 + 16 * ((2 * u + h) ^ ((c >> 2) & 3)));
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        acc[i][j] = mfma_bf16_32x32x16(ahi[u][i], b[u][j], acc[i][j]);
-        acc[i][j] = mfma_bf16_32x32x16(alo[u][i], b[u][j], acc[i][j]);
-      }
-}
-
 // CH: RTp of 64 .. 256 (a multiple of 32), the low-rank term streamed through the two LDS buffers
 // in chunks of 32 ranks after the main loop (chunk 0 prefetched by the last stage as for RTp = 32,
 // chunk c + 1's DMA under chunk c's MFMAs); without it those ranks read their operands from global
@@ -2160,9 +2195,19 @@ hipError_t launch_w4a4(const GemmParams& p, int G, int mode, bool out_f32, hipSt
       return hipGetLastError();
     }
     const bool full = p.K % 512 == 0;   // two full 256-column stages per main-loop iteration
+    // ranks 64 .. 256 without store ops: the low-rank term in LDS chunks
+    const bool ch = !p.epi && p.RTp > 32 && p.RTp <= 256 && p.RTp % 32 == 0;
 #define SVDQ_E3M2(GG)                                                                  \
   if (G == GG) {                                                                       \
-    if (full) {                                                                        \
+    if (ch) {                                                                          \
+      if (full) {                                                                      \
+        if (out_f32) w4a4_e3m2_kernel<GG, true, true, false, true><<<grid, 512, 0, st>>>(p);   \
+        else w4a4_e3m2_kernel<GG, false, true, false, true><<<grid, 512, 0, st>>>(p);          \
+      } else {                                                                         \
+        if (out_f32) w4a4_e3m2_kernel<GG, true, false, false, true><<<grid, 512, 0, st>>>(p);  \
+        else w4a4_e3m2_kernel<GG, false, false, false, true><<<grid, 512, 0, st>>>(p);         \
+      }                                                                                \
+    } else if (full) {                                                                 \
       if (out_f32) w4a4_e3m2_kernel<GG, true, true><<<grid, 512, 0, st>>>(p);           \
       else if (p.epi) w4a4_e3m2_kernel<GG, false, true, true><<<grid, 512, 0, st>>>(p); \
       else w4a4_e3m2_kernel<GG, false, true><<<grid, 512, 0, st>>>(p);                  \

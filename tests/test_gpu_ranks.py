@@ -3,7 +3,8 @@
 The down projections run in launches of 4 MFMA column tiles of 32 (rank r in ceil(r/32) tiles, then
 the concatenated LoRA ranks): r = 64 with two rank-64 adapters (the reference's MLP rank with two
 adapters, 6 tiles) and r = 160 with a rank-48 adapter (the low-rank tiles themselves span both
-launches).  Reference: runtime/linear.py:88-111,156-161 (any number of adapters, each on the raw x).
+launches).  Padded ranks up to 256 take the GEMM's low-rank term in 32-rank LDS chunks; r = 32 with
+adapters of ranks 128, 128 and 40 (padded rank 352) takes its global-memory path.  Reference: runtime/linear.py:88-111,156-161 (any number of adapters, each on the raw x).
 """
 import numpy as np
 import pytest
@@ -18,7 +19,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("r,ranks,mode", [
     (64, (64, 64), "w4a4"), (64, (64, 64), "w4a16"),
-    (160, (48,), "w4a4"), (32, (128, 16, 40), "w4a4"),
+    (160, (48,), "w4a4"), (32, (128, 16, 40), "w4a4"), (32, (128, 128, 40), "w4a4"),
 ])
 def test_many_tiles_match_oracle(dev, r, ranks, mode):
     from krea2_svdquant_amd.kernels.hip import backend, ops

@@ -47,7 +47,7 @@ def _layers(dev, shapes, seed, bias=False):
 def test_wide_tiles_bit_identical_to_narrow(dev, m, n, k, lora, out_f32):
     from krea2_svdquant_amd.kernels.hip.backend import forward_prepared
     mod = _layers(dev, [(n, k)], seed=m + n + k, bias=True)[0]
-    if lora:   # rank 64 + 32: the epilogue's global-memory path (RTp 128)
+    if lora:   # LoRA ranks 64 + 32 on the rank-32 branch: RTp 128, the low-rank term in LDS chunks
         gen = torch.Generator(device=dev).manual_seed(7)
         for r in (64, 32):
             mod.add_lora_adapter((torch.randn(r, k, device=dev, generator=gen) * 0.02).to(torch.bfloat16),
