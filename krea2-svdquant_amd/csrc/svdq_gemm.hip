@@ -1077,8 +1077,9 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_kernel(GemmParams p) {
 // numbered back to back (layer i from tile0[i]), that order is spread over the XCDs as in
 // tile_coords, and each workgroup runs one tile of one layer with that layer's parameters.  The
 // tiles are the single-layer kernel's, so every output is bit-identical to a launch per layer;
-// what changes is that the layers' tiles share the rounds of workgroups over the CUs.
-template <int G, bool OUT_F32>
+// what changes is that the layers' tiles share the rounds of workgroups over the CUs.  CH: the
+// low-rank term in LDS chunks (every layer's RTp a multiple of 32 up to 256).
+template <int G, bool OUT_F32, bool CH = false>
 __global__ void __launch_bounds__(512, 1) w4a4_e3m2_siblings_kernel(GemmSiblings gs) {
   const int total = gs.tile0[gs.count];
   int lin = blockIdx.x;
@@ -1091,7 +1092,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_siblings_kernel(GemmSiblings
   const int nbm = (p.M + 255) / 256, nbn = (p.N + 127) / 128;
   int bm, bn;
   tile_of_linear(lin - gs.tile0[i], nbm, nbn, 4, bm, bn);
-  w4a4_e3m2_tile<G, OUT_F32, true>(p, bm, bn);
+  w4a4_e3m2_tile<G, OUT_F32, true, false, CH>(p, bm, bn);
 }
 
 // W4A4 GEMM, wide tiles (group 64, K a multiple of 256): block tile 256 x 256, 8 waves in a
@@ -1380,7 +1381,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_wide_kernel(GemmParams p) {
 
 // Sibling layers on the wide tiles: as w4a4_e3m2_siblings_kernel with 256 x 256 tiles (tile0 counts
 // them); every output is bit-identical to a launch per layer.
-template <bool OUT_F32>
+template <bool OUT_F32, bool CH = false>
 __global__ void __launch_bounds__(512, 1) w4a4_e3m2_wide_siblings_kernel(GemmSiblings gs) {
   const int total = gs.tile0[gs.count];
   int lin = blockIdx.x;
@@ -1392,7 +1393,7 @@ __global__ void __launch_bounds__(512, 1) w4a4_e3m2_wide_siblings_kernel(GemmSib
   const GemmParams& p = gs.layer[i];
   int bm, bn;
   tile_of_linear(lin - gs.tile0[i], p.M / 256, p.N / 256, 4, bm, bn);
-  w4a4_e3m2_wide_tile<OUT_F32>(p, bm, bn);
+  w4a4_e3m2_wide_tile<OUT_F32, CH>(p, bm, bn);
 }
 
 // Weight operand of the W4A4 GEMM, once per layer: each packed dword (8 nibbles, k0 in the
@@ -2235,6 +2236,14 @@ hipError_t launch_w4a4_siblings(const GemmSiblings& gs, int G, bool out_f32, hip
     tiles += ((p.M + 255) / 256) * ((p.N + 127) / 128);
   }
   if (gs.tile0[gs.count] != tiles || K % 512) return hipErrorInvalidValue;
+  // a layer of rank 64 .. 256: every layer's low-rank term in LDS chunks (rank 32 in one chunk)
+  bool ch = false, ch_ok = true;
+  for (int i = 0; i < gs.count; ++i) {
+    const int r = gs.layer[i].RTp;
+    ch = ch || r > 32;
+    ch_ok = ch_ok && r > 0 && r <= 256 && r % 32 == 0;
+  }
+  ch = ch && ch_ok;
   if (G == 64) {
     // the wide tiles when every layer takes them and they pay over the whole launch
     bool apply = true;
@@ -2252,15 +2261,26 @@ hipError_t launch_w4a4_siblings(const GemmSiblings& gs, int G, bool out_f32, hip
         t += (M / 256) * (gs.layer[i].N / 256);
       }
       w.tile0[gs.count] = t;
-      if (out_f32) w4a4_e3m2_wide_siblings_kernel<true><<<dim3((unsigned)t), 512, 0, st>>>(w);
-      else w4a4_e3m2_wide_siblings_kernel<false><<<dim3((unsigned)t), 512, 0, st>>>(w);
+      if (ch) {
+        if (out_f32) w4a4_e3m2_wide_siblings_kernel<true, true><<<dim3((unsigned)t), 512, 0, st>>>(w);
+        else w4a4_e3m2_wide_siblings_kernel<false, true><<<dim3((unsigned)t), 512, 0, st>>>(w);
+      } else {
+        if (out_f32) w4a4_e3m2_wide_siblings_kernel<true><<<dim3((unsigned)t), 512, 0, st>>>(w);
+        else w4a4_e3m2_wide_siblings_kernel<false><<<dim3((unsigned)t), 512, 0, st>>>(w);
+      }
       return hipGetLastError();
     }
   }
   const dim3 grid((unsigned)tiles);
-  if (G == 64) {
+  if (G == 64 && ch) {
+    if (out_f32) w4a4_e3m2_siblings_kernel<64, true, true><<<grid, 512, 0, st>>>(gs);
+    else w4a4_e3m2_siblings_kernel<64, false, true><<<grid, 512, 0, st>>>(gs);
+  } else if (G == 64) {
     if (out_f32) w4a4_e3m2_siblings_kernel<64, true><<<grid, 512, 0, st>>>(gs);
     else w4a4_e3m2_siblings_kernel<64, false><<<grid, 512, 0, st>>>(gs);
+  } else if (G == 128 && ch) {
+    if (out_f32) w4a4_e3m2_siblings_kernel<128, true, true><<<grid, 512, 0, st>>>(gs);
+    else w4a4_e3m2_siblings_kernel<128, false, true><<<grid, 512, 0, st>>>(gs);
   } else if (G == 128) {
     if (out_f32) w4a4_e3m2_siblings_kernel<128, true><<<grid, 512, 0, st>>>(gs);
     else w4a4_e3m2_siblings_kernel<128, false><<<grid, 512, 0, st>>>(gs);

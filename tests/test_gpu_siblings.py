@@ -11,11 +11,11 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _layers(dev, shapes, seed, backend, group=64):
+def _layers(dev, shapes, seed, backend, group=64, rank=32):
     from krea2_svdquant_amd.runtime.krea2_standin import random_quantized_state
     from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
     gen = torch.Generator(device=dev).manual_seed(seed)
-    return [SVDQuantLinear(random_quantized_state(n, k, rank=32, group_size=group, device=dev, generator=gen),
+    return [SVDQuantLinear(random_quantized_state(n, k, rank=rank, group_size=group, device=dev, generator=gen),
                            backend=backend) for n, k in shapes]
 
 
@@ -91,13 +91,15 @@ def test_grouped_gemms_match_single_layer_forwards(dev, k, group, out_f32):
 
 
 def test_grouped_gemms_at_the_block_shapes(dev):
-    """to_q, to_k, to_v, to_gate at M = 4352 (2040 tiles over the XCDs) and ff.up, ff.gate."""
+    """to_q, to_k, to_v, to_gate at M = 4352 (2040 tiles over the XCDs) and ff.up, ff.gate, also at
+    rank 64 (the reference's default MLP rank, config.py:21-23: the low-rank term in LDS chunks)."""
     from krea2_svdquant_amd.kernels.hip.backend import forward_prepared, forward_prepared_siblings
     gen = torch.Generator(device=dev).manual_seed(8)
     x = torch.randn(4352, 6144, device=dev, generator=gen).to(torch.bfloat16)
-    for shapes, seed in (([(6144, 6144), (1536, 6144), (1536, 6144), (6144, 6144)], 41),
-                         ([(16384, 6144), (16384, 6144)], 42)):
-        preps = _prepared(_layers(dev, shapes, seed=seed, backend="hip_gfx950"), dev)
+    for shapes, seed, rank in (([(6144, 6144), (1536, 6144), (1536, 6144), (6144, 6144)], 41, 32),
+                               ([(16384, 6144), (16384, 6144)], 42, 32),
+                               ([(16384, 6144), (16384, 6144)], 43, 64)):
+        preps = _prepared(_layers(dev, shapes, seed=seed, backend="hip_gfx950", rank=rank), dev)
         grouped = forward_prepared_siblings(x, preps)
         for i, p in enumerate(preps):
             assert torch.equal(forward_prepared(x, p), grouped[i]), f"layer {i} of {shapes}"

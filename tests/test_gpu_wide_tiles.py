@@ -28,13 +28,14 @@ def _tiles(policy):
             os.environ["SVDQ_W4A4_TILES"] = old
 
 
-def _layers(dev, shapes, seed, bias=False):
+def _layers(dev, shapes, seed, bias=False, ranks=None):
     from krea2_svdquant_amd.runtime.krea2_standin import random_quantized_state
     from krea2_svdquant_amd.runtime.linear import SVDQuantLinear
     gen = torch.Generator(device=dev).manual_seed(seed)
     mods = []
-    for n, k in shapes:
-        st = random_quantized_state(n, k, rank=32, group_size=64, device=dev, generator=gen)
+    for i, (n, k) in enumerate(shapes):
+        rank = ranks[i] if ranks else 32
+        st = random_quantized_state(n, k, rank=rank, group_size=64, device=dev, generator=gen)
         if bias:
             st.bias = (torch.randn(n, device=dev, generator=gen) * 0.1).to(torch.bfloat16)
         mods.append(SVDQuantLinear(st, backend="hip_gfx950"))
@@ -66,9 +67,12 @@ def test_wide_tiles_bit_identical_to_narrow(dev, m, n, k, lora, out_f32):
 
 
 @pytest.mark.parametrize("out_f32", [False, True])
-def test_wide_tiles_siblings_bit_identical(dev, out_f32):
+@pytest.mark.parametrize("ranks", [None, (64, 32, 64)])
+def test_wide_tiles_siblings_bit_identical(dev, out_f32, ranks):
+    """Sibling launches on both tilings against a launch per layer; ranks (64, 32, 64) take the
+    low-rank term in LDS chunks for every layer of the launch (the rank-32 one in a single chunk)."""
     from krea2_svdquant_amd.kernels.hip.backend import forward_prepared, forward_prepared_siblings
-    mods = _layers(dev, [(768, 1024), (256, 1024), (512, 1024)], seed=23)
+    mods = _layers(dev, [(768, 1024), (256, 1024), (512, 1024)], seed=23, ranks=ranks)
     preps = [m._prepare(dev, with_adapters=False) for m in mods]
     gen = torch.Generator(device=dev).manual_seed(13)
     x = torch.randn(512, 1024, device=dev, generator=gen).to(torch.bfloat16)
