@@ -222,8 +222,9 @@ BLOCK_ORDER = [("to_q", "to_gate", "to_k", "to_v"), ("to_out.0",), ("ff.up", "ff
 
 def block_layers(args, dev, m: int, mode: str, seed0: int) -> dict:
     """The 8 block linears at M=m (``mode`` "w4a4" or "w4a16"): each timed alone, and the block
-    in dependency order (siblings that read the same input grouped, ``BLOCK_ORDER``), once with
-    the siblings issued one after another and once concurrently on side streams."""
+    in dependency order (siblings that read the same input grouped, ``BLOCK_ORDER``), with the
+    siblings issued one after another, concurrently on side streams, and with their GEMMs as one
+    launch (``forward_prepared_siblings``)."""
     import torch
     from krea2_svdquant_amd.kernels.hip import backend
     from krea2_svdquant_amd.runtime.siblings import run_concurrent
@@ -247,17 +248,15 @@ def block_layers(args, dev, m: int, mode: str, seed0: int) -> dict:
             x, fns = layers[group[0]][0], [fwd(nm) for nm in group]
             run_concurrent(x, fns) if concurrent else [f(x) for f in fns]
 
-    def block_grouped():   # W4A4: the siblings' GEMMs as one launch
+    def block_grouped():   # the siblings' GEMMs as one launch (W4A16: where that pays)
         for group in BLOCK_ORDER:
-            backend.forward_prepared_siblings(layers[group[0]][0], [layers[nm][1] for nm in group])
+            backend.forward_prepared_siblings(layers[group[0]][0], [layers[nm][1] for nm in group], mode=mode)
     for c in (False, True):
         block(c)
     ms_seq = time_avg(lambda: block(False), 10)
     ms_conc = time_avg(lambda: block(True), 10)
-    ms_grp = None
-    if mode == "w4a4":
-        block_grouped()
-        ms_grp = time_avg(block_grouped, 10)
+    block_grouped()
+    ms_grp = time_avg(block_grouped, 10)
     del layers
     torch.cuda.empty_cache()
     return {"per": per, "total": sum(per.values()), "ops": ops_total, "seq": ms_seq, "conc": ms_conc,
@@ -353,11 +352,14 @@ def w4a16_line(args, dev) -> dict:
             "bf16_peak_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
             "ms_per_block_in_order": round(b["seq"], 4),
             "ms_per_block_in_order_concurrent_siblings": round(b["conc"], 4),
+            "ms_per_block_in_order_grouped_siblings": round(b["grp"], 4),
+            "TFLOPs_in_order_grouped_siblings": round(b["ops"] / (b["grp"] * 1e-3) / 1e12, 1),
             "ffup_gemm_ms": round(ms_gemm, 4), "ffup_gemm_TFLOPs": round(tf_gemm, 1),
             "ffup_gemm_bf16_peak_frac": round(tf_gemm / BF16_PEAK_TFLOPS, 4),
             "note": "W4A16 (bf16 x_hat x in-register dequantized INT4 weights, bf16 MFMA), M=2304, layer = "
                     "x_hat pass + GEMM with low-rank epilogue; ms_per_block_linears = each layer timed alone, "
-                    "summed; *_in_order as in block_config1; ffup_gemm_* = ff.up's GEMM alone (HIP events over "
+                    "summed; *_in_order as in block_config1 (grouped: the attention inputs' GEMMs as one launch of "
+                    "192 x 256 tiles, ff.gate + ff.up as theirs); ffup_gemm_* = ff.up's GEMM alone (HIP events over "
                     "50 back-to-back calls on one x_hat; the specialized-wave kernel at this shape)"}
 
 

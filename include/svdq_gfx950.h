@@ -265,6 +265,33 @@ typedef struct svdq_w4a4_sibling {
 int svdq_w4a4_gemm_siblings(const svdq_w4a4_sibling* layers, int count, int operand, int M, int K, int group,
                             int out_f32, hipStream_t stream);
 
+/* The same for W4A16 layers: up to SVDQ_MAX_SIBLINGS svdq_w4a16_gemm calls over the same rows (same
+ * M, K and group; each layer with its own x_hat from its own svdq_act_quant, since the smoothing
+ * differs per layer), e.g. attn.to_q / to_gate / to_k / to_v.  The reference calls them one after
+ * another through SVDQuantLinear.forward (reference runtime/linear.py:156-161); each output here
+ * equals svdq_w4a16_gemm's for that layer bit for bit.  With group 64 or 128 and every layer fit
+ * for the specialized-wave kernel (no fused op; x_hat 16-byte aligned rows) the layers' 192 x 256
+ * output tiles run in one launch when their rounds over the CUs cost no more than the layers'
+ * own launches (the attention inputs at M = 2304: 720 tiles in 3 rounds against 2 rounds of
+ * 256 x 256 tiles and 2 of 128 x 128 tiles); otherwise the layers run one after another on
+ * `stream`.
+ *   layers[i]: the per-layer arguments of svdq_w4a16_gemm, with out_f32 = 0 or 1 for all. */
+typedef struct svdq_w4a16_sibling {
+  const void* xhat;
+  int64_t ldxh;
+  const void* qw;
+  const void* sw;
+  const void* mid;
+  const void* l1cat;
+  int RTp;
+  const void* bias;
+  int N;
+  void* y;
+  int64_t ldy;
+} svdq_w4a16_sibling;
+int svdq_w4a16_gemm_siblings(const svdq_w4a16_sibling* layers, int count, int M, int K, int group, int out_f32,
+                             hipStream_t stream);
+
 /* The sigmoid output gate and the SwiGLU product of a DiT block as one pass each over contiguous
  * bf16 tensors: out[i] = op(y[i], aux[i]) with op SVDQ_EPI_MUL_SIGMOID (aux * sigmoid(y)) or
  * SVDQ_EPI_SILU_MUL (silu(aux) * y), rounded as the fused store ops above (and as the torch ops on

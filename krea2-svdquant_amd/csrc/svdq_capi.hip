@@ -587,4 +587,40 @@ int svdq_w4a16_gemm_epi(const void* xhat, int64_t ldxh, const void* qw, const vo
   return launched(svdq::launch_w4a16(p, group, out_f32 == 1, stream), "w4a16_gemm");
 }
 
+int svdq_w4a16_gemm_siblings(const svdq_w4a16_sibling* layers, int count, int M, int K, int group, int out_f32,
+                             hipStream_t stream) {
+  if (!layers) return fail(SVDQ_ERR_ARG, "w4a16_gemm_siblings: null layer array");
+  if (count < 1 || count > SVDQ_MAX_SIBLINGS)
+    return fail(SVDQ_ERR_ARG, "w4a16_gemm_siblings: count=%d, must be 1..%d", count, SVDQ_MAX_SIBLINGS);
+  svdq::GemmSiblings gs{};
+  gs.count = count;
+  int tiles = 0;
+  bool fits = fast_group(group);
+  for (int i = 0; i < count; ++i) {
+    const svdq_w4a16_sibling& l = layers[i];
+    if (int e = gemm_common_checks("w4a16_gemm_siblings", l.qw, l.sw, l.mid, l.l1cat, l.RTp, M, l.N, K, group, l.y,
+                                   l.ldy, out_f32))
+      return e;
+    if (!l.xhat) return fail(SVDQ_ERR_ARG, "w4a16_gemm_siblings: layer %d: null xhat", i);
+    if (l.ldxh < K || l.ldxh % 8 || !aligned16(l.xhat))
+      return fail(SVDQ_ERR_ALIGN, "w4a16_gemm_siblings: layer %d: xhat must be 16-byte aligned with ldxh >= K, "
+                  "ldxh %% 8 == 0", i);
+    svdq::GemmParams& p = gs.layer[i];
+    p = gemm_params(l.qw, l.sw, l.mid, l.l1cat, l.RTp, l.bias, M, l.N, K, l.y, l.ldy);
+    p.xhat = static_cast<const uint16_t*>(l.xhat);
+    p.ldxh = l.ldxh;
+    fits = fits && svdq::w4a16_ws_fits(p);
+    gs.tile0[i] = tiles;
+    tiles += ((M + 191) / 192) * ((l.N + 255) / 256);
+  }
+  gs.tile0[count] = tiles;
+  if (fits && svdq::w4a16_siblings_pay(gs))
+    return launched(svdq::launch_w4a16_siblings(gs, group, out_f32 == 1, stream), "w4a16_gemm_siblings");
+  // otherwise one launch per layer, in order, each with its own tile choice
+  for (int i = 0; i < count; ++i)
+    if (int e = launched(svdq::launch_w4a16(gs.layer[i], group, out_f32 == 1, stream), "w4a16_gemm_siblings"))
+      return e;
+  return SVDQ_OK;
+}
+
 }  // extern "C"

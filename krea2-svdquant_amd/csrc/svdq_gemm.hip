@@ -1861,7 +1861,7 @@ __global__ void __launch_bounds__(256, 1) w4a16_wide_kernel(GemmParams p) {
 // takes hi_k then lo_k as in the epilogue's low-rank MFMAs, and the epilogue only adds the bias and
 // stores (the 192 accumulators leave no room for its operands).
 template <int G, bool OUT_F32>
-__global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
+__device__ __forceinline__ void w4a16_ws_tile(const GemmParams& p, int bm, int bn) {
   constexpr int NT = 256, TBM = 192, TBN = 256, KB = 64, RI = TBM / 64;
   constexpr int PITCH = 2 * KB + 16;
   constexpr int ALD = TBM * 8 / NT;            // x_hat DMA instructions per producer wave and stage
@@ -1872,9 +1872,6 @@ __global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nbm = (p.M + TBM - 1) / TBM, nbn = (p.N + TBN - 1) / TBN;
-  int bm, bn;
-  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
   const int m0 = bm * TBM, n0 = bn * TBN;
   const int K = p.K, ngroups = K / G, kp = K / 2, nst = K / KB;
   // the low-rank term mid @ l1cat^T as RTp / 32 more stages: A rows [hi_2e | lo_2e | hi_2e+1 |
@@ -2054,6 +2051,33 @@ __global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
       epilogue<OUT_F32>(pe, part, wrow + 64 * qi, n0 + 128 * wn + 64 * qj, lr, h, &sA[0][0] + wave * 4096,
                         nullptr, nullptr, 0, 0, wend);
     }
+}
+
+template <int G, bool OUT_F32>
+__global__ void __launch_bounds__(512, 1) w4a16_ws_kernel(GemmParams p) {
+  const int nbm = (p.M + 191) / 192, nbn = (p.N + 255) / 256;
+  int bm, bn;
+  tile_coords(blockIdx.x, nbm, nbn, 4, bm, bn);
+  w4a16_ws_tile<G, OUT_F32>(p, bm, bn);
+}
+
+// Sibling layers (same rows M, same K and group, each with its own x_hat) in one launch on the
+// 192 x 256 tiles: numbered back to back (layer i from tile0[i]) and spread over the XCDs as in
+// w4a4_e3m2_siblings_kernel; each workgroup runs one tile of one layer, so every output is
+// bit-identical to a launch per layer.
+template <int G, bool OUT_F32>
+__global__ void __launch_bounds__(512, 1) w4a16_ws_siblings_kernel(GemmSiblings gs) {
+  const int total = gs.tile0[gs.count];
+  int lin = blockIdx.x;
+  if (total % 8 == 0) lin = (lin % 8) * (total / 8) + lin / 8;
+  int i = 0;
+#pragma unroll
+  for (int c = 1; c < MAX_SIBLINGS; ++c) i += (c < gs.count && lin >= gs.tile0[c]) ? 1 : 0;
+  i = __builtin_amdgcn_readfirstlane(i);
+  const GemmParams& p = gs.layer[i];
+  int bm, bn;
+  tile_of_linear(lin - gs.tile0[i], (p.M + 191) / 192, (p.N + 255) / 256, 4, bm, bn);
+  w4a16_ws_tile<G, OUT_F32>(p, bm, bn);
 }
 
 // W4A4 GEMM for group sizes other than 64 / 128 (any multiple of 16 dividing K): the generic path.
@@ -2319,6 +2343,53 @@ hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, 
   return hipGetLastError();
 }
 
+// The specialized-wave kernel takes a layer without a fused op whose x_hat rows are 16-byte
+// aligned and whose DMA offsets fit 32 bits, unless SVDQ_W4A16_KERNEL=wide.
+bool w4a16_ws_fits(const GemmParams& p) {
+  const char* ke = getenv("SVDQ_W4A16_KERNEL");
+  const bool xa = (reinterpret_cast<uintptr_t>(p.xhat) & 15) == 0 && p.ldxh % 8 == 0;
+  const bool off32 = ((long)p.M - 1) * p.ldxh * 2 + 128 <= 0xFFFFFFFFL && (long)p.M * 4 * p.RTp <= 0xFFFFFFFFL;
+  return !p.epi && xa && off32 && !(ke && !strcmp(ke, "wide"));
+}
+
+// Sibling layers on one launch of 192 x 256 tiles pay when their rounds over the 256 CUs cost no
+// more than the layers' own launches.  Cost of a round = its tile height in rows (time per tile at
+// a given K grows with the rows: 142 / 187 us for 192 / 256 rows at K = 6144); the 128 x 128
+// kernel's rounds (one 4-wave workgroup per CU) count 110, its measured 82 us against 142.
+bool w4a16_siblings_pay(const GemmSiblings& gs) {
+  long own = 0, t192 = 0;
+  for (int i = 0; i < gs.count; ++i) {
+    const GemmParams& p = gs.layer[i];
+    const long nb256 = (p.N + 255) / 256, tw = (long)((p.M + 255) / 256) * nb256;
+    const long t = (long)((p.M + 191) / 192) * nb256;
+    t192 += t;
+    if (tw >= 128) own += std::min((t + 255) / 256 * 192, (tw + 255) / 256 * 256);
+    else own += ((long)((p.M + 127) / 128) * ((p.N + 127) / 128) + 255) / 256 * 110;
+  }
+  return (t192 + 255) / 256 * 192 <= own;
+}
+
+hipError_t launch_w4a16_siblings(const GemmSiblings& gs, int G, bool out_f32, hipStream_t st) {
+  if (gs.count < 1 || gs.count > MAX_SIBLINGS || (G != 64 && G != 128)) return hipErrorInvalidValue;
+  const int M = gs.layer[0].M, K = gs.layer[0].K;
+  int tiles = 0;
+  for (int i = 0; i < gs.count; ++i) {
+    const GemmParams& p = gs.layer[i];
+    if (p.M != M || p.K != K || gs.tile0[i] != tiles || !w4a16_ws_fits(p)) return hipErrorInvalidValue;
+    tiles += ((M + 191) / 192) * ((p.N + 255) / 256);
+  }
+  if (gs.tile0[gs.count] != tiles) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)tiles);
+  if (G == 64) {
+    if (out_f32) w4a16_ws_siblings_kernel<64, true><<<grid, 512, 0, st>>>(gs);
+    else w4a16_ws_siblings_kernel<64, false><<<grid, 512, 0, st>>>(gs);
+  } else {
+    if (out_f32) w4a16_ws_siblings_kernel<128, true><<<grid, 512, 0, st>>>(gs);
+    else w4a16_ws_siblings_kernel<128, false><<<grid, 512, 0, st>>>(gs);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st) {
   if (G != 64 && G != 128) {
     // other group sizes (multiples of 16 dividing K): the 128 x 128 kernel with a run-time group
@@ -2353,10 +2424,7 @@ hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st
     // rows 16-byte aligned) unless SVDQ_W4A16_KERNEL=wide.  Its DMA addresses a row by a 32-bit
     // byte offset from the x_hat base (row * ldxh * 2) and from the mid planes' (row * 4 * RTp):
     // larger operands take the register-staged kernel, which addresses rows in 64 bits.
-    const char* ke = getenv("SVDQ_W4A16_KERNEL");
-    const bool xa = (reinterpret_cast<uintptr_t>(p.xhat) & 15) == 0 && p.ldxh % 8 == 0;
-    const bool off32 = ((long)p.M - 1) * p.ldxh * 2 + 128 <= 0xFFFFFFFFL && (long)p.M * 4 * p.RTp <= 0xFFFFFFFFL;
-    if (t192 && !p.epi && xa && off32 && !(ke && !strcmp(ke, "wide"))) {
+    if (t192 && w4a16_ws_fits(p)) {
       const dim3 grid((unsigned)tiles192);
       if (G == 64) {
         if (out_f32) w4a16_ws_kernel<64, true><<<grid, 512, 0, st>>>(p);

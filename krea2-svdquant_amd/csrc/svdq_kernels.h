@@ -100,6 +100,12 @@ hipError_t launch_weight_scale_pairs(const uint16_t* sw, uint32_t* out, int n, i
 // bytes per row)
 hipError_t launch_weight_operand(const uint8_t* qw, uint8_t* qwe, int N, int K, int mode, hipStream_t st);
 hipError_t launch_w4a16(const GemmParams& p, int G, bool out_f32, hipStream_t st);
+// W4A16 sibling layers (same M, K and group; tile0 counting 192 x 256 tiles) in one launch of the
+// specialized-wave kernel; hipErrorInvalidValue when a layer cannot take it (w4a16_ws_fits).
+// w4a16_siblings_pay: whether that launch beats the layers' own launches (their tile rounds).
+bool w4a16_ws_fits(const GemmParams& p);
+bool w4a16_siblings_pay(const GemmSiblings& gs);
+hipError_t launch_w4a16_siblings(const GemmSiblings& gs, int G, bool out_f32, hipStream_t st);
 // W4A4 GEMM for any group size G (multiple of 16 dividing K): int8 operands (SVDQ_OPERAND_I8 layout)
 hipError_t launch_w4a4_any_group(const GemmParams& p, int G, bool out_f32, hipStream_t st);
 // Stand-in block normalizations (svdq_block.hip): adaptive RMS norm of rows [T, H] (H % 8 == 0),

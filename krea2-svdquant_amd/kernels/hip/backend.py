@@ -242,13 +242,14 @@ def forward_prepared(x: Tensor, prep: PreparedLayer, *, mode: str = "w4a4", out_
     return y.reshape(*lead, prep.n)
 
 
-def forward_prepared_siblings(x: Tensor, preps: Sequence[PreparedLayer], *, out_f32: bool = False,
-                              exact_div: bool = False, operand: str = "e3m2") -> list[Tensor]:
-    """W4A4 forwards of sibling layers (same input ``x``, same K and group size) on prepared
-    operands: an activation pass per layer (each layer has its own smoothing; one launch for all
-    when none has LoRA adapters, ``svdq::act_quant_siblings``), then the layers' GEMMs as one
-    launch (``svdq::w4a4_gemm_siblings``).  Every output is bit-identical to
-    ``forward_prepared(x, prep)`` of its layer."""
+def forward_prepared_siblings(x: Tensor, preps: Sequence[PreparedLayer], *, mode: str = "w4a4",
+                              out_f32: bool = False, exact_div: bool = False, operand: str = "e3m2") -> list[Tensor]:
+    """Forwards of sibling layers (same input ``x``, same K and group size) on prepared operands.
+    W4A4: an activation pass per layer (each layer has its own smoothing; one launch for all when
+    none has LoRA adapters, ``svdq::act_quant_siblings``), then the layers' GEMMs as one launch
+    (``svdq::w4a4_gemm_siblings``).  W4A16: each layer's x_hat pass, then the layers' GEMMs as one
+    launch where that pays (``svdq::w4a16_gemm_siblings``).  Every output is bit-identical to
+    ``forward_prepared(x, prep, mode=mode)`` of its layer."""
     if not x.is_cuda:
         raise RuntimeError("HIP gfx950 backend needs a GPU tensor")
     if x.dtype != torch.bfloat16:
@@ -263,6 +264,8 @@ def forward_prepared_siblings(x: Tensor, preps: Sequence[PreparedLayer], *, out_
             raise ValueError("sibling layers need the same padded in_features and group size")
     if p0.group_size not in FAST_GROUPS:
         raise ValueError(f"sibling launch needs group size 64 or 128, got {p0.group_size}")
+    if mode not in ("w4a4", "w4a16"):
+        raise ValueError(f"mode must be 'w4a4' or 'w4a16', got {mode!r}")
     if operand not in ops.OPERAND_NAMES:
         raise ValueError(f"operand must be 'e4m3', 'e3m2' or 'i8', got {operand!r}")
     opc = ops.OPERAND_NAMES[operand]
@@ -271,6 +274,13 @@ def forward_prepared_siblings(x: Tensor, preps: Sequence[PreparedLayer], *, out_
         raise ValueError(f"activation K={x2.shape[1]} exceeds packed weight K={p0.kp}")
     if x2.shape[1] != p0.kp:
         x2 = _pad_cols(x2, p0.kp)
+    if mode == "w4a16":
+        acts = [ops.act_quant(x2, p.srs, p.l2, p.lora_down, p.lora_mult, p.group_size, p.rtp, ops.OPERAND_NONE,
+                              False, True, exact_div) for p in preps]
+        ys = ops.w4a16_gemm_siblings([a[3] for a in acts], [p.qweight for p in preps],
+                                     [p.weight_scales for p in preps], [a[4] for a in acts],
+                                     [p.l1cat for p in preps], [p.bias for p in preps], p0.group_size, out_f32)
+        return [y.reshape(*lead, p.n) for y, p in zip(ys, preps)]
     if opc == ops.OPERAND_E3M2 and all(p.lora_down is None and p.rtp == p0.rtp for p in preps):
         # one activation-pass launch for the layers (each its own smoothing) and one finalize
         flat = ops.act_quant_siblings(x2, [p.srs for p in preps], [p.l2 for p in preps], p0.group_size, p0.rtp,

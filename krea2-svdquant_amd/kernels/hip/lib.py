@@ -33,7 +33,7 @@ SVDQ_EPI_MUL_SIGMOID = 1
 SVDQ_EPI_SILU_MUL = 2
 SVDQ_EPI_RESIDUAL_GATE = 3
 
-# sibling layers of one svdq_w4a4_gemm_siblings call (SVDQ_MAX_SIBLINGS)
+# sibling layers of one svdq_w4a4_gemm_siblings / svdq_w4a16_gemm_siblings call (SVDQ_MAX_SIBLINGS)
 SVDQ_MAX_SIBLINGS = 4
 
 STATUS = {0: "SVDQ_OK", -1: "SVDQ_ERR_ARG", -2: "SVDQ_ERR_SHAPE", -3: "SVDQ_ERR_ALIGN",
@@ -53,6 +53,12 @@ class ActSibling(ctypes.Structure):
 class W4A4Sibling(ctypes.Structure):
     """``svdq_w4a4_sibling``: one layer of ``svdq_w4a4_gemm_siblings``."""
     _fields_ = [("qa", _P), ("sxp", _P), ("qwe", _P), ("swp", _P), ("mid", _P), ("l1cat", _P), ("RTp", _I),
+                ("bias", _P), ("N", _I), ("y", _P), ("ldy", _L)]
+
+
+class W4A16Sibling(ctypes.Structure):
+    """``svdq_w4a16_sibling``: one layer of ``svdq_w4a16_gemm_siblings``."""
+    _fields_ = [("xhat", _P), ("ldxh", _L), ("qw", _P), ("sw", _P), ("mid", _P), ("l1cat", _P), ("RTp", _I),
                 ("bias", _P), ("N", _I), ("y", _P), ("ldy", _L)]
 
 
@@ -78,6 +84,7 @@ SIGNATURES = {
                                  _I, _P, _L, _P, _P]),
     "svdq_act_quant_siblings": (_I, [_P, _L, ctypes.POINTER(ActSibling), _I, _I, _I, _I, _I, _U, _I, _P]),
     "svdq_w4a4_gemm_siblings": (_I, [ctypes.POINTER(W4A4Sibling), _I, _I, _I, _I, _I, _I, _P]),
+    "svdq_w4a16_gemm_siblings": (_I, [ctypes.POINTER(W4A16Sibling), _I, _I, _I, _I, _I, _P]),
     "svdq_gate_op": (_I, [_I, _P, _P, _P, _L, _P]),
     "svdq_rms_norm_modulate": (_I, [_P, _L, _P, _P, _I, _I, ctypes.c_float, _P, _L, _P]),
     "svdq_residual_rms_norm_modulate": (_I, [_P, _L, _P, _L, _P, _P, _P, _I, _I, ctypes.c_float, _P, _L, _P, _L,

@@ -422,6 +422,42 @@ def _(xhat, qweight, weight_scales, mid, l1cat, bias, group_size, out_f32, epi=0
     return xhat.new_empty((xhat.shape[0], qweight.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)
 
 
+@torch.library.custom_op("svdq::w4a16_gemm_siblings", mutates_args=())
+def w4a16_gemm_siblings(xhat: list[Tensor], qweight: list[Tensor], weight_scales: list[Tensor], mid: list[Tensor],
+                        l1cat: list[Tensor], bias: list[Optional[Tensor]], group_size: int,
+                        out_f32: bool) -> list[Tensor]:
+    """``w4a16_gemm`` of up to ``lib.SVDQ_MAX_SIBLINGS`` layers over the same rows (the i-th entry
+    of every list belongs to layer i; each layer its own x_hat), in one launch when that pays
+    (``svdq_w4a16_gemm_siblings``); each output is bit-identical to that layer's ``w4a16_gemm``."""
+    count = len(xhat)
+    _need(1 <= count <= lib.SVDQ_MAX_SIBLINGS, ValueError, f"1..{lib.SVDQ_MAX_SIBLINGS} layers, got {count}")
+    _need(all(len(a) == count for a in (qweight, weight_scales, mid, l1cat, bias)), ValueError,
+          "one entry per layer in every list")
+    _need(xhat[0].is_cuda, RuntimeError, "svdq::w4a16_gemm_siblings needs GPU tensors")
+    dev = xhat[0].device
+    m, k = xhat[0].shape
+    ns = []
+    for i in range(count):
+        _check_dev(f"layer {i}: xhat", xhat[i], dev, torch.bfloat16)
+        _need(tuple(xhat[i].shape) == (m, k), ValueError,
+              f"sibling layers need the same M and K, got {tuple(xhat[i].shape)} and {(m, k)}")
+        ns.append(_check_gemm(qweight[i], weight_scales[i], mid[i], l1cat[i], bias[i], m, k, group_size, dev))
+    ys = [torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev) for n in ns]
+    arr = (lib.W4A16Sibling * count)()
+    for i, (y, n) in enumerate(zip(ys, ns)):
+        arr[i] = lib.W4A16Sibling(xhat[i].data_ptr(), k, qweight[i].data_ptr(), weight_scales[i].data_ptr(),
+                                  mid[i].data_ptr(), l1cat[i].data_ptr(), mid[i].shape[2], _vp(bias[i]), n,
+                                  y.data_ptr(), n)
+    lib.call("svdq_w4a16_gemm_siblings", arr, count, m, k, group_size, int(out_f32), _stream(dev))
+    return ys
+
+
+@w4a16_gemm_siblings.register_fake
+def _(xhat, qweight, weight_scales, mid, l1cat, bias, group_size, out_f32):
+    return [x.new_empty((x.shape[0], w.shape[0]), dtype=torch.float32 if out_f32 else torch.bfloat16)
+            for x, w in zip(xhat, qweight)]
+
+
 # ---- stand-in block normalizations -------------------------------------------------------------
 @torch.library.custom_op("svdq::gate_op", mutates_args=())
 def gate_op(y: Tensor, aux: Tensor, op: int) -> Tensor:

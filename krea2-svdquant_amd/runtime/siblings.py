@@ -26,6 +26,10 @@ smoothing vector, so the codes differ), then the layers' GEMMs in ONE launch
 M = 4352 the four attention inputs then run 2040 tiles in 8 rounds over the 256 CUs instead of
 3.19 + 0.8 + 0.8 + 3.19 rounds rounded up to 10, and ff.gate + ff.up 4352 tiles in 17 rounds
 instead of 18.  The tiles are the single-layer kernel's, so the outputs are again bit-identical.
+W4A16 layers take the same route (``svdq_w4a16_gemm_siblings``): each layer's x_hat pass, then
+one launch of the specialized-wave kernel's 192 x 256 tiles where its rounds cost no more than
+the layers' own launches: the attention inputs at M = 2304 run 720 tiles in 3 rounds (383 us)
+instead of 538 us in four launches.
 """
 from __future__ import annotations
 
@@ -77,18 +81,19 @@ def _groupable(x: Tensor, layers: Sequence[nn.Module]) -> bool:
     if not all(isinstance(m, SVDQuantLinear) for m in layers):
         return False
     l0 = layers[0]
-    return all(m._mode(x.device) == "w4a4" and m.group_size in FAST_GROUPS and m.group_size == l0.group_size
+    mode = l0._mode(x.device)
+    return all(m._mode(x.device) == mode and m.group_size in FAST_GROUPS and m.group_size == l0.group_size
                and m.original_shape[1] == l0.original_shape[1] and m.padded_in_features == l0.padded_in_features
                for m in layers)
 
 
 def run_grouped(x: Tensor, layers: Sequence[nn.Module]) -> list[Tensor]:
-    """``[layer(x) for layer in layers]``; when every layer is a W4A4 ``SVDQuantLinear`` with group
-    size 64 or 128 and the same in_features (2 to 4 layers, on the GPU), their GEMMs run as one
-    launch (``forward_prepared_siblings``), each with its layer's LoRA adapters.  Other layer sets
-    run one after another."""
+    """``[layer(x) for layer in layers]``; when every layer is an ``SVDQuantLinear`` of one mode
+    (W4A4 or W4A16) with group size 64 or 128 and the same in_features (2 to 4 layers, on the
+    GPU), their GEMMs run as one launch (``forward_prepared_siblings``; W4A16 where the grouped
+    tiles pay), each with its layer's LoRA adapters.  Other layer sets run one after another."""
     if not _groupable(x, layers):
         return [m(x) for m in layers]
     from ..kernels.hip.backend import forward_prepared_siblings
     preps = [m._prepare(x.device, with_adapters=bool(m.lora_adapters)) for m in layers]
-    return forward_prepared_siblings(x, preps)
+    return forward_prepared_siblings(x, preps, mode=layers[0]._mode(x.device))

@@ -187,6 +187,23 @@ def test_gate_op_and_siblings_reject_bad_arguments_before_any_launch():
     with pytest.raises(lib.SVDQError) as ei:
         lib.call("svdq_w4a4_gemm_siblings", layers, 2, 2, 256, 1024, 64, 0, None)   # null pointers
     assert ei.value.status == -1 and "null pointer" in str(ei.value)
+    w16 = (lib.W4A16Sibling * 5)()
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a16_gemm_siblings", w16, 5, 256, 1024, 64, 0, None)
+    assert ei.value.status == -1 and "count=5" in str(ei.value)
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a16_gemm_siblings", w16, 2, 256, 1024, 64, 0, None)   # N = 0
+    assert ei.value.status == -1 and "N=0" in str(ei.value)
+    for lay in w16[:2]:
+        lay.N, lay.RTp, lay.ldy, lay.ldxh = 128, 32, 128, 1024
+        lay.qw = lay.sw = lay.mid = lay.l1cat = lay.y = 0x1000
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a16_gemm_siblings", w16, 2, 256, 1024, 64, 0, None)   # x_hat missing
+    assert ei.value.status == -1 and "null xhat" in str(ei.value)
+    w16[0].xhat = w16[1].xhat = 0x1008
+    with pytest.raises(lib.SVDQError) as ei:
+        lib.call("svdq_w4a16_gemm_siblings", w16, 2, 256, 1024, 64, 0, None)   # x_hat not 16-byte aligned
+    assert ei.value.status == -3 and "xhat" in str(ei.value)
 
 
 def test_attention_qnorm_rejects_bad_tables_before_any_launch():

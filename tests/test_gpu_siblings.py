@@ -107,6 +107,33 @@ def test_grouped_gemms_at_the_block_shapes(dev):
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("out_f32", [False, True])
+@pytest.mark.parametrize("group", [64, 128])
+def test_grouped_w4a16_gemms_match_single_layer_forwards(dev, group, out_f32):
+    """W4A16 siblings (``svdq_w4a16_gemm_siblings``): the attention inputs at M = 2304 (one launch of
+    720 tiles of 192 x 256), and ragged rows and columns with a LoRA-widened layer (RTp 96 beside
+    32; one launch of 18 tiles, the grouped rounds cheaper than three launches); every output
+    bit-identical to the layer's own W4A16 forward."""
+    from krea2_svdquant_amd.kernels.hip.backend import forward_prepared, forward_prepared_siblings
+    gen = torch.Generator(device=dev).manual_seed(21 + group)
+    for m, shapes, lora in ((2304, [(6144, 6144), (6144, 6144), (1536, 6144), (1536, 6144)], False),
+                            (517, [(640, 1024), (160, 1024), (384, 1024)], True)):
+        print(f"w4a16 siblings: M={m} shapes={shapes} group={group} lora={lora} f32={out_f32}", flush=True)
+        mods = _layers(dev, shapes, seed=m + group, backend="hip_gfx950_w4a16", group=group)
+        if lora:
+            k = shapes[1][1]
+            mods[1].add_lora_adapter((torch.randn(48, k, device=dev, generator=gen) * 0.05).to(torch.bfloat16),
+                                     (torch.randn(160, 48, device=dev, generator=gen) * 0.05).to(torch.bfloat16),
+                                     scale=0.8)
+        preps = _prepared(mods, dev)
+        x = torch.randn(m, shapes[0][1], device=dev, generator=gen).to(torch.bfloat16)
+        grouped = forward_prepared_siblings(x, preps, mode="w4a16", out_f32=out_f32)
+        for i, p in enumerate(preps):
+            assert torch.equal(forward_prepared(x, p, mode="w4a16", out_f32=out_f32), grouped[i]), f"M={m} layer {i}"
+        del mods, preps, grouped
+        torch.cuda.empty_cache()
+
+
 def test_run_grouped_modules_and_standin(dev):
     from krea2_svdquant_amd.runtime.krea2_standin import Krea2Dims, Krea2StandInTransformer
     from krea2_svdquant_amd.runtime.siblings import run_grouped
@@ -115,7 +142,7 @@ def test_run_grouped_modules_and_standin(dev):
     x = torch.randn(2, 150, 512, device=dev, generator=gen).to(torch.bfloat16)   # leading dims kept
     for a, b in zip([m(x) for m in mods], run_grouped(x, mods)):
         assert a.shape == b.shape and torch.equal(a, b)
-    w16 = _layers(dev, [(256, 512), (256, 512)], seed=52, backend="hip_gfx950_w4a16")   # not groupable
+    w16 = _layers(dev, [(256, 512), (256, 512)], seed=52, backend="hip_gfx950_w4a16")   # W4A16 siblings
     for a, b in zip([m(x) for m in w16], run_grouped(x, w16)):
         assert torch.equal(a, b)
     dims = Krea2Dims(layers=2, hidden=512, heads=4, kv_heads=1, head_dim=128, mlp=1024)   # K % 512 == 0
