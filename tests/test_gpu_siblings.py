@@ -111,13 +111,15 @@ def test_grouped_gemms_at_the_block_shapes(dev):
 @pytest.mark.parametrize("group", [64, 128])
 def test_grouped_w4a16_gemms_match_single_layer_forwards(dev, group, out_f32):
     """W4A16 siblings (``svdq_w4a16_gemm_siblings``): the attention inputs at M = 2304 (one launch of
-    720 tiles of 192 x 256), and ragged rows and columns with a LoRA-widened layer (RTp 96 beside
-    32; one launch of 18 tiles, the grouped rounds cheaper than three launches); every output
-    bit-identical to the layer's own W4A16 forward."""
+    720 tiles of 192 x 256), ragged rows and columns with a LoRA-widened layer (RTp 96 beside 32;
+    one launch of 18 tiles, the grouped rounds cheaper than three launches), and two N = 6144
+    layers at M = 2304 (one round of 256 x 256 tiles each beats three rounds of 192-row tiles: a
+    launch per layer); every output bit-identical to the layer's own W4A16 forward."""
     from krea2_svdquant_amd.kernels.hip.backend import forward_prepared, forward_prepared_siblings
     gen = torch.Generator(device=dev).manual_seed(21 + group)
     for m, shapes, lora in ((2304, [(6144, 6144), (6144, 6144), (1536, 6144), (1536, 6144)], False),
-                            (517, [(640, 1024), (160, 1024), (384, 1024)], True)):
+                            (517, [(640, 1024), (160, 1024), (384, 1024)], True),
+                            (2304, [(6144, 1024), (6144, 1024)], False)):
         print(f"w4a16 siblings: M={m} shapes={shapes} group={group} lora={lora} f32={out_f32}", flush=True)
         mods = _layers(dev, shapes, seed=m + group, backend="hip_gfx950_w4a16", group=group)
         if lora:
